@@ -1,0 +1,172 @@
+#!/usr/bin/env python3
+"""Batch-1 greedy decode of the MiniCPM5-2.4B-shaped Q4_K_M model on one MI355X.
+
+Workload (the BASELINE full-model configuration): 40 layers, hidden 2304,
+32 q / 8 kv heads of 64, FFN 5760 SwiGLU, vocab 130560 with a tied Q6_K LM
+head, Q6_K attn_v / ffn_down, Q4_K elsewhere, F32 norms; random-init weights
+N(0, 0.02) from a fixed seed; a 32-token random-ID prompt, then greedy decode.
+A step is one decoded token (one captured hipGraph replay of the whole
+forward plus argmax on the device).  --warmup steps run untimed, then exactly
+--steps steps are timed between device synchronisations.
+
+Printed: one JSON line with tokens/s, the achieved HBM bandwidth of the
+dominant kernel against the 8 TB/s peak (HIP events around its launches, on
+the engine stream), and the reference's CPU path timed on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "minicpm5.cpp_amd", "python"))
+
+import mcpm  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+SEED = 20260105  # BASELINE seed 20260101 + configuration index 4
+PROMPT = 32
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def kernel_breakdown(eng, n_tokens=8):
+    """Per-class average launch duration (HIP events on the engine stream)."""
+    out = {}
+    for kc, name in enumerate(mcpm.KC_NAMES):
+        eng.set_kernel_timing(kc)
+        eng.decode_steps(n_tokens)
+        eng.sync()
+        ms, n = eng.kernel_time()
+        eng.set_kernel_timing(-1)
+        per_launch_us = 1000.0 * ms / max(n, 1)
+        launches_per_token = n / n_tokens
+        out[name] = {"avg_us": per_launch_us, "launches_per_token": launches_per_token,
+                     "us_per_token": per_launch_us * launches_per_token,
+                     "bytes_per_launch": eng.kernel_bytes(kc)}
+    return out
+
+
+def cpu_baseline(image, cfg_vocab, budget_s=15.0):
+    """The reference's own CPU ops (oracle/_ref, AVX2 + OpenMP) when built,
+    else the oracle's C restatement, timed on a bounded decode sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    cores = min(16, os.cpu_count() or 1)
+    kind = "reference" if O.reference() is not None else "port"
+    if kind == "reference":
+        O.reference().ref_set_threads(cores)
+    else:
+        os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    model = O.OracleModel(image, use_reference_ops=(kind == "reference"))
+    model.init_kv(64)
+    rng = np.random.default_rng(SEED)
+    lg = np.empty(cfg_vocab, np.float32)
+    tok = int(rng.integers(0, cfg_vocab))
+    model.forward(tok, 0, lg)  # warm-up
+    n = 0
+    t0 = time.perf_counter()
+    while n < 48 and time.perf_counter() - t0 < budget_s:
+        tok = model.forward(tok, n + 1, lg)
+        n += 1
+    dt = time.perf_counter() - t0
+    model.close()
+    return {"value": n / dt, "unit": "tokens/s", "cores": cores, "kind": kind,
+            "sample": f"{n} greedy decode tokens of the same 2.4B-shaped model at positions 1..{n} "
+                      f"({dt:.1f} s, {'oracle/_ref: reference src/ops compiled -O3 -mavx2 -mfma -ffast-math -fopenmp' if kind == 'reference' else 'oracle C port'})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mix", type=int, default=0, help="0: Q6_K v/down in every layer; 1: llama.cpp layers")
+    ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of a graph replay")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(batch-1 decode does not shard, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    cfg = mcpm.config_2p4b()
+    log("synthesizing the 2.4B-shaped model")
+    t = time.perf_counter()
+    image = mcpm.synth_gguf(cfg, seed=SEED, mix=args.mix)
+    log(f"  {image.nbytes / 1e9:.3f} GB GGUF in {time.perf_counter() - t:.1f} s")
+    ctx = mcpm.Context(0)
+    n_cu, arch = ctx.info()
+    eng = mcpm.Engine(ctx, image=image)
+    if args.eager:
+        eng.set_graph(False)
+    log(f"loaded into HBM on {arch} ({n_cu} CUs){' eager launches' if args.eager else ''}")
+    total_steps = args.warmup + args.steps + 8 * len(mcpm.KC_NAMES)
+    eng.init_kv_cache(PROMPT + total_steps + 8)
+    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, PROMPT).astype(np.int32)
+
+    # prefill + warmup (untimed), then exactly --steps timed steps
+    eng.generate_greedy(prompt, 1 + args.warmup)
+    eng.sync()
+    t0 = time.perf_counter()
+    eng.decode_steps(args.steps)
+    eng.sync()
+    t1 = time.perf_counter()
+    dt = t1 - t0
+    tps = args.steps / dt
+    wbytes = eng.weight_bytes_per_token()
+    log(f"decode: {args.steps} tokens in {dt * 1e3:.1f} ms -> {tps:.1f} tok/s, "
+        f"{wbytes * tps / 1e9:.1f} GB/s effective")
+
+    # per-kernel durations with HIP events (eager launches of the same kernels)
+    bd = kernel_breakdown(eng)
+    dom = max(bd, key=lambda k: bd[k]["us_per_token"])
+    d = bd[dom]
+    achieved = d["bytes_per_launch"] / (d["avg_us"] * 1e-6) / 1e9
+    for k, v in bd.items():
+        log(f"  {k:8s} {v['avg_us']:8.2f} us x {v['launches_per_token']:.0f}/token "
+            f"= {v['us_per_token']:8.1f} us/token  {v['bytes_per_launch'] / (v['avg_us'] * 1e-6) / 1e9 if v['bytes_per_launch'] else 0:7.1f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline(image, cfg.vocab)
+        log(f"  cpu: {cpu['value']:.2f} tok/s ({cpu['kind']}, {cpu['cores']} cores)")
+
+    res = {
+        "metric": "decode tokens/s, batch 1, 2.4B Q4_K_M shape; GEMV achieved HBM GB/s vs peak",
+        "value": round(tps, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * dt / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 dot (Q4_K/Q6_K x Q8_K), fp32 scale/accumulate",
+        "data": "synthetic: random-init weights N(0,0.02) seed 20260105, random-ID prompt",
+        "config": {"workload": "greedy decode, batch 1, 2.4B-shaped Q4_K_M decoder", "layers": cfg.n_layers,
+                   "hidden": cfg.dim, "heads": f"{cfg.n_heads}q/{cfg.n_kv_heads}kv x {cfg.head_dim}",
+                   "ffn": cfg.ffn, "vocab": cfg.vocab, "quant_mix": "literal" if args.mix == 0 else "llama",
+                   "launch": "eager" if args.eager else "hipGraph per token", "prompt_tokens": PROMPT, "context_at_end": PROMPT + args.warmup + args.steps,
+                   "weight_bytes_per_token": wbytes, "effective_GBps": round(wbytes * tps / 1e9, 1),
+                   "token_roofline_frac": round(wbytes * tps / 1e9 / HBM_PEAK_GBPS, 4),
+                   "kernels_us_per_token": {k: round(v["us_per_token"], 2) for k, v in bd.items()}},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    eng.free()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

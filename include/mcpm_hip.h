@@ -1,0 +1,240 @@
+/*
+ * mcpm_hip.h -- C ABI of the MI355X (gfx950) decode engine for MiniCPM5-style
+ * GGUF models.  Plain pointers and sizes; no C++ or torch types cross it.
+ *
+ * Three layers, mirroring the reference (astrowar/MiniCPM5.cpp):
+ *   1. Context, device memory and weights (the reference keeps weights in one
+ *      host buffer, src/model.cpp:44-69; here they are uploaded once to HBM).
+ *   2. Per-op entry points, one per kernel of the backend seam
+ *      (src/ops/ops_internal.h:13-72) and of the ops API (include/ops.h:112-160).
+ *      Activations are device pointers; calls are ordered on the context's
+ *      stream and return after enqueueing.  mcpm_sync() waits for them.
+ *   3. The engine: load_model / init_kv_cache / forward of MiniCPM5Engine
+ *      (include/model.h:37-45) plus the decode loop of ChatSession
+ *      (src/chat_session.cpp:154-186).
+ *
+ * Every function returns MCPM_OK (0) or a negative MCPM_ERR_* code; nothing
+ * throws across this boundary.  mcpm_last_error() returns the message of the
+ * calling thread's last failure.  A context is used by one host thread at a
+ * time (the reference engine is single-threaded, include/model.h:37-45).
+ *
+ * Block formats are ggml's (include/ops.h:33-65): Q8_0 34 B per 32 weights,
+ * Q4_K 144 B per 256, Q6_K 210 B per 256, activation Q8_K 292 B per 256.
+ */
+#ifndef MCPM_HIP_H
+#define MCPM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MCPM_OK 0
+#define MCPM_ERR_HIP (-1)         /* a HIP runtime call failed */
+#define MCPM_ERR_ARG (-2)         /* invalid argument (shape, null pointer) */
+#define MCPM_ERR_UNSUPPORTED (-3) /* tensor type without a kernel */
+#define MCPM_ERR_CONTEXT (-4)     /* pos >= max_seq_len, or KV cache missing */
+#define MCPM_ERR_IO (-5)          /* file could not be read */
+#define MCPM_ERR_FORMAT (-6)      /* malformed GGUF or missing tensor */
+#define MCPM_ERR_NOMEM (-7)       /* device or host allocation failed */
+
+/* ggml tensor type ids, as stored in GGUF. */
+#define MCPM_TYPE_F32 0
+#define MCPM_TYPE_Q8_0 8
+#define MCPM_TYPE_Q4_K 12
+#define MCPM_TYPE_Q6_K 14
+
+#define MCPM_QK_K 256
+#define MCPM_Q8K_BYTES 292
+
+typedef struct mcpm_ctx mcpm_ctx;
+typedef struct mcpm_tensor mcpm_tensor;
+typedef struct mcpm_engine mcpm_engine;
+
+/* ------------------------------------------------------------ context ---- */
+
+/* Opens `device` and creates one HIP stream for all calls on the context. */
+int mcpm_init(int device, mcpm_ctx **out);
+void mcpm_destroy(mcpm_ctx *ctx);
+const char *mcpm_last_error(void);
+int mcpm_sync(mcpm_ctx *ctx);
+/* Number of compute units and the device name (for reports). */
+int mcpm_device_info(mcpm_ctx *ctx, int *n_cu, char *name, size_t name_len);
+
+int mcpm_device_alloc(mcpm_ctx *ctx, size_t bytes, void **dptr);
+int mcpm_device_free(mcpm_ctx *ctx, void *dptr);
+/* Synchronous copies on the context stream. */
+int mcpm_copy_to_device(mcpm_ctx *ctx, void *dst, const void *src, size_t bytes);
+int mcpm_copy_to_host(mcpm_ctx *ctx, void *dst, const void *src, size_t bytes);
+int mcpm_fill_device(mcpm_ctx *ctx, void *dst, int byte_value, size_t bytes);
+
+/* ------------------------------------------------------------ weights ---- */
+
+/* Uploads a weight matrix given in its native GGUF block layout (host memory),
+ * cols = dims[0] (K), rows = dims[1] (include/ops.h:104-110).  The device copy
+ * is re-laid out for coalesced loads (same bytes per block).  Replaces the
+ * Tensor{type_str, dims, data_ptr} the reference's ops take. */
+int mcpm_tensor_upload(mcpm_ctx *ctx, const void *host_blocks, size_t bytes, int ggml_type, int64_t cols,
+                       int64_t rows, mcpm_tensor **out);
+/* Writes the native block layout back to host memory (bytes == native size). */
+int mcpm_tensor_download(mcpm_ctx *ctx, const mcpm_tensor *t, void *host_blocks, size_t bytes);
+int mcpm_tensor_info(const mcpm_tensor *t, int *ggml_type, int64_t *cols, int64_t *rows);
+void mcpm_tensor_free(mcpm_tensor *t);
+/* Dequantizes rows [row0, row0+n_rows) to fp32 (device out, n_rows*cols). */
+int mcpm_tensor_dequantize_rows(mcpm_ctx *ctx, const mcpm_tensor *t, int64_t row0, int64_t n_rows, float *out);
+
+/* ------------------------------------------------------------ per-op ----- */
+
+/* quantize_row_q8_K (src/ops/ops.cpp:300-308; AVX2 ties-to-even,
+ * src/ops/ops_avx2.cpp:85-144).  n multiple of 256; y: n/256 Q8_K blocks. */
+int mcpm_quantize_row_q8_K(mcpm_ctx *ctx, const float *x, int n, void *y);
+
+/* gemv_q4_K_q8_K_avx2 / gemv_q6_K_q8_K_avx2 (src/ops/ops_internal.h:39-40). */
+int mcpm_gemv_q4_K_q8_K(mcpm_ctx *ctx, const mcpm_tensor *w, const void *xq, float *out, int rows, int cols);
+int mcpm_gemv_q6_K_q8_K(mcpm_ctx *ctx, const mcpm_tensor *w, const void *xq, float *out, int rows, int cols);
+
+/* gemv_qkv_q4_K_q8_K_avx2 / gemv_qkv_q4_q4_q6_q8_K_avx2
+ * (src/ops/ops_internal.h:43-50): q, k Q4_K; v Q4_K or Q6_K (wv's type). */
+int mcpm_gemv_qkv_q8_K(mcpm_ctx *ctx, const mcpm_tensor *wq, const mcpm_tensor *wk, const mcpm_tensor *wv,
+                       const void *xq, float *q, float *k, float *v, int q_rows, int kv_rows, int cols);
+
+/* gemv_gate_up_q4_K_q8_K_avx2 (src/ops/ops_internal.h:51-54). */
+int mcpm_gemv_gate_up_q4_K_q8_K(mcpm_ctx *ctx, const mcpm_tensor *wg, const mcpm_tensor *wu, const void *xq,
+                                float *gate, float *up, int rows, int cols);
+
+/* gemv_q4_K_avx2 / gemv_q6_K_avx2 (src/ops/ops_internal.h:35-36): fp32 input
+ * quantized to Q8_K (ties-to-even), then the Q8_K GEMV. */
+int mcpm_gemv_q4_K(mcpm_ctx *ctx, const mcpm_tensor *w, const float *x, float *out, int rows, int cols);
+int mcpm_gemv_q6_K(mcpm_ctx *ctx, const mcpm_tensor *w, const float *x, float *out, int rows, int cols);
+
+/* gemv_q8_0 / gemv_f32 (src/ops/ops.cpp:32-43, 58-79): fp32 activations. */
+int mcpm_gemv_q8_0(mcpm_ctx *ctx, const mcpm_tensor *w, const float *x, float *out, int rows, int cols);
+int mcpm_gemv_f32(mcpm_ctx *ctx, const mcpm_tensor *w, const float *x, float *out, int rows, int cols);
+
+/* matmul (src/ops/ops.cpp:264-290): dispatch on w's type.  Unsupported types
+ * fill out with 0.001f and return MCPM_ERR_UNSUPPORTED. */
+int mcpm_matmul(mcpm_ctx *ctx, const mcpm_tensor *w, const float *x, float *out);
+/* matmul_q8k (src/ops/ops.cpp:317-349): Q4_K or Q6_K; other types fill 0.0f
+ * and return MCPM_ERR_UNSUPPORTED. */
+int mcpm_matmul_q8k(mcpm_ctx *ctx, const mcpm_tensor *w, const void *xq, int num_cols, float *out);
+
+/* rmsnorm (src/ops/ops.cpp:468-481). */
+int mcpm_rmsnorm(mcpm_ctx *ctx, float *out, const float *x, const float *w, int dim, float eps);
+/* rmsnorm_and_quantize_q8k (src/ops/ops.cpp:676-723), dim multiple of 256. */
+int mcpm_rmsnorm_and_quantize_q8k(mcpm_ctx *ctx, void *out_q8k, const float *x, const float *w, int dim,
+                                  float eps);
+/* swiglu_and_quantize_q8k (src/ops/ops.cpp:725-765): dim/256 blocks. */
+int mcpm_swiglu_and_quantize_q8k(mcpm_ctx *ctx, void *out_q8k, const float *gate, const float *up, int dim);
+/* apply_rope for heads 0..n_heads-1 (src/ops/ops.cpp:502-516, loop
+ * src/model.cpp:187-192), in place. */
+int mcpm_apply_rope(mcpm_ctx *ctx, float *vec, int pos, int n_heads, int head_dim, float rope_base);
+/* execute_attention (src/ops/ops.cpp:537-628) over caller-owned caches laid
+ * out [max_seq_len][n_kv_heads][head_dim].  Returns MCPM_ERR_CONTEXT and
+ * leaves attn_out untouched when pos >= max_seq_len. */
+int mcpm_execute_attention(mcpm_ctx *ctx, float *attn_out, const float *q, const float *k_cur,
+                           const float *v_cur, float *k_cache, float *v_cache, int pos, int max_seq_len,
+                           int n_heads, int n_kv_heads, int head_dim);
+/* get_embedding (src/ops/ops.cpp:631-673) for Q4_K and Q6_K tables. */
+int mcpm_get_embedding(mcpm_ctx *ctx, float *out, const mcpm_tensor *embd, int token);
+/* First index of the maximum of x[0..n) into *out (device int). */
+int mcpm_argmax(mcpm_ctx *ctx, const float *x, int n, int *out);
+
+/* ------------------------------------------------------------ engine ----- */
+
+typedef struct {
+    int n_layers, dim, n_heads, n_kv_heads, head_dim;
+    int ffn;     /* feed_forward_length */
+    int ffn_pad; /* ffn rounded up to whole 256-blocks (the down-projection's K) */
+    int vocab;
+    float rope_base, eps;
+    int tied_embeddings; /* 1 when token_embd also serves as the LM head */
+} mcpm_model_config;
+
+/* MiniCPM5Engine::load_model (src/model.cpp:33-133): parses the GGUF header
+ * at run time (the reference bakes offsets at compile time) and uploads every
+ * tensor once.  From a file or from a GGUF image in host memory. */
+int mcpm_engine_load_gguf(mcpm_ctx *ctx, const char *path, mcpm_engine **out);
+int mcpm_engine_load_gguf_memory(mcpm_ctx *ctx, const void *data, size_t bytes, mcpm_engine **out);
+void mcpm_engine_free(mcpm_engine *e);
+int mcpm_engine_config(const mcpm_engine *e, mcpm_model_config *out);
+/* Weight bytes read per decode token (all layers, LM head, one embedding row). */
+int64_t mcpm_engine_weight_bytes_per_token(const mcpm_engine *e);
+
+/* MiniCPM5Engine::init_kv_cache (src/model.cpp:17-24): fp32 K and V,
+ * [n_layers][max_seq_len][n_kv_heads*head_dim], zeroed. */
+int mcpm_engine_init_kv_cache(mcpm_engine *e, int max_seq_len);
+
+/* MiniCPM5Engine::forward (src/model.cpp:142-242): one token at position pos.
+ * logits (vocab floats, host) and argmax (host int) may each be NULL.
+ * MCPM_ERR_CONTEXT when pos >= the KV capacity or max_seq_len. */
+int mcpm_engine_forward(mcpm_engine *e, int token, int pos, int max_seq_len, float *logits, int *argmax);
+
+/* The prefill + greedy decode loop of ChatSession::generate_response
+ * (src/chat_session.cpp:154-186) with argmax in place of the sampler: feeds
+ * prompt[0..n_prompt) at positions 0.., then generates n_gen tokens
+ * (out_tokens[0] is the argmax after the last prompt token).  Runs on the
+ * device without host round trips between tokens. */
+int mcpm_engine_generate_greedy(mcpm_engine *e, const int *prompt, int n_prompt, int n_gen, int *out_tokens);
+
+/* Continues the greedy loop for n_steps more tokens from the device state the
+ * previous generate/decode call left (the last argmax at the next position),
+ * appending to the generated-token list; returns once the work is queued
+ * (mcpm_sync waits for it).  MCPM_ERR_CONTEXT when the KV cache is full. */
+int mcpm_engine_decode_steps(mcpm_engine *e, int n_steps);
+/* Copies the first n generated tokens (since the last generate call). */
+int mcpm_engine_tokens(mcpm_engine *e, int *out, int n);
+
+/* Same loop with the reference's temperature / top-p sampler
+ * (src/sampler.cpp:8-73) drawing from std::mt19937(seed). */
+int mcpm_engine_generate_sampled(mcpm_engine *e, const int *prompt, int n_prompt, int n_gen, float temperature,
+                                 float top_p, uint32_t seed, int *out_tokens);
+
+/* Sampler::sample (src/sampler.cpp:8-73) on host logits for a given uniform
+ * draw r in [0,1): returns the token id, or a negative error code. */
+int mcpm_sample_logits(const float *logits, int n, float temperature, float top_p, float r);
+
+/* 1: replay each token as one captured hipGraph (default); 0: eager launches. */
+int mcpm_engine_set_graph(mcpm_engine *e, int enable);
+
+/* Kernel-level timing for measurement.  Kernel classes: */
+#define MCPM_KC_QKV 0
+#define MCPM_KC_ATTN 1
+#define MCPM_KC_OPROJ 2
+#define MCPM_KC_GATE_UP 3
+#define MCPM_KC_DOWN 4
+#define MCPM_KC_LM_HEAD 5
+#define MCPM_KC_COUNT 6
+/* When enabled, HIP events bracket every launch of `kernel_class` on the
+ * engine stream (inside the captured graph too); mcpm_engine_kernel_time
+ * returns the summed milliseconds and launch count since the last reset. */
+int mcpm_engine_set_kernel_timing(mcpm_engine *e, int kernel_class);
+int mcpm_engine_kernel_time(mcpm_engine *e, double *total_ms, int64_t *launches);
+/* Algorithmic bytes one launch of `kernel_class` moves (weights + activations). */
+int64_t mcpm_engine_kernel_bytes(const mcpm_engine *e, int kernel_class);
+
+/* ------------------------------------------------ synthetic GGUF models -- */
+
+/* Writes a random-init MiniCPM5-shaped model as a GGUF v3 image: weights
+ * N(0, 0.02) and norm gains 1 + N(0, 0.1) from a counter-based generator
+ * keyed by (seed, tensor, index), quantized with this library's Q4_K / Q6_K /
+ * Q8_0 encoders.  mix 0: Q6_K for every attn_v and ffn_down (literal
+ * Q4_K_M reading); mix 1: llama.cpp's use_more_bits layers only.
+ * tied: one Q6_K token_embd shared with the LM head.  When path is NULL the
+ * image is returned in *image (free with mcpm_free_host) and its size in
+ * *image_bytes. */
+int mcpm_synth_gguf(const mcpm_model_config *cfg, uint64_t seed, int mix, const char *path, void **image,
+                    size_t *image_bytes);
+void mcpm_free_host(void *p);
+
+/* Deterministic host-side generators, exposed for tests and benchmarks. */
+void mcpm_synth_normal(uint64_t seed, uint64_t tensor_id, float mean, float stddev, float *out, size_t n);
+/* Encode fp32 rows (cols multiple of the block size) into ggml blocks. */
+int mcpm_quantize_rows(int ggml_type, const float *src, int64_t rows, int64_t cols, void *dst);
+size_t mcpm_type_row_bytes(int ggml_type, int64_t cols);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,593 @@
+// mcpm_engine.cpp -- the decode engine: GGUF load into HBM, KV cache, the
+// per-token kernel sequence (captured as one hipGraph) and the decode loops.
+//
+// One token (src/model.cpp:142-242), five fused kernels per layer:
+//   qkv    RMSNorm+Q8_K (lround) prologue, Q/K/V GEMV, RoPE + KV append epilogue
+//   attn   split softmax over 64-position chunks, last wave combines
+//   oproj  Q8_K (ties-even) prologue, O GEMV, residual add epilogue
+//   gateup RMSNorm+Q8_K (lround) prologue, gate/up GEMV, SwiGLU epilogue
+//   down   Q8_K (lround) prologue, down GEMV, residual add epilogue
+// then embedding at the start and RMSNorm+LM head+argmax at the end.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "gguf.h"
+#include "mcpm_host.h"
+
+using namespace mcpm;
+
+namespace {
+
+struct Layer {
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  DevTensor wq, wk, wv, wo, wg, wu, wd;
+};
+
+struct TimedPair {
+  hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct mcpm_engine {
+  mcpm_ctx* ctx = nullptr;
+  mcpm_model_config cfg{};
+  DevTensor embd, out_w;
+  float* out_norm = nullptr;
+  std::vector<Layer> L;
+  // activations
+  float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
+  float2* argmax_part = nullptr;
+  int lm_grid = 0;
+  StepState* st = nullptr;
+  StepState* h_st = nullptr;  // pinned staging, one per queued prefill token
+  int h_st_cap = 0;
+  int* out_tokens = nullptr;
+  int out_cap = 0;
+  int gen_count = 0;  // tokens generated since the last generate call
+  int next_pos = 0;   // position the next decode step runs at
+  // KV cache and attention scratch
+  float *kc = nullptr, *vc = nullptr;
+  int max_seq = 0;
+  int max_chunks = 0;
+  float2* rope = nullptr;
+  float* attn_part = nullptr;
+  unsigned* attn_cnt = nullptr;
+  // graph
+  bool use_graph = true;
+  hipGraphExec_t graph = nullptr;
+  // timing
+  int timing_class = -1;
+  std::vector<TimedPair> events;
+  size_t events_used = 0;
+  int64_t weight_bytes = 0;
+};
+
+namespace {
+
+int alloc_dev(void** p, size_t bytes) {
+  MCPM_HIP(hipMalloc(p, bytes ? bytes : 4));
+  MCPM_HIP(hipMemset(*p, 0, bytes ? bytes : 4));
+  return MCPM_OK;
+}
+
+void drop_graph(mcpm_engine* e) {
+  if (e->graph) (void)hipGraphExecDestroy(e->graph);
+  e->graph = nullptr;
+}
+
+void free_engine(mcpm_engine* e) {
+  if (!e) return;
+  (void)hipStreamSynchronize(e->ctx->stream);
+  drop_graph(e);
+  for (auto& p : e->events) {
+    (void)hipEventDestroy(p.a);
+    (void)hipEventDestroy(p.b);
+  }
+  free_tensor(e->embd);
+  free_tensor(e->out_w);
+  if (e->out_norm) (void)hipFree(e->out_norm);
+  for (auto& l : e->L) {
+    if (l.attn_norm) (void)hipFree(l.attn_norm);
+    if (l.ffn_norm) (void)hipFree(l.ffn_norm);
+    for (DevTensor* t : {&l.wq, &l.wk, &l.wv, &l.wo, &l.wg, &l.wu, &l.wd}) free_tensor(*t);
+  }
+  for (void* p : {static_cast<void*>(e->x), static_cast<void*>(e->q), static_cast<void*>(e->att),
+                  static_cast<void*>(e->h), static_cast<void*>(e->logits), static_cast<void*>(e->argmax_part),
+                  static_cast<void*>(e->st), static_cast<void*>(e->out_tokens), static_cast<void*>(e->kc),
+                  static_cast<void*>(e->vc), static_cast<void*>(e->rope), static_cast<void*>(e->attn_part),
+                  static_cast<void*>(e->attn_cnt)})
+    if (p) (void)hipFree(p);
+  if (e->h_st) (void)hipHostFree(e->h_st);
+  delete e;
+}
+
+int load_f32(mcpm_ctx* ctx, const GgufTensor* t, int n, float** out) {
+  if (!t || t->type != MCPM_TYPE_F32 || static_cast<int64_t>(t->dims[0]) != n)
+    return fail(MCPM_ERR_FORMAT, "missing or malformed F32 tensor " + (t ? t->name : std::string("?")));
+  MCPM_HIP(hipMalloc(out, n * sizeof(float)));
+  MCPM_HIP(hipMemcpyAsync(*out, t->data, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+  MCPM_HIP(hipStreamSynchronize(ctx->stream));
+  return MCPM_OK;
+}
+
+int load_mat(mcpm_ctx* ctx, const GgufTensor* t, int64_t cols, int64_t rows, std::initializer_list<int> types,
+             DevTensor& out, int64_t& bytes) {
+  if (!t) return fail(MCPM_ERR_FORMAT, "missing tensor");
+  if (t->dims.size() < 2 || static_cast<int64_t>(t->dims[0]) != cols || static_cast<int64_t>(t->dims[1]) != rows)
+    return fail(MCPM_ERR_FORMAT, "tensor " + t->name + " has unexpected dims");
+  if (std::find(types.begin(), types.end(), static_cast<int>(t->type)) == types.end())
+    return fail(MCPM_ERR_UNSUPPORTED, "tensor " + t->name + " has unsupported type " + std::to_string(t->type));
+  bytes += static_cast<int64_t>(t->bytes);
+  return upload_tensor(ctx, t->data, t->bytes, static_cast<int>(t->type), cols, rows, out);
+}
+
+int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine** out) {
+  GgufFile f;
+  std::string err;
+  if (!gguf_parse(data, size, f, err)) return fail(MCPM_ERR_FORMAT, "GGUF: " + err);
+  std::string arch = "llama";
+  f.get_str("general.architecture", arch);
+  auto geti = [&](const std::string& k, int64_t dflt) {
+    int64_t v;
+    return f.get_int(arch + "." + k, v) ? v : dflt;
+  };
+  auto getf = [&](const std::string& k, double dflt) {
+    double v;
+    return f.get_float(arch + "." + k, v) ? v : dflt;
+  };
+  mcpm_model_config c{};
+  c.n_layers = static_cast<int>(geti("block_count", 0));
+  c.dim = static_cast<int>(geti("embedding_length", 0));
+  c.ffn = static_cast<int>(geti("feed_forward_length", 0));
+  c.n_heads = static_cast<int>(geti("attention.head_count", 0));
+  c.n_kv_heads = static_cast<int>(geti("attention.head_count_kv", c.n_heads));
+  c.head_dim = c.n_heads ? static_cast<int>(geti("attention.key_length", c.dim / c.n_heads)) : 0;
+  c.rope_base = static_cast<float>(getf("rope.freq_base", 10000.0));
+  c.eps = static_cast<float>(getf("attention.layer_norm_rms_epsilon", 1e-6));
+  const GgufTensor* te = f.find("token_embd.weight");
+  if (!te || te->dims.size() < 2) return fail(MCPM_ERR_FORMAT, "GGUF: token_embd.weight missing");
+  c.vocab = static_cast<int>(te->dims[1]);
+  const GgufTensor* td0 = f.find("blk.0.ffn_down.weight");
+  c.ffn_pad = td0 ? static_cast<int>(td0->dims[0]) : (c.ffn + 255) / 256 * 256;
+  const GgufTensor* to = f.find("output.weight");
+  c.tied_embeddings = to ? 0 : 1;
+  const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+  if (c.n_layers <= 0 || c.dim <= 0 || c.dim % QK_K || c.dim / QK_K > MAX_NB || qd % QK_K || qd / QK_K > MAX_NB ||
+      c.ffn <= 0 || c.ffn_pad < c.ffn || c.ffn_pad % QK_K || c.ffn_pad / QK_K > MAX_NB || c.n_kv_heads <= 0 ||
+      c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 8 || c.head_dim % 8 || c.head_dim > 128 ||
+      kvd % 8 || c.n_kv_heads > 256)
+    return fail(MCPM_ERR_FORMAT, "GGUF: model shape not supported by the engine");
+
+  auto* e = new mcpm_engine();
+  e->ctx = ctx;
+  e->cfg = c;
+  int rc = MCPM_OK;
+  int64_t wb = 0;
+  auto T = [&](const std::string& n) { return f.find(n); };
+  rc = load_mat(ctx, te, c.dim, c.vocab, {MCPM_TYPE_Q4_K, MCPM_TYPE_Q6_K}, e->embd, wb);
+  const int64_t embd_bytes = wb;
+  wb = 0;
+  if (!rc) rc = load_f32(ctx, T("output_norm.weight"), c.dim, &e->out_norm);
+  if (!rc && to) rc = load_mat(ctx, to, c.dim, c.vocab, {MCPM_TYPE_Q4_K, MCPM_TYPE_Q6_K}, e->out_w, wb);
+  if (!rc && !to) {
+    e->out_w = e->embd;
+    e->out_w.owned = false;
+    wb += embd_bytes;
+  }
+  e->L.resize(c.n_layers);
+  for (int l = 0; l < c.n_layers && !rc; ++l) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    Layer& L = e->L[l];
+    rc = load_f32(ctx, T(p + "attn_norm.weight"), c.dim, &L.attn_norm);
+    if (!rc) rc = load_f32(ctx, T(p + "ffn_norm.weight"), c.dim, &L.ffn_norm);
+    if (!rc) rc = load_mat(ctx, T(p + "attn_q.weight"), c.dim, qd, {MCPM_TYPE_Q4_K}, L.wq, wb);
+    if (!rc) rc = load_mat(ctx, T(p + "attn_k.weight"), c.dim, kvd, {MCPM_TYPE_Q4_K}, L.wk, wb);
+    if (!rc) rc = load_mat(ctx, T(p + "attn_v.weight"), c.dim, kvd, {MCPM_TYPE_Q4_K, MCPM_TYPE_Q6_K}, L.wv, wb);
+    if (!rc) rc = load_mat(ctx, T(p + "attn_output.weight"), qd, c.dim, {MCPM_TYPE_Q4_K, MCPM_TYPE_Q6_K}, L.wo, wb);
+    if (!rc) rc = load_mat(ctx, T(p + "ffn_gate.weight"), c.dim, c.ffn, {MCPM_TYPE_Q4_K}, L.wg, wb);
+    if (!rc) rc = load_mat(ctx, T(p + "ffn_up.weight"), c.dim, c.ffn, {MCPM_TYPE_Q4_K}, L.wu, wb);
+    if (!rc) rc = load_mat(ctx, T(p + "ffn_down.weight"), c.ffn_pad, c.dim, {MCPM_TYPE_Q4_K, MCPM_TYPE_Q6_K}, L.wd, wb);
+    wb += 2 * static_cast<int64_t>(c.dim) * 4;  // the two norm gains
+  }
+  // per token: every layer, LM head, output norm, one embedding row
+  e->weight_bytes = wb + static_cast<int64_t>(c.dim) * 4 + static_cast<int64_t>(embd_bytes / c.vocab);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->x), c.dim * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->q), qd * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->att), qd * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->h), c.ffn_pad * 4);  // padding stays zero
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->logits), static_cast<size_t>(c.vocab) * 4);
+  if (!rc) {
+    GemvArgs a{};
+    a.total_rows = c.vocab;
+    a.nreg = 1;
+    e->lm_grid = gemv_grid(a, ctx->n_cu);
+    rc = alloc_dev(reinterpret_cast<void**>(&e->argmax_part), e->lm_grid * sizeof(float2));
+  }
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->st), sizeof(StepState));
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->attn_cnt), 256 * sizeof(unsigned));
+  if (rc) {
+    free_engine(e);
+    return rc;
+  }
+  *out = e;
+  return MCPM_OK;
+}
+
+int ensure_out_tokens(mcpm_engine* e, int n) {
+  if (n <= e->out_cap) return MCPM_OK;
+  if (e->out_tokens) (void)hipFree(e->out_tokens);
+  e->out_tokens = nullptr;
+  e->out_cap = 0;
+  int rc = alloc_dev(reinterpret_cast<void**>(&e->out_tokens), n * sizeof(int));
+  if (rc) return rc;
+  e->out_cap = n;
+  drop_graph(e);  // the argmax node holds the array pointer
+  return MCPM_OK;
+}
+
+int ensure_staging(mcpm_engine* e, int n) {
+  if (n <= e->h_st_cap) return MCPM_OK;
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  if (e->h_st) (void)hipHostFree(e->h_st);
+  e->h_st = nullptr;
+  e->h_st_cap = 0;
+  MCPM_HIP(hipHostMalloc(reinterpret_cast<void**>(&e->h_st), n * sizeof(StepState), hipHostMallocDefault));
+  e->h_st_cap = n;
+  return MCPM_OK;
+}
+
+// Launch helper that brackets the launch with events when its class is timed.
+template <class F>
+hipError_t timed(mcpm_engine* e, int kc, F&& launch) {
+  hipStream_t s = e->ctx->stream;
+  if (kc != e->timing_class) return launch();
+  if (e->events_used == e->events.size()) {
+    TimedPair p;
+    hipError_t err = hipEventCreate(&p.a);
+    if (err == hipSuccess) err = hipEventCreate(&p.b);
+    if (err != hipSuccess) return err;
+    e->events.push_back(p);
+  }
+  TimedPair& p = e->events[e->events_used++];
+  hipError_t err = hipEventRecord(p.a, s);
+  if (err == hipSuccess) err = launch();
+  if (err == hipSuccess) err = hipEventRecord(p.b, s);
+  return err;
+}
+
+// All kernels of one token, reading token and pos from e->st.
+int enqueue_token(mcpm_engine* e) {
+  const mcpm_model_config& c = e->cfg;
+  hipStream_t s = e->ctx->stream;
+  const int n_cu = e->ctx->n_cu;
+  const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+  const int* st = reinterpret_cast<const int*>(e->st);
+  MCPM_HIP(launch_embedding(view_of(e->embd), st, c.dim, e->x, s));
+  for (int l = 0; l < c.n_layers; ++l) {
+    const Layer& L = e->L[l];
+    float* kc = e->kc + static_cast<size_t>(l) * e->max_seq * kvd;
+    float* vc = e->vc + static_cast<size_t>(l) * e->max_seq * kvd;
+    {
+      GemvArgs a{};
+      a.reg[0] = GemvRegion{view_of(L.wq), e->q, 0, qd};
+      a.reg[1] = GemvRegion{view_of(L.wk), nullptr, qd, kvd};
+      a.reg[2] = GemvRegion{view_of(L.wv), nullptr, qd + kvd, kvd};
+      a.nreg = 3;
+      a.total_rows = qd + 2 * kvd;
+      a.nb = c.dim / QK_K;
+      a.x = e->x;
+      a.gamma = L.attn_norm;
+      a.eps = c.eps;
+      a.state = st;
+      a.rope_cs = e->rope;
+      a.head_dim = c.head_dim;
+      a.k_cache = kc;
+      a.v_cache = vc;
+      a.kvd = kvd;
+      MCPM_HIP(timed(e, MCPM_KC_QKV, [&] { return launch_gemv(a, PRO_NORM_AWAY, EPI_QKV, n_cu, s); }));
+    }
+    MCPM_HIP(timed(e, MCPM_KC_ATTN, [&] {
+      return launch_attention(e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, e->attn_part,
+                              e->attn_cnt, e->att, s);
+    }));
+    {
+      GemvArgs a{};
+      a.reg[0] = GemvRegion{view_of(L.wo), nullptr, 0, c.dim};
+      a.nreg = 1;
+      a.total_rows = c.dim;
+      a.nb = qd / QK_K;
+      a.x = e->att;
+      a.resid = e->x;
+      MCPM_HIP(timed(e, MCPM_KC_OPROJ, [&] { return launch_gemv(a, PRO_QUANT_EVEN, EPI_RESID, n_cu, s); }));
+    }
+    {
+      GemvArgs a{};
+      a.reg[0] = GemvRegion{view_of(L.wg), nullptr, 0, c.ffn};
+      a.reg[1] = GemvRegion{view_of(L.wu), nullptr, 0, c.ffn};
+      a.nreg = 2;
+      a.pair = 1;
+      a.total_rows = c.ffn;
+      a.nb = c.dim / QK_K;
+      a.x = e->x;
+      a.gamma = L.ffn_norm;
+      a.eps = c.eps;
+      a.h_out = e->h;
+      MCPM_HIP(timed(e, MCPM_KC_GATE_UP, [&] { return launch_gemv(a, PRO_NORM_AWAY, EPI_SWIGLU, n_cu, s); }));
+    }
+    {
+      GemvArgs a{};
+      a.reg[0] = GemvRegion{view_of(L.wd), nullptr, 0, c.dim};
+      a.nreg = 1;
+      a.total_rows = c.dim;
+      a.nb = c.ffn_pad / QK_K;
+      a.x = e->h;
+      a.resid = e->x;
+      MCPM_HIP(timed(e, MCPM_KC_DOWN, [&] { return launch_gemv(a, PRO_QUANT_AWAY, EPI_RESID, n_cu, s); }));
+    }
+  }
+  {
+    GemvArgs a{};
+    a.reg[0] = GemvRegion{view_of(e->out_w), e->logits, 0, c.vocab};
+    a.nreg = 1;
+    a.total_rows = c.vocab;
+    a.nb = c.dim / QK_K;
+    a.x = e->x;
+    a.gamma = e->out_norm;
+    a.eps = c.eps;
+    a.argmax_part = e->argmax_part;
+    MCPM_HIP(timed(e, MCPM_KC_LM_HEAD, [&] { return launch_gemv(a, PRO_NORM_EVEN, EPI_LOGITS, n_cu, s); }));
+  }
+  MCPM_HIP(launch_argmax_final(e->argmax_part, e->lm_grid, nullptr, e->st, e->out_tokens, s));
+  return MCPM_OK;
+}
+
+int run_token(mcpm_engine* e) {
+  // Events recorded inside a captured graph cannot be read back with
+  // hipEventElapsedTime, so a timed kernel class runs the same launches eagerly.
+  if (!e->use_graph || e->timing_class >= 0) return enqueue_token(e);
+  if (!e->graph) {
+    hipStream_t s = e->ctx->stream;
+    MCPM_HIP(hipStreamSynchronize(s));
+    MCPM_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_token(e);
+    hipGraph_t g = nullptr;
+    const hipError_t ce = hipStreamEndCapture(s, &g);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (ce != hipSuccess) return hip_fail(ce, "hipStreamEndCapture");
+    const hipError_t ie = hipGraphInstantiate(&e->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess) {
+      e->graph = nullptr;
+      return hip_fail(ie, "hipGraphInstantiate");
+    }
+  }
+  MCPM_HIP(hipGraphLaunch(e->graph, e->ctx->stream));
+  return MCPM_OK;
+}
+
+// Queues a state write (token, pos) from pinned staging slot `slot`.
+int queue_state(mcpm_engine* e, int slot, int token, int pos, int step) {
+  StepState& hs = e->h_st[slot];
+  hs.token = token;
+  hs.pos = pos;
+  hs.step = step;
+  hs.n_out = e->out_cap;
+  MCPM_HIP(hipMemcpyAsync(e->st, &hs, sizeof(StepState), hipMemcpyHostToDevice, e->ctx->stream));
+  return MCPM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mcpm_engine_load_gguf(mcpm_ctx* ctx, const char* path, mcpm_engine** out) {
+  if (!ctx || !path || !out) return fail(MCPM_ERR_ARG, "mcpm_engine_load_gguf: null argument");
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) return fail(MCPM_ERR_IO, std::string("Failed to open GGUF file: ") + path);
+  struct stat sb;
+  if (fstat(fd, &sb) != 0 || sb.st_size <= 0) {
+    close(fd);
+    return fail(MCPM_ERR_IO, std::string("Cannot stat GGUF file: ") + path);
+  }
+  void* m = mmap(nullptr, static_cast<size_t>(sb.st_size), PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  if (m == MAP_FAILED) return fail(MCPM_ERR_IO, std::string("Cannot map GGUF file: ") + path);
+  const int rc = load_from_image(ctx, static_cast<const uint8_t*>(m), static_cast<size_t>(sb.st_size), out);
+  munmap(m, static_cast<size_t>(sb.st_size));
+  return rc;
+}
+
+int mcpm_engine_load_gguf_memory(mcpm_ctx* ctx, const void* data, size_t bytes, mcpm_engine** out) {
+  if (!ctx || !data || !out) return fail(MCPM_ERR_ARG, "mcpm_engine_load_gguf_memory: null argument");
+  return load_from_image(ctx, static_cast<const uint8_t*>(data), bytes, out);
+}
+
+void mcpm_engine_free(mcpm_engine* e) { free_engine(e); }
+
+int mcpm_engine_config(const mcpm_engine* e, mcpm_model_config* out) {
+  if (!e || !out) return fail(MCPM_ERR_ARG, "mcpm_engine_config: null argument");
+  *out = e->cfg;
+  return MCPM_OK;
+}
+
+int64_t mcpm_engine_weight_bytes_per_token(const mcpm_engine* e) { return e ? e->weight_bytes : 0; }
+
+int mcpm_engine_init_kv_cache(mcpm_engine* e, int max_seq_len) {
+  if (!e || max_seq_len <= 0) return fail(MCPM_ERR_ARG, "mcpm_engine_init_kv_cache: bad argument");
+  const mcpm_model_config& c = e->cfg;
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  drop_graph(e);
+  for (void** p : {reinterpret_cast<void**>(&e->kc), reinterpret_cast<void**>(&e->vc),
+                   reinterpret_cast<void**>(&e->rope), reinterpret_cast<void**>(&e->attn_part)}) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+  }
+  e->max_seq = 0;
+  const size_t kvd = static_cast<size_t>(c.n_kv_heads) * c.head_dim;
+  const size_t kv_bytes = static_cast<size_t>(c.n_layers) * max_seq_len * kvd * sizeof(float);
+  int rc = alloc_dev(reinterpret_cast<void**>(&e->kc), kv_bytes);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->vc), kv_bytes);
+  if (rc) return rc;
+  // RoPE (cos, sin) table for positions 0..max_seq_len-1 (src/ops/ops.cpp:503-508).
+  std::vector<float2> tab(static_cast<size_t>(max_seq_len) * (c.head_dim / 2));
+  for (int p = 0; p < max_seq_len; ++p) rope_row(p, c.head_dim, c.rope_base, tab.data() + static_cast<size_t>(p) * (c.head_dim / 2));
+  MCPM_HIP(hipMalloc(&e->rope, tab.size() * sizeof(float2)));
+  MCPM_HIP(hipMemcpy(e->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+  e->max_chunks = (max_seq_len + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  rc = alloc_dev(reinterpret_cast<void**>(&e->attn_part),
+                 static_cast<size_t>(c.n_heads) * e->max_chunks * (2 + c.head_dim) * sizeof(float));
+  if (rc) return rc;
+  e->max_seq = max_seq_len;
+  return MCPM_OK;
+}
+
+int mcpm_engine_set_graph(mcpm_engine* e, int enable) {
+  if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_set_graph: null engine");
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  e->use_graph = enable != 0;
+  drop_graph(e);
+  return MCPM_OK;
+}
+
+int mcpm_engine_forward(mcpm_engine* e, int token, int pos, int max_seq_len, float* logits, int* argmax) {
+  if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_forward: null engine");
+  if (!e->kc) return fail(MCPM_ERR_CONTEXT, "mcpm_engine_forward: KV cache not initialised");
+  if (pos < 0 || pos >= max_seq_len || pos >= e->max_seq)
+    return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
+  if (token < 0 || token >= e->cfg.vocab) return fail(MCPM_ERR_ARG, "mcpm_engine_forward: token out of range");
+  int rc = ensure_out_tokens(e, 1);
+  if (!rc) rc = ensure_staging(e, 1);
+  if (rc) return rc;
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  rc = queue_state(e, 0, token, pos, 0);
+  if (!rc) rc = run_token(e);
+  if (rc) return rc;
+  e->gen_count = 0;
+  if (logits)
+    MCPM_HIP(hipMemcpyAsync(logits, e->logits, static_cast<size_t>(e->cfg.vocab) * 4, hipMemcpyDeviceToHost,
+                            e->ctx->stream));
+  if (argmax) MCPM_HIP(hipMemcpyAsync(e->h_st, e->st, sizeof(StepState), hipMemcpyDeviceToHost, e->ctx->stream));
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  if (argmax) *argmax = e->h_st[0].token;
+  return MCPM_OK;
+}
+
+int mcpm_engine_generate_greedy(mcpm_engine* e, const int* prompt, int n_prompt, int n_gen, int* out_tokens) {
+  if (!e || !prompt || !out_tokens || n_prompt <= 0 || n_gen <= 0)
+    return fail(MCPM_ERR_ARG, "mcpm_engine_generate_greedy: bad argument");
+  if (!e->kc) return fail(MCPM_ERR_CONTEXT, "KV cache not initialised");
+  if (n_prompt + n_gen - 1 > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab) return fail(MCPM_ERR_ARG, "prompt token out of range");
+  int rc = ensure_out_tokens(e, n_gen);
+  if (!rc) rc = ensure_staging(e, n_prompt);
+  if (rc) return rc;
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  for (int p = 0; p < n_prompt && !rc; ++p) {
+    rc = queue_state(e, p, prompt[p], p, 0);
+    if (!rc) rc = run_token(e);
+  }
+  for (int i = 1; i < n_gen && !rc; ++i) rc = run_token(e);
+  if (rc) return rc;
+  e->gen_count = n_gen;
+  e->next_pos = n_prompt + n_gen - 1;
+  MCPM_HIP(hipMemcpyAsync(out_tokens, e->out_tokens, n_gen * sizeof(int), hipMemcpyDeviceToHost, e->ctx->stream));
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  return MCPM_OK;
+}
+
+int mcpm_engine_decode_steps(mcpm_engine* e, int n_steps) {
+  if (!e || n_steps < 0) return fail(MCPM_ERR_ARG, "mcpm_engine_decode_steps: bad argument");
+  if (e->gen_count == 0) return fail(MCPM_ERR_ARG, "mcpm_engine_decode_steps: no generate call to continue");
+  if (e->next_pos + n_steps > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
+  if (e->gen_count + n_steps > e->out_cap) {
+    // grow the token list, keeping what is there
+    std::vector<int> keep(e->gen_count);
+    MCPM_HIP(hipMemcpyAsync(keep.data(), e->out_tokens, keep.size() * sizeof(int), hipMemcpyDeviceToHost,
+                            e->ctx->stream));
+    MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+    int rc = ensure_out_tokens(e, e->gen_count + n_steps);
+    if (rc) return rc;
+    MCPM_HIP(hipMemcpy(e->out_tokens, keep.data(), keep.size() * sizeof(int), hipMemcpyHostToDevice));
+    // the state's capacity field must follow the new array
+    StepState st;
+    MCPM_HIP(hipMemcpy(&st, e->st, sizeof(st), hipMemcpyDeviceToHost));
+    st.n_out = e->out_cap;
+    MCPM_HIP(hipMemcpy(e->st, &st, sizeof(st), hipMemcpyHostToDevice));
+  }
+  for (int i = 0; i < n_steps; ++i) {
+    const int rc = run_token(e);
+    if (rc) return rc;
+  }
+  e->gen_count += n_steps;
+  e->next_pos += n_steps;
+  return MCPM_OK;
+}
+
+int mcpm_engine_tokens(mcpm_engine* e, int* out, int n) {
+  if (!e || !out || n < 0 || n > e->gen_count) return fail(MCPM_ERR_ARG, "mcpm_engine_tokens: bad argument");
+  MCPM_HIP(hipMemcpyAsync(out, e->out_tokens, n * sizeof(int), hipMemcpyDeviceToHost, e->ctx->stream));
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  return MCPM_OK;
+}
+
+int mcpm_engine_set_kernel_timing(mcpm_engine* e, int kernel_class) {
+  if (!e || kernel_class < -1 || kernel_class >= MCPM_KC_COUNT)
+    return fail(MCPM_ERR_ARG, "mcpm_engine_set_kernel_timing: bad argument");
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  e->timing_class = kernel_class;
+  e->events_used = 0;
+  drop_graph(e);
+  return MCPM_OK;
+}
+
+int mcpm_engine_kernel_time(mcpm_engine* e, double* total_ms, int64_t* launches) {
+  if (!e || !total_ms || !launches) return fail(MCPM_ERR_ARG, "mcpm_engine_kernel_time: null argument");
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  double t = 0.0;
+  for (size_t i = 0; i < e->events_used; ++i) {
+    float ms = 0.0f;
+    MCPM_HIP(hipEventElapsedTime(&ms, e->events[i].a, e->events[i].b));
+    t += ms;
+  }
+  *total_ms = t;
+  *launches = static_cast<int64_t>(e->events_used);
+  return MCPM_OK;
+}
+
+int64_t mcpm_engine_kernel_bytes(const mcpm_engine* e, int kc) {
+  if (!e) return 0;
+  const mcpm_model_config& c = e->cfg;
+  const int64_t qd = static_cast<int64_t>(c.n_heads) * c.head_dim, kvd = static_cast<int64_t>(c.n_kv_heads) * c.head_dim;
+  const Layer& L = e->L[0];
+  switch (kc) {
+    case MCPM_KC_QKV:
+      return static_cast<int64_t>(L.wq.bytes + L.wk.bytes + L.wv.bytes) + 8 * c.dim + 4 * (qd + 2 * kvd);
+    case MCPM_KC_OPROJ:
+      return static_cast<int64_t>(L.wo.bytes) + 4 * qd + 8 * c.dim;
+    case MCPM_KC_GATE_UP:
+      return static_cast<int64_t>(L.wg.bytes + L.wu.bytes) + 8 * c.dim + 4 * static_cast<int64_t>(c.ffn);
+    case MCPM_KC_DOWN:
+      return static_cast<int64_t>(L.wd.bytes) + 4 * static_cast<int64_t>(c.ffn_pad) + 8 * c.dim;
+    case MCPM_KC_LM_HEAD:
+      return static_cast<int64_t>(e->out_w.bytes) + 8 * c.dim + 4 * static_cast<int64_t>(c.vocab);
+    case MCPM_KC_ATTN:
+      // K and V rows of the current context, the query and the output
+      return 2 * static_cast<int64_t>(e->next_pos + 1) * kvd * 4 + 8 * qd;
+    default:
+      return 0;
+  }
+}
+
+}  // extern "C"

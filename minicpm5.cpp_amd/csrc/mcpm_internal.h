@@ -1,0 +1,230 @@
+// mcpm_internal.h -- definitions shared by the HIP kernels and the host code of
+// libmcpm_hip.so.  Not installed; the public surface is include/mcpm_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "mcpm_hip.h"
+
+namespace mcpm {
+
+constexpr int QK_K = 256;
+constexpr int QK8_0 = 32;
+constexpr int MAX_NB = 32;        // largest K / 256 the Q8_K GEMVs accept (K <= 8192)
+constexpr int ATTN_CHUNK = 64;    // positions per attention split
+constexpr int GEMV_THREADS = 256; // 4 waves
+constexpr int ROWS_PER_GROUP = 8; // output rows per GEMV work item (8 lanes each)
+
+// ggml block layouts (include/ops.h:33-65).  Byte images only; the kernels
+// read the re-laid-out planes described in DevTensor.
+struct BlockQ8_0 { uint16_t d; int8_t qs[32]; };
+struct BlockQ4K { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; };
+struct BlockQ6K { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; };
+struct BlockQ8K { float d; int8_t qs[256]; int16_t bsums[16]; };
+static_assert(sizeof(BlockQ8_0) == 34, "Q8_0 block is 34 bytes");
+static_assert(sizeof(BlockQ4K) == 144, "Q4_K block is 144 bytes");
+static_assert(sizeof(BlockQ6K) == 210, "Q6_K block is 210 bytes");
+static_assert(sizeof(BlockQ8K) == 292, "Q8_K block is 292 bytes");
+
+// IEEE binary16 -> binary32, exact for every input (the conversion of
+// include/ops.h:14-31 and of F16C's _cvtsh_ss).
+__host__ __device__ inline float fp16_to_fp32(uint16_t h) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+#else
+  uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
+  int32_t exp = (h >> 10) & 0x1f;
+  uint32_t mant = h & 0x3ffu;
+  uint32_t bits;
+  if (exp == 0x1f) {
+    bits = sign | 0x7f800000u | (mant << 13);
+  } else if (exp == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else {
+      int e = -1;
+      do { mant <<= 1; e++; } while (!(mant & 0x400u));
+      bits = sign | (static_cast<uint32_t>(112 - e) << 23) | ((mant & 0x3ffu) << 13);
+    }
+  } else {
+    bits = sign | (static_cast<uint32_t>(exp + 112) << 23) | (mant << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+#endif
+}
+
+// fp32 -> binary16, round to nearest even (used by the weight encoders).
+uint16_t fp32_to_fp16(float f);
+
+// exp(x) in fp32 from the mathematics: k = nearest integer to x/ln2, r = x -
+// k*ln2 with ln2 split in two parts (Cody-Waite), exp(r) by its Taylor series
+// to degree 7 (Horner, fused multiply-adds), times 2^k.  Host and device run
+// the same operation sequence, so they round identically.  Used where the
+// reference calls std::exp (SiLU ops.cpp:740, softmax ops.cpp:601,
+// sampler.cpp:30,36).
+__host__ __device__ inline float exp_f32(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.972084045410156f) return 0.0f;
+  const float inv_ln2 = 1.44269502162933349609375f;
+  const float ln2_hi = 0.693145751953125f;
+  const float ln2_lo = 1.428606765330187045e-06f;
+  const float k = __builtin_rintf(x * inv_ln2);
+  float r = __builtin_fmaf(-k, ln2_hi, x);
+  r = __builtin_fmaf(-k, ln2_lo, r);
+  float p = 1.98412698412698412526e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888894189e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333321769e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666643537e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666657415e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, static_cast<int>(k));
+}
+
+// A weight matrix in HBM.  Blocks are stored block-column-major (block b of
+// row r at index b*rows + r) so the 8 rows a wave reads for one block column
+// are contiguous, and each block's bytes are split into planes:
+//   Q4_K  p0: 128 B quants per block, dword (j*8+m) moved to (m*4+j), so lane
+//             m of 8 reads its 16 B with one load;  p1: 16 B header (d, dmin,
+//             12 scale bytes) exactly as in the block.
+//   Q6_K  p0: 128 B ql, the same dword permutation;  p1: 64 B qh, dword
+//             (h*8+m) moved to (m*2+h);  p2: 16 B int8 scales;  p3: 2 B d.
+//   Q8_0  p0: 32 B quants;  p1: 2 B d.
+//   F32   p0: row-major floats.
+// Bytes per block are unchanged (144 / 210 / 34), so dequantized values are
+// bit-identical to the GGUF blocks.
+struct DevTensor {
+  int type = -1;
+  int64_t rows = 0, cols = 0;
+  int nb = 0;  // blocks per row
+  void* base = nullptr;
+  size_t bytes = 0;  // native (GGUF) size == device size
+  const uint8_t* p0 = nullptr;
+  const uint8_t* p1 = nullptr;
+  const uint8_t* p2 = nullptr;
+  const uint8_t* p3 = nullptr;
+  bool owned = true;
+};
+
+// Kernel-side view of one weight matrix.
+struct WView {
+  int type;
+  int rows;
+  int nb;
+  const uint8_t* p0;
+  const uint8_t* p1;
+  const uint8_t* p2;
+  const uint8_t* p3;
+};
+
+inline WView view_of(const DevTensor& t) {
+  return WView{t.type, static_cast<int>(t.rows), t.nb, t.p0, t.p1, t.p2, t.p3};
+}
+
+size_t type_row_bytes(int type, int64_t cols);
+int type_block_elems(int type);
+// Host-side plane layout: native GGUF bytes <-> device image.
+void repack_to_device_image(int type, int64_t rows, int64_t cols, const uint8_t* native, uint8_t* image);
+void repack_from_device_image(int type, int64_t rows, int64_t cols, const uint8_t* image, uint8_t* native);
+void set_planes(DevTensor& t);
+
+// ------------------------------------------------------------ errors -------
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+#define MCPM_HIP(call)                                      \
+  do {                                                      \
+    hipError_t e_ = (call);                                 \
+    if (e_ != hipSuccess) return ::mcpm::hip_fail(e_, #call); \
+  } while (0)
+
+// ------------------------------------------------------------ launches -----
+// Prologue modes of the Q8_K GEMV: how the WG obtains its Q8_K activations.
+enum Prologue : int {
+  PRO_Q8K = 0,        // native Q8_K blocks in global memory
+  PRO_QUANT_EVEN = 1, // quantize an fp32 vector, ties to even (quantize_row_q8_K)
+  PRO_QUANT_AWAY = 2, // quantize an fp32 vector, ties away (lround)
+  PRO_NORM_AWAY = 3,  // RMSNorm then quantize, ties away (rmsnorm_and_quantize_q8k)
+  PRO_NORM_EVEN = 4,  // RMSNorm then quantize, ties to even (rmsnorm + matmul)
+};
+
+// Epilogue modes.
+enum Epilogue : int {
+  EPI_STORE = 0,   // out[row] = v
+  EPI_QKV = 1,     // RoPE on q,k; q -> out0, k,v -> KV cache at pos
+  EPI_RESID = 2,   // x[row] += v
+  EPI_SWIGLU = 3,  // gate/up pairs -> h = silu(g)*u
+  EPI_LOGITS = 4,  // out[row] = v plus per-WG argmax
+};
+
+struct GemvRegion {
+  WView w;
+  float* out;
+  int row0;  // first virtual row of this region
+  int rows;
+};
+
+struct GemvArgs {
+  GemvRegion reg[3];
+  int nreg;
+  int total_rows;  // virtual rows (pair mode: rows of one matrix)
+  int nb;
+  int pair;        // 1: slots 0-3 from reg[0], 4-7 from reg[1], same rows
+  // prologue inputs
+  const BlockQ8K* xq;
+  const float* x;
+  const float* gamma;
+  float eps;
+  // epilogue inputs
+  const int* state;      // [0] token, [1] pos
+  const float2* rope_cs; // [max_seq][head_dim/2] (cos, sin)
+  int head_dim;
+  float* k_cache;        // layer base, [max_seq][kvd]
+  float* v_cache;
+  int kvd;
+  float* resid;
+  float* h_out;
+  float2* argmax_part;   // per WG (value, index as float bits)
+};
+
+// Device step state shared by the engine's kernels.
+struct StepState {
+  int token;
+  int pos;
+  int step;       // index of the next generated token
+  int n_out;      // capacity of the generated-token array
+};
+
+hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s);
+int gemv_grid(const GemvArgs& a, int n_cu);
+
+hipError_t launch_quantize_q8k(const float* x, const float* gamma, float eps, int dim, int mode, BlockQ8K* out,
+                               hipStream_t s);
+hipError_t launch_rmsnorm(const float* x, const float* w, float eps, int dim, float* out, hipStream_t s);
+hipError_t launch_swiglu_quant(const float* g, const float* u, int dim, BlockQ8K* out, hipStream_t s);
+hipError_t launch_rope(float* vec, const float2* cs, int n_heads, int head_dim, hipStream_t s);
+hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc, const int* state, int kvd,
+                            hipStream_t s);
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, const int* state, int n_heads,
+                            int n_kv_heads, int head_dim, int max_chunks, float* part, unsigned* counters,
+                            float* out, hipStream_t s);
+hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s);
+hipError_t launch_dequant_rows(const WView& w, int row0, int n_rows, int cols, float* out, hipStream_t s);
+hipError_t launch_gemv_f32(const float* w, const float* x, float* out, int rows, int cols, hipStream_t s);
+hipError_t launch_gemv_q8_0(const WView& w, const float* x, float* out, int rows, int cols, hipStream_t s);
+hipError_t launch_argmax_partial(const float* x, int n, float2* part, int nparts, hipStream_t s);
+hipError_t launch_argmax_final(const float2* part, int nparts, int* out_token, StepState* st, int* out_tokens,
+                               hipStream_t s);
+hipError_t launch_fill_f32(float* p, float v, size_t n, hipStream_t s);
+
+}  // namespace mcpm

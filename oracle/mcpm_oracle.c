@@ -181,19 +181,17 @@ void or_dequant_row(int type, const void *blocks, int n, float *out) {
 void or_q4k_block_lanes(const or_block_q4_K *w, const or_block_q8_K *a, int32_t isum[8], int32_t *minsum) {
     uint8_t sc[8], mn[8];
     or_q4k_scales_mins(w->scales, sc, mn);
-    for (int m = 0; m < 8; ++m) {
-        int32_t s = 0;
-        for (int j = 0; j < 4; ++j) {
-            int32_t lo = 0, hi = 0;
-            for (int l = 4 * m; l < 4 * m + 4; ++l) {
-                const uint8_t q = w->qs[32 * j + l];
-                lo += (int32_t)(q & 0x0f) * a->qs[64 * j + l];
-                hi += (int32_t)(q >> 4) * a->qs[64 * j + 32 + l];
-            }
-            s += (int32_t)sc[2 * j] * lo + (int32_t)sc[2 * j + 1] * hi;
+    /* Integer sums are exact, so they are formed per byte column l and folded
+     * into lane l/4 afterwards. */
+    int32_t col[32] = {0};
+    for (int j = 0; j < 4; ++j) {
+        const int32_t s_lo = sc[2 * j], s_hi = sc[2 * j + 1];
+        for (int l = 0; l < 32; ++l) {
+            const int32_t q = w->qs[32 * j + l];
+            col[l] += s_lo * (q & 0x0f) * a->qs[64 * j + l] + s_hi * (q >> 4) * a->qs[64 * j + 32 + l];
         }
-        isum[m] = s;
     }
+    for (int m = 0; m < 8; ++m) isum[m] = col[4 * m] + col[4 * m + 1] + col[4 * m + 2] + col[4 * m + 3];
     int32_t ms = 0;
     for (int g = 0; g < 8; ++g) ms += (int32_t)mn[g] * ((int32_t)a->bsums[2 * g] + (int32_t)a->bsums[2 * g + 1]);
     *minsum = ms;
@@ -205,21 +203,23 @@ void or_q4k_block_lanes(const or_block_q4_K *w, const or_block_q8_K *a, int32_t 
  * [0,63]; then minus 32*(bsums[2m]*sc[2m] + bsums[2m+1]*sc[2m+1]).
  */
 void or_q6k_block_lanes(const or_block_q6_K *w, const or_block_q8_K *a, int32_t isum[8]) {
-    for (int m = 0; m < 8; ++m) {
-        int32_t s = 0;
-        for (int h = 0; h < 2; ++h) {
-            for (int g = 0; g < 4; ++g) {
-                int32_t dot = 0;
-                for (int l = 4 * m; l < 4 * m + 4; ++l) {
-                    const int e = 128 * h + 32 * g + l;
-                    dot += (int32_t)q6_code(w, e) * a->qs[e];
-                }
-                s += (int32_t)w->scales[8 * h + 2 * g + (m >= 4)] * dot;
-            }
+    int32_t col[32] = {0};
+    for (int h = 0; h < 2; ++h) {
+        const uint8_t *ql = w->ql + 64 * h, *qh = w->qh + 32 * h;
+        const int8_t *x = a->qs + 128 * h;
+        for (int l = 0; l < 32; ++l) {
+            const int32_t H = qh[l], A0 = ql[l], A1 = ql[32 + l];
+            const int hi = l >= 16;
+            const int32_t q0 = (A0 & 15) | ((H & 3) << 4), q1 = (A1 & 15) | (((H >> 2) & 3) << 4);
+            const int32_t q2 = (A0 >> 4) | (((H >> 4) & 3) << 4), q3 = (A1 >> 4) | (((H >> 6) & 3) << 4);
+            col[l] += w->scales[8 * h + 0 + hi] * q0 * x[l] + w->scales[8 * h + 2 + hi] * q1 * x[32 + l] +
+                      w->scales[8 * h + 4 + hi] * q2 * x[64 + l] + w->scales[8 * h + 6 + hi] * q3 * x[96 + l];
         }
+    }
+    for (int m = 0; m < 8; ++m) {
         const int32_t off = (int32_t)a->bsums[2 * m] * w->scales[2 * m] +
                             (int32_t)a->bsums[2 * m + 1] * w->scales[2 * m + 1];
-        isum[m] = s - 32 * off;
+        isum[m] = col[4 * m] + col[4 * m + 1] + col[4 * m + 2] + col[4 * m + 3] - 32 * off;
     }
 }
 

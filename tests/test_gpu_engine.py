@@ -1,0 +1,179 @@
+"""The decode engine (GGUF load, KV cache, graph-captured forward, decode loops)
+against the CPU oracle and the reference's golden tokens."""
+import hashlib
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import mcpm
+import oracle as O
+from conftest import announce, assert_bits, golden
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layers=4, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1400, vocab=4000)
+
+
+@pytest.fixture(scope="module")
+def small_image():
+    g = golden("small_model_greedy.npz")
+    img = mcpm.synth_gguf(mcpm.make_config(**SMALL), seed=int(g["seed"]), mix=0)
+    assert hashlib.sha256(img.tobytes()).hexdigest() == str(g["image_sha"]), "model generator changed"
+    return img
+
+
+@pytest.fixture(scope="module")
+def small_engine(ctx, small_image):
+    e = mcpm.Engine(ctx, image=small_image)
+    e.init_kv_cache(256)
+    yield e
+    e.free()
+
+
+def test_config_from_gguf(small_engine):
+    c = small_engine.cfg
+    assert (c.n_layers, c.dim, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn, c.ffn_pad, c.vocab) == \
+        (4, 512, 8, 2, 64, 1400, 1536, 4000)
+    assert c.tied_embeddings == 1
+    assert abs(c.rope_base - 10000.0) < 1e-3
+
+
+def test_forward_logits_bit_exact(small_engine, small_image):
+    om = O.OracleModel(small_image)
+    om.init_kv(256)
+    rng = np.random.default_rng(11)
+    toks = rng.integers(0, 4000, 70)
+    want = np.empty(4000, np.float32)
+    for pos, t in enumerate(toks):
+        announce(f"small forward pos={pos}")
+        got, am = small_engine.forward(int(t), pos)
+        om.forward(int(t), pos, want)
+        assert_bits(got, want)
+        assert am == int(np.argmax(want))
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_greedy_matches_oracle_and_reference(small_engine, small_image, graph):
+    g = golden("small_model_greedy.npz")
+    small_engine.set_graph(graph)
+    announce(f"small greedy graph={graph}")
+    got = small_engine.generate_greedy(g["prompt"], len(g["tokens"]))
+    om = O.OracleModel(small_image)
+    want = om.generate_greedy(g["prompt"], len(g["tokens"]))
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(got, g["tokens"])  # the reference's own ops
+    small_engine.set_graph(True)
+
+
+def test_forward_context_errors(small_engine):
+    with pytest.raises(mcpm.McpmError) as ei:
+        small_engine.forward(1, 256)
+    assert ei.value.code == -4
+    with pytest.raises(mcpm.McpmError) as ei:
+        small_engine.forward(1, 10, max_seq_len=10)
+    assert ei.value.code == -4
+    with pytest.raises(mcpm.McpmError):
+        small_engine.forward(4000, 0)
+
+
+def test_load_from_file_and_errors(ctx, small_image):
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "m.gguf")
+        small_image.tofile(p)
+        e = mcpm.Engine(ctx, gguf_path=p)
+        assert e.cfg.n_layers == 4
+        e.free()
+        bad = os.path.join(d, "bad.gguf")
+        small_image[: len(small_image) // 2].tofile(bad)
+        with pytest.raises(mcpm.McpmError) as ei:
+            mcpm.Engine(ctx, gguf_path=bad)
+        assert ei.value.code == -6
+    with pytest.raises(mcpm.McpmError) as ei:
+        mcpm.Engine(ctx, gguf_path="/nonexistent/model.gguf")
+    assert ei.value.code == -5
+
+
+def test_sampled_matches_oracle_sampler(small_engine, small_image):
+    prompt = np.arange(10, 26, dtype=np.int32)
+    announce("small sampled T=0.8 top_p=0.95")
+    got = small_engine.generate_sampled(prompt, 24, 0.8, 0.95, 1234)
+    om = O.OracleModel(small_image)
+    om.init_kv(64)
+    orc = O.oracle()
+    gen = np.zeros(625, np.uint32)  # or_mt19937 state
+    orc.or_mt_seed(gen.ctypes.data, 1234)
+    lg = np.empty(4000, np.float32)
+    for p, t in enumerate(prompt):
+        om.forward(int(t), p, lg)
+    out = []
+    for i in range(24):
+        nxt = orc.or_sample(lg.ctypes.data, 4000, 0.8, 0.95, orc.or_mt_uniform01(gen.ctypes.data))
+        out.append(nxt)
+        if i < 23:
+            om.forward(nxt, len(prompt) + i, lg)
+    np.testing.assert_array_equal(got, np.array(out, np.int32))
+
+
+def test_kernel_timing_counts(small_engine):
+    small_engine.set_kernel_timing(mcpm.KC_GATE_UP)
+    small_engine.generate_greedy(np.array([1, 2, 3], np.int32), 2)
+    t, n = small_engine.kernel_time()
+    assert n == small_engine.cfg.n_layers and t > 0
+    small_engine.set_kernel_timing(-1)
+
+
+def _sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).view(np.uint8).tobytes()).hexdigest()
+
+
+def test_full_model_greedy_64(ctx):
+    """2.4B-shaped model (40 layers, 2304 hidden, 32/8 heads of 64, FFN 5760,
+    vocab 130560, tied Q6_K head, Q6_K v/down): the 32-token prompt and 64
+    greedy steps reproduce the CPU oracle bit for bit -- every step's logits
+    (SHA-256) and every token."""
+    g = golden("full_model_oracle.npz")
+    announce("full model synth")
+    img = mcpm.synth_gguf(mcpm.config_2p4b(), seed=int(g["seed"]), mix=0)
+    assert _sha(img) == str(g["image_sha"]), "model generator changed"
+    e = mcpm.Engine(ctx, image=img)
+    del img
+    e.init_kv_cache(128)
+    announce("full model greedy 32+64 (device loop)")
+    toks = e.generate_greedy(g["prompt"], 64)
+    np.testing.assert_array_equal(toks, g["tokens"])
+    announce("full model per-step logits")
+    prompt = [int(t) for t in g["prompt"]]
+    feed = prompt + [int(t) for t in g["tokens"][:-1]]
+    n_p = len(prompt)
+    for pos, t in enumerate(feed):
+        logits, am = e.forward(t, pos)
+        if pos >= n_p - 1:
+            step = pos - (n_p - 1)
+            assert _sha(logits) == str(g["logits_sha"][step]), f"logits differ at step {step}"
+            assert am == int(g["tokens"][step])
+    e.free()
+
+
+@pytest.mark.parametrize("name", ["refshape_1layer_greedy.npz", "refshape_3layer_greedy.npz"])
+def test_reference_geometry_tokens(ctx, name):
+    """The reference's own MiniCPM5-2B geometry (hidden 2048, 16/2 heads of
+    128, FFN 6144, rope base 5e6) at reduced depth: tokens equal the
+    reference's for as long as the oracle's do (all 64 steps for one layer),
+    and equal the oracle's for all 64 steps."""
+    g = golden(name)
+    L, D, NH, NKV, HD, F, V = [int(v) for v in g["config"]]
+    cfg = mcpm.make_config(L, D, NH, NKV, HD, F, V, rope_base=float(g["rope_base"]))
+    img = mcpm.synth_gguf(cfg, seed=int(g["seed"]), mix=0)
+    assert _sha(img) == str(g["image_sha"]), "model generator changed"
+    e = mcpm.Engine(ctx, image=img)
+    e.init_kv_cache(96)
+    n = len(g["tokens"])
+    announce(f"{name} greedy")
+    got = e.generate_greedy(g["prompt"], n)
+    k = int(g["oracle_agree_steps"])
+    np.testing.assert_array_equal(got[:k], g["tokens"][:k])
+    want = O.OracleModel(img).generate_greedy(g["prompt"], n)
+    np.testing.assert_array_equal(got, want)
+    e.free()
