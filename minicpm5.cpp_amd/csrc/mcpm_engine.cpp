@@ -208,6 +208,7 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
     GemvArgs a{};
     a.total_rows = c.vocab;
     a.nreg = 1;
+    a.nb = c.dim / QK_K;
     e->lm_grid = gemv_grid(a, ctx->n_cu);
     rc = alloc_dev(reinterpret_cast<void**>(&e->argmax_part), e->lm_grid * sizeof(float2));
   }

@@ -1,0 +1,819 @@
+// mcpm_gemv.hip -- the Q4_K / Q6_K x Q8_K GEMV family (QKV, O, gate/up, down,
+// LM head and the per-op entry points).
+//
+// Arithmetic.  A row dot is that of one AVX2 row (src/ops/ops_avx2.cpp:153-196
+// for Q4_K, 201-276 for Q6_K): per block, eight integer lane sums isum[m]
+// (lane m owns bytes 4m..4m+3 of every 32-byte chunk), then, blocks in order,
+//   acc[m] = fma(d_x*d_w, float(isum[m]), acc[m])
+//   Q4_K:  acc_min = fma(-(d_x*dmin_w), float(minsum), acc_min)
+//   row = ((acc0+acc4)+(acc2+acc6)) + ((acc1+acc5)+(acc3+acc7))  [+ acc_min]
+// Integer sums are exact, so how they are formed is free; the float chain is
+// the reference's.
+//
+// Work.  One GPU lane forms all eight isum of one (row, block) from the
+// block's bytes (a 16-byte load per chunk, consecutive lanes on consecutive
+// rows) and the Q8_K activations in LDS.  Two shapes:
+//   ROW   a lane owns one row, visits its blocks in order and keeps the float
+//         chain in registers; a wave covers 64 rows.
+//   TILE  a wave covers S rows ("slots") of all nb blocks: pair q = lane +
+//         64k (k < KB steps) is block q / S of slot q % S.  The lanes leave
+//         (isum[8], d_x*d_w, d_x*dmin_w, minsum) per (block, slot) in LDS,
+//         then 8 lanes per row run the chain over the blocks in order.
+// Each wave streams its (item, step) sequence through two register sets,
+// loading one step ahead.  Every load is unconditional: rows, blocks and
+// steps past the end are clamped into the tensor and their results masked.
+// Work groups share the activations (prologue) and nothing else.
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "mcpm_device.h"
+
+namespace mcpm {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+// A copy of a wave-uniform value in a scalar register, so the compiler knows
+// it is uniform across the wave.
+__device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Region reg's copy of a field, selected by value: a ?: over two lvalues is an
+// lvalue, i.e. a select of addresses and one load through it.
+template <typename T>
+__device__ __forceinline__ T pick(int reg, T a, T b, T c) {
+  return reg == 2 ? c : reg == 1 ? b : a;
+}
+#define MCPM_PICK(reg, A, B, C, f) pick((reg), (A).f, (B).f, (C).f)
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ------------------------------------------------------------- LDS plan ----
+// Dynamic LDS in dwords, by blocks per row nb:
+//   xs   [nb][68]  Q8_K quants of block b (64 dwords, native order) + pad
+//   xd   [nb]      Q8_K d
+//   xbp  [nb][4]   (bsums[4i]+bsums[4i+1], bsums[4i+2]+bsums[4i+3]) as i16 pairs
+//   xbs  [nb][16]  bsums as ints
+//   red  [260]     reduction scratch
+//   vrow [4][64]   TILE: row values of each wave's current item
+//   U              fp32 activations for the RMS partials (nb*256), later the
+//                  TILE chain areas (4 waves x nb*S*12)
+// Every region starts on a 16-byte boundary.
+struct LdsPlan {
+  int xs, xd, xbp, xbs, red, vrow, u, words;
+};
+
+__host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool norm) {
+  LdsPlan L;
+  L.xs = 0;
+  L.xd = nb * 68;
+  L.xbp = L.xd + ((nb + 3) & ~3);
+  L.xbs = L.xbp + nb * 4;
+  L.red = L.xbs + nb * 16;
+  L.vrow = L.red + 260;
+  L.u = L.vrow + (tile ? 4 * 64 : 0);
+  const int usz = std::max(norm ? nb * QK_K : 0, tile ? 4 * nb * S * 12 : 0);
+  L.words = L.u + usz;
+  return L;
+}
+
+// ------------------------------------------------------------- prologue ----
+// Each row of 16 lanes takes one block: block 16r + 4*wave + row (round r,
+// row = lane/16), lane j = lane%16 holding values 16j..16j+15 (one Q8_K bsum
+// group).  Blocks past nb re-read block nb-1 (in bounds, results unused).
+constexpr int NR = (MAX_NB + 15) / 16;
+
+struct ProRegs {
+  f32x4 x[NR][4];  // fp32 activations of the lane's 16 values
+  f32x4 g[NR][4];  // RMSNorm weights, same layout
+  u32x4 q[NR];     // Q8_K codes of the lane's 16 values
+  int bs[NR];      // Q8_K bsums[j]
+  float d[NR];     // Q8_K d
+};
+
+template <int PRO>
+__device__ __forceinline__ void prologue_load(const GemvArgs& a, int wave, int lane, ProRegs& X) {
+  const int nb = a.nb, row = lane >> 4, j = lane & 15;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (16 * r < nb) {  // uniform
+      const int b = min(16 * r + 4 * wave + row, nb - 1);
+      if constexpr (PRO == PRO_Q8K) {
+        const BlockQ8K* blk = a.xq + b;
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(blk->qs) + 4 * j;  // 4-byte aligned only
+        X.q[r] = u32x4{q[0], q[1], q[2], q[3]};
+        X.bs[r] = blk->bsums[j];
+        X.d[r] = blk->d;
+      } else {
+        const f32x4* xp = reinterpret_cast<const f32x4*>(a.x + b * QK_K + 16 * j);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X.x[r][i] = xp[i];
+        if constexpr (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN) {
+          const f32x4* gp = reinterpret_cast<const f32x4*>(a.gamma + b * QK_K + 16 * j);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) X.g[r][i] = gp[i];
+        }
+      }
+    }
+  }
+}
+
+// Block b (lane j of its row) into LDS: codes, d, bsums and the bsum pair
+// sums.  Every lane of the row takes part (lane moves); `live` gates stores.
+__device__ __forceinline__ void store_xblock(uint32_t* L, const LdsPlan& P, int b, int j, bool live, u32x4 q,
+                                             float d, int bs) {
+  // bsums[2g] + bsums[2g+1] on lane 2g; pairs (2i, 2i+1) on lane 4i
+  const int v = bs + dpp_i<DPP_XOR1>(bs);
+  const uint32_t w = (static_cast<uint32_t>(v) & 0xffffu) | (static_cast<uint32_t>(dpp_i<DPP_XOR2>(v)) << 16);
+  if (live) {
+    *reinterpret_cast<u32x4*>(L + P.xs + b * 68 + 4 * j) = q;
+    L[P.xbs + b * 16 + j] = static_cast<uint32_t>(bs);
+    if (j == 0) L[P.xd + b] = __float_as_uint(d);
+    if ((j & 3) == 0) L[P.xbp + b * 4 + (j >> 2)] = w;
+  }
+}
+
+// Q8_K activations of the work group into LDS: as given (PRO_Q8K), or
+// quantized from fp32 (ties-even or ties-away), optionally after RMSNorm
+// (src/ops/ops.cpp:676-723, 745-789).  Ends with a work-group barrier.
+template <int PRO>
+__device__ __forceinline__ void prologue_compute(const GemvArgs& a, int wave, int lane, const ProRegs& X,
+                                                 uint32_t* L, const LdsPlan& P) {
+  const int nb = a.nb, row = lane >> 4, j = lane & 15;
+  if constexpr (PRO == PRO_Q8K) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (16 * r < nb) {
+        const int b = 16 * r + 4 * wave + row;
+        store_xblock(L, P, min(b, nb - 1), j, b < nb, X.q[r], X.d[r], X.bs[r]);
+      }
+    }
+  } else {
+    constexpr bool norm = (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN);
+    constexpr bool away = (PRO == PRO_QUANT_AWAY || PRO == PRO_NORM_AWAY);
+    float rms = 1.0f;
+    if constexpr (norm) {
+      // thread t's partial runs over x[t], x[t+256], ... (multiply then add)
+      float* sx = reinterpret_cast<float*>(L + P.u);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int b = 16 * r + 4 * wave + row;
+        if (16 * r < nb && b < nb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) *reinterpret_cast<f32x4*>(&sx[b * QK_K + 16 * j + 4 * i]) = X.x[r][i];
+        }
+      }
+      __syncthreads();
+      const int tid = threadIdx.x;
+      float p = 0.0f;
+#pragma unroll 8
+      for (int jj = 0; jj < nb; ++jj) {
+        const float v = sx[jj * QK_K + tid];
+        p = p + v * v;
+      }
+      rms = block_rms_from_partials(p, nb * QK_K, a.eps, reinterpret_cast<float*>(L + P.red));
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (16 * r < nb) {  // uniform
+        const int b = 16 * r + 4 * wave + row;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[4 * i] = X.x[r][i].x;
+          v[4 * i + 1] = X.x[r][i].y;
+          v[4 * i + 2] = X.x[r][i].z;
+          v[4 * i + 3] = X.x[r][i].w;
+        }
+        if constexpr (norm) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[4 * i] = (v[4 * i] * rms) * X.g[r][i].x;
+            v[4 * i + 1] = (v[4 * i + 1] * rms) * X.g[r][i].y;
+            v[4 * i + 2] = (v[4 * i + 2] * rms) * X.g[r][i].z;
+            v[4 * i + 3] = (v[4 * i + 3] * rms) * X.g[r][i].w;
+          }
+        }
+        u32x4 packed;
+        float d;
+        int gsum;
+        quant_block_row16(v, away, packed, d, gsum);
+        store_xblock(L, P, min(b, nb - 1), j, b < nb, packed, d, gsum);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------- weight rows ----
+// Weight types a kernel instance handles: Q4_K only, Q6_K only, or both (per
+// region, e.g. a Q6_K attn_v beside Q4_K q and k).  A single-type instance
+// holds only its own block registers.
+enum { WT_Q4 = 0, WT_Q6 = 1, WT_MIX = 2 };
+struct Region {
+  const uint8_t* p0;
+  const uint8_t* p1;
+  const uint8_t* p2;
+  const uint8_t* p3;
+  float* out;
+  int rows;
+  int row0;  // first item of the region (region mode)
+  int type;
+};
+
+__device__ __forceinline__ Region region_of(const GemvRegion& g) {
+  return Region{g.w.p0, g.w.p1, g.w.p2, g.w.p3, g.out, g.rows, g.row0, g.w.type};
+}
+
+// One slot of a work item: region, row, and the row's position in each plane
+// (block 0, chunk 0).  Rows past the region's end point at its last row, so
+// every load stays inside the tensor; `valid` masks their results.
+struct RowRef {
+  const uint8_t* p0;
+  const uint8_t* p1;
+  const uint8_t* p2;
+  const uint8_t* p3;
+  float* out;
+  size_t rs;  // rows * 16: bytes between consecutive chunk planes
+  int reg;
+  int r;
+  bool valid;
+  bool q4;  // wave-uniform
+};
+
+template <int WT>
+__device__ __forceinline__ RowRef row_of(const GemvArgs& a, const Region& A, const Region& B, const Region& C,
+                                         int S, int item, int s) {
+  RowRef t;
+  int reg, r, rows;
+  if (a.pair) {
+    // slots 0..S/2-1 from region 0, the rest from region 1, same rows
+    const int half = S / 2;
+    reg = s < half ? 0 : 1;
+    r = item * half + (s < half ? s : s - half);
+    rows = a.total_rows;
+    t.q4 = A.type == MCPM_TYPE_Q4_K;  // both regions share the type
+  } else {
+    reg = 0;
+    if (a.nreg > 1 && item >= B.row0) reg = 1;
+    if (a.nreg > 2 && item >= C.row0) reg = 2;
+    r = (item - MCPM_PICK(reg, A, B, C, row0)) * S + s;
+    rows = MCPM_PICK(reg, A, B, C, rows);
+    t.q4 = MCPM_PICK(reg, A, B, C, type) == MCPM_TYPE_Q4_K;
+  }
+  if constexpr (WT != WT_MIX) t.q4 = (WT == WT_Q4);
+  t.valid = r < rows && s < S;
+  const size_t rr = static_cast<size_t>(min(r, rows - 1));
+  t.reg = reg;
+  t.r = r;
+  t.rs = static_cast<size_t>(rows) * 16;
+  t.p0 = MCPM_PICK(reg, A, B, C, p0) + rr * 16;
+  t.p1 = MCPM_PICK(reg, A, B, C, p1) + rr * 16;
+  t.p2 = MCPM_PICK(reg, A, B, C, p2) + rr * 16;
+  t.p3 = MCPM_PICK(reg, A, B, C, p3) + rr * 2;
+  t.out = MCPM_PICK(reg, A, B, C, out);
+  return t;
+}
+
+// One block of one row in registers.  Q4_K: w[0..7] quant chunks, w[8]
+// header.  Q6_K: w[0..7] ql chunks, w[8..11] qh chunks, w[12] scales, d.
+template <int WT>
+struct Blk {
+  u32x4 w[WT == WT_Q4 ? 9 : 13];
+  uint32_t d;
+};
+
+template <int WT>
+__device__ __forceinline__ void load_blk(Blk<WT>& K, const RowRef& t, int b) {
+  const size_t rs = t.rs;
+  if constexpr (WT == WT_Q4) {
+    const uint8_t* q = t.p0 + static_cast<size_t>(b) * 8 * rs;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) K.w[c] = ld_stream4(q + c * rs);
+    K.w[8] = ld_stream4(t.p1 + static_cast<size_t>(b) * rs);
+    return;
+  } else {
+  if (WT == WT_MIX && t.q4) {
+    const uint8_t* q = t.p0 + static_cast<size_t>(b) * 8 * rs;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) K.w[c] = ld_stream4(q + c * rs);
+    K.w[8] = ld_stream4(t.p1 + static_cast<size_t>(b) * rs);
+  } else {
+    const uint8_t* ql = t.p0 + static_cast<size_t>(b) * 8 * rs;
+    const uint8_t* qh = t.p1 + static_cast<size_t>(b) * 4 * rs;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) K.w[c] = ld_stream4(ql + c * rs);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) K.w[8 + c] = ld_stream4(qh + c * rs);
+    K.w[12] = ld_stream4(t.p2 + static_cast<size_t>(b) * rs);
+    K.d = ld_stream_u16(t.p3 + static_cast<size_t>(b) * (rs / 8));
+  }
+  }
+}
+
+// dword i of the vectors starting at w (i a compile-time constant after unrolling)
+__device__ __forceinline__ uint32_t dw(const u32x4* w, int i) {
+  const u32x4 v = w[i >> 2];
+  return (i & 3) == 0 ? v.x : (i & 3) == 1 ? v.y : (i & 3) == 2 ? v.z : v.w;
+}
+
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), 0, false);
+}
+
+// bytes k and k+1 of w as a pair of (zero-extended) 16-bit lanes
+__device__ __forceinline__ uint32_t byte_pair(uint32_t w, int k) {
+  return __builtin_amdgcn_perm(0u, w, 0x0c000c00u | (static_cast<uint32_t>(k + 1) << 16) | static_cast<uint32_t>(k));
+}
+
+__device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(i16x2, a), __builtin_bit_cast(i16x2, b), c, false);
+}
+
+// Eight lane sums of a Q4_K block against Q8_K block xs (64 dwords), and the
+// block's min sum over the 8 sub-blocks of mn_g*(bsums[2g]+bsums[2g+1]) (xbp:
+// those pair sums as i16 pairs).  Native quant dword 8j+m holds, per byte,
+// sub-block 2j (low nibble) and 2j+1 (high nibble) at positions 4m..4m+3.
+template <int WT>
+__device__ __forceinline__ void q4k_rowblock(const Blk<WT>& K, const uint32_t* __restrict__ xs,
+                                             const uint32_t* __restrict__ xbp, int (&is)[8], int& ms) {
+  const uint32_t s0 = K.w[8].y, s1 = K.w[8].z, s2 = K.w[8].w;
+  // scales (sc) and mins (mn) of sub-blocks 0..3 and 4..7, one per byte
+  const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+  const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+  const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+  const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+#pragma unroll
+  for (int m = 0; m < 8; ++m) is[m] = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t sw = (j < 2) ? sc_lo : sc_hi;
+    const int sce = (sw >> (16 * (j & 1))) & 0xff;      // sc[2j]
+    const int sco = (sw >> (16 * (j & 1) + 8)) & 0xff;  // sc[2j+1]
+    const u32x4 xe0 = *reinterpret_cast<const u32x4*>(xs + 16 * j);
+    const u32x4 xe1 = *reinterpret_cast<const u32x4*>(xs + 16 * j + 4);
+    const u32x4 xo0 = *reinterpret_cast<const u32x4*>(xs + 16 * j + 8);
+    const u32x4 xo1 = *reinterpret_cast<const u32x4*>(xs + 16 * j + 12);
+    const uint32_t xe[8] = {xe0.x, xe0.y, xe0.z, xe0.w, xe1.x, xe1.y, xe1.z, xe1.w};
+    const uint32_t xo[8] = {xo0.x, xo0.y, xo0.z, xo0.w, xo1.x, xo1.y, xo1.z, xo1.w};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const uint32_t q = dw(K.w, 8 * j + m);
+      is[m] = mad24(sce, dot4(q & 0x0f0f0f0fu, xe[m]), is[m]);
+      is[m] = mad24(sco, dot4((q >> 4) & 0x0f0f0f0fu, xo[m]), is[m]);
+    }
+  }
+  const u32x4 bp = *reinterpret_cast<const u32x4*>(xbp);
+  int v = dot2(byte_pair(mn_lo, 0), bp.x, 0);
+  v = dot2(byte_pair(mn_lo, 2), bp.y, v);
+  v = dot2(byte_pair(mn_hi, 0), bp.z, v);
+  ms = dot2(byte_pair(mn_hi, 2), bp.w, v);
+}
+
+// Eight lane sums of a Q6_K block (codes kept in [0, 63], the -32 applied as
+// 32*(bsums[2m]*sc[2m] + bsums[2m+1]*sc[2m+1])).  For half h and lane m:
+// ql dwords 16h+m, 16h+8+m, qh dword 8h+m, activations 32h+8g+m (g = 0..3),
+// scale 8h+2g+(m>=4).
+template <int WT>
+__device__ __forceinline__ void q6k_rowblock(const Blk<WT>& K, const uint32_t* __restrict__ xs,
+                                             const uint32_t* __restrict__ xbs, int (&is)[8]) {
+  int sc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    sc[i] = static_cast<int>(static_cast<int8_t>((dw(&K.w[12], i >> 2) >> (8 * (i & 3))) & 0xffu));
+#pragma unroll
+  for (int m = 0; m < 8; ++m) is[m] = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t xv[4][8];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const u32x4 x0 = *reinterpret_cast<const u32x4*>(xs + 32 * h + 8 * g);
+      const u32x4 x1 = *reinterpret_cast<const u32x4*>(xs + 32 * h + 8 * g + 4);
+      xv[g][0] = x0.x;
+      xv[g][1] = x0.y;
+      xv[g][2] = x0.z;
+      xv[g][3] = x0.w;
+      xv[g][4] = x1.x;
+      xv[g][5] = x1.y;
+      xv[g][6] = x1.z;
+      xv[g][7] = x1.w;
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int hi = (m >= 4) ? 1 : 0;
+      const uint32_t a0 = dw(K.w, 16 * h + m), a1 = dw(K.w, 16 * h + 8 + m), hb = dw(&K.w[8], 8 * h + m);
+      const uint32_t q0 = (a0 & 0x0f0f0f0fu) | ((hb << 4) & 0x30303030u);
+      const uint32_t q1 = (a1 & 0x0f0f0f0fu) | ((hb << 2) & 0x30303030u);
+      const uint32_t q2 = ((a0 >> 4) & 0x0f0f0f0fu) | (hb & 0x30303030u);
+      const uint32_t q3 = ((a1 >> 4) & 0x0f0f0f0fu) | ((hb >> 2) & 0x30303030u);
+      int v = is[m];
+      v = mad24(sc[8 * h + 0 + hi], dot4(q0, xv[0][m]), v);
+      v = mad24(sc[8 * h + 2 + hi], dot4(q1, xv[1][m]), v);
+      v = mad24(sc[8 * h + 4 + hi], dot4(q2, xv[2][m]), v);
+      v = mad24(sc[8 * h + 6 + hi], dot4(q3, xv[3][m]), v);
+      is[m] = v;
+    }
+  }
+  int bsv[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 t = *reinterpret_cast<const u32x4*>(xbs + 4 * i);
+    bsv[4 * i] = static_cast<int>(t.x);
+    bsv[4 * i + 1] = static_cast<int>(t.y);
+    bsv[4 * i + 2] = static_cast<int>(t.z);
+    bsv[4 * i + 3] = static_cast<int>(t.w);
+  }
+#pragma unroll
+  for (int m = 0; m < 8; ++m) is[m] -= 32 * mad24(bsv[2 * m], sc[2 * m], __mul24(bsv[2 * m + 1], sc[2 * m + 1]));
+}
+
+__device__ __forceinline__ float hsum8(const float (&acc)[8]) {
+  return ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+}
+
+// ---------------------------------------------------------------- kernel ---
+// TILE: S slots per item, KB steps per item.  ROW: S = 64, KB = nb.
+template <int PRO, int EPI, bool TILE, int WT>
+__global__ void __launch_bounds__(GEMV_THREADS) k_gemv(const GemvArgs a, int n_items, int S, int KB) {
+  extern __shared__ uint32_t L[];
+  const int lane = threadIdx.x & 63;
+  const int wave = sgpr(static_cast<int>(threadIdx.x >> 6));
+  const int nb = a.nb;
+  constexpr bool norm = (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN);
+  const LdsPlan P = lds_plan(nb, S, TILE, norm);
+  const int stride = gridDim.x * 4;
+  const Region A = region_of(a.reg[0]), B = region_of(a.reg[1]), C = region_of(a.reg[2]);
+
+  // This wave's steps: item first + (t / KB) * stride, step t % KB.  Steps
+  // past the last re-read the last one (cached, results unused), so every
+  // load is issued unconditionally and no wait depends on a branch.
+  const int first = blockIdx.x * 4 + wave;
+  const int n_mine = first < n_items ? (n_items - 1 - first) / stride + 1 : 0;
+  const int n_steps = n_mine * KB;
+  const float invS = 1.0f / static_cast<float>(S);
+
+  // slot and block of this lane at step k of an item
+  auto slot_at = [&](int k, int& s, int& b) {
+    if constexpr (TILE) {
+      const int q = lane + 64 * k;
+      const int bq = static_cast<int>((static_cast<float>(q) + 0.5f) * invS);  // q / S, exact for q < 2^16
+      s = q - bq * S;
+      b = bq;
+    } else {
+      s = lane;
+      b = k;
+    }
+  };
+  auto ref_at = [&](int t, int& b, int& s) {
+    const int tt = min(t, max(n_steps - 1, 0));
+    const int it = n_steps > 0 ? first + (tt / KB) * stride : 0;
+    slot_at(tt % KB, s, b);
+    return row_of<WT>(a, A, B, C, S, it, s);
+  };
+
+  // Epilogue inputs of the row this lane finishes (ROW: its row; TILE: slot
+  // `lane`), loaded with each step's weights so the epilogue reads no memory:
+  // the residual (RESID) or the RoPE cos/sin (QKV).  Every step loads them,
+  // at clamped indices, so no load depends on a branch.
+  const int pos = (EPI == EPI_QKV) ? a.state[1] : 0;
+  auto prefetch_epi = [&](int t, float2& e) {
+    const int tt = min(t, max(n_steps - 1, 0));
+    const int it = n_steps > 0 ? first + (tt / KB) * stride : 0;
+    const RowRef te = row_of<WT>(a, A, B, C, S, it, min(lane, S - 1));
+    if constexpr (EPI == EPI_RESID) {
+      e.x = a.resid[min(te.r, a.total_rows - 1)];
+    } else if constexpr (EPI == EPI_QKV) {
+      const int i = te.r % a.head_dim;
+      e = a.rope_cs[static_cast<size_t>(pos) * (a.head_dim / 2) + (i >> 1)];
+    }
+  };
+
+  ProRegs X;
+  prologue_load<PRO>(a, wave, lane, X);
+  Blk<WT> K0, K1;
+  float2 e0 = make_float2(0.0f, 0.0f), e1 = make_float2(0.0f, 0.0f);
+  int b0, s0, b1, s1;
+  RowRef t0 = ref_at(0, b0, s0), t1;
+  prefetch_epi(0, e0);
+  load_blk(K0, t0, min(b0, nb - 1));  // in flight during the prologue
+  prologue_compute<PRO>(a, wave, lane, X, L, P);
+
+  float acc[8], accm = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) acc[m] = 0.0f;
+  float best_v = -__builtin_inff();
+  int best_i = 0x7fffffff;
+  uint32_t* chain = L + P.u + wave * (nb * S * 12);  // TILE: entry (b, s) at (b*S + s)*12
+
+  // the epilogue for row value v of slot s of item `it`; lanes with s >= S
+  // or an invalid row only take part in the shuffles before it
+  auto epilogue = [&](int it, int s, float v, float partner, float up, float2 e) {
+    const RowRef t = row_of<WT>(a, A, B, C, S, it, min(s, S - 1));
+    const bool writer = s < S && t.valid;
+    const int r = t.r;
+    if constexpr (EPI == EPI_STORE) {
+      if (writer) t.out[r] = v;
+    } else if constexpr (EPI == EPI_RESID) {
+      if (writer) a.resid[r] = e.x + v;
+    } else if constexpr (EPI == EPI_SWIGLU) {
+      if (writer && s < S / 2) {
+        const float silu = v / (1.0f + exp_f32(-v));
+        a.h_out[r] = silu * up;
+      }
+    } else if constexpr (EPI == EPI_QKV) {
+      // adjacent-pair RoPE (src/ops/ops.cpp:502-516) on q (region 0) and k
+      // (region 1); k and v rows go to the KV cache at pos.
+      if (writer) {
+        if (t.reg < 2) {
+          const int i = r % a.head_dim;
+          const float2 cs = e;
+          float o;
+          if ((i & 1) == 0) o = v * cs.x - partner * cs.y;
+          else o = partner * cs.y + v * cs.x;
+          if (t.reg == 0) t.out[r] = o;
+          else a.k_cache[static_cast<size_t>(pos) * a.kvd + r] = o;
+        } else {
+          a.v_cache[static_cast<size_t>(pos) * a.kvd + r] = v;
+        }
+      }
+    } else if constexpr (EPI == EPI_LOGITS) {
+      if (writer) {
+        t.out[r] = v;
+        if (v > best_v || (v == best_v && r < best_i)) {
+          best_v = v;
+          best_i = r;
+        }
+      }
+    }
+  };
+
+  // integer work of one step, then the float chain (ROW) or its LDS entry
+  // (TILE); the item's last step finishes its rows
+  auto consume = [&](const Blk<WT>& Kb, float2 e, const RowRef& t, int t_idx, int b, int s) {
+    const int k = t_idx % KB;
+    const int it = first + (t_idx / KB) * stride;
+    const int bc = min(b, nb - 1);
+    int is[8], ms = 0;
+    float ds, dm = 0.0f;
+    const float xdv = __uint_as_float(L[P.xd + bc]);
+    if (WT == WT_Q4 || (WT == WT_MIX && t.q4)) {
+      q4k_rowblock(Kb, L + P.xs + bc * 68, L + P.xbp + bc * 4, is, ms);
+      ds = xdv * fp16_to_fp32(static_cast<uint16_t>(Kb.w[8].x & 0xffffu));
+      dm = xdv * fp16_to_fp32(static_cast<uint16_t>(Kb.w[8].x >> 16));
+    } else {
+      if constexpr (WT != WT_Q4) {
+        q6k_rowblock(Kb, L + P.xs + bc * 68, L + P.xbs + bc * 16, is);
+        ds = xdv * fp16_to_fp32(static_cast<uint16_t>(Kb.d & 0xffffu));
+      }
+    }
+    if constexpr (!TILE) {
+      if (k == 0) {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) acc[m] = 0.0f;
+        accm = 0.0f;
+      }
+#pragma unroll
+      for (int m = 0; m < 8; ++m) acc[m] = __builtin_fmaf(ds, static_cast<float>(is[m]), acc[m]);
+      accm = __builtin_fmaf(-dm, static_cast<float>(ms), accm);
+      if (k == KB - 1) {
+        float v = hsum8(acc);
+        if (t.q4) v = v + accm;
+        const float partner = __shfl(v, lane ^ 1);
+        const float up = __shfl(v, (lane + 32) & 63);
+        epilogue(it, lane, v, partner, up, e);
+      }
+    } else {
+      if (b < nb) {
+        u32x4* e = reinterpret_cast<u32x4*>(chain + (b * S + s) * 12);
+        e[0] = u32x4{static_cast<uint32_t>(is[0]), static_cast<uint32_t>(is[1]), static_cast<uint32_t>(is[2]),
+                     static_cast<uint32_t>(is[3])};
+        e[1] = u32x4{static_cast<uint32_t>(is[4]), static_cast<uint32_t>(is[5]), static_cast<uint32_t>(is[6]),
+                     static_cast<uint32_t>(is[7])};
+        e[2] = u32x4{__float_as_uint(ds), __float_as_uint(dm), static_cast<uint32_t>(ms), 0u};
+      }
+      if (k == KB - 1) {
+        wave_sync();
+        // 8 lanes per row (lane = 8*row + m, S/8 passes) run the chain; the
+        // row values go to vrow for the epilogue's RoPE and gate/up partners
+        const int m = lane & 7;
+        float* vrow = reinterpret_cast<float*>(L + P.vrow) + wave * 64;
+#pragma unroll 1
+        for (int pass = 0; pass * 8 < S; ++pass) {
+          const int sr = pass * 8 + (lane >> 3);
+          const int src = min(sr, S - 1);
+          float ac = 0.0f, am = 0.0f;
+#pragma unroll 4
+          for (int bb = 0; bb < nb; ++bb) {
+            const uint32_t* e = chain + (bb * S + src) * 12;
+            ac = __builtin_fmaf(__uint_as_float(e[8]), static_cast<float>(static_cast<int>(e[m])), ac);
+            am = __builtin_fmaf(-__uint_as_float(e[9]), static_cast<float>(static_cast<int>(e[10])), am);
+          }
+          float v = ac + __shfl_down(ac, 4);
+          v = v + __shfl_down(v, 2);
+          v = v + __shfl_down(v, 1);
+          if (t.q4) v = v + am;
+          if (m == 0 && sr < S) vrow[sr] = v;
+        }
+        wave_sync();
+        const int se = min(lane, S - 1);
+        const float v = vrow[se];
+        const float partner = vrow[(se ^ 1) < S ? (se ^ 1) : se];
+        const float up = vrow[(se + S / 2) % S];
+        wave_sync();  // every read of the chain area precedes the next item's entries
+        epilogue(it, lane, v, partner, up, e);
+      }
+    }
+  };
+
+  // two register sets used in turn: a copy between them would wait for the
+  // loads still landing in the source
+  for (int t = 0; t < n_steps; t += 2) {
+    t1 = ref_at(t + 1, b1, s1);
+    prefetch_epi(t + 1, e1);
+    load_blk(K1, t1, min(b1, nb - 1));
+    consume(K0, e0, t0, t, b0, s0);
+    if (t + 1 >= n_steps) break;
+    t0 = ref_at(t + 2, b0, s0);
+    prefetch_epi(t + 2, e0);
+    load_blk(K0, t0, min(b0, nb - 1));
+    consume(K1, e1, t1, t + 1, b1, s1);
+  }
+
+  if constexpr (EPI == EPI_LOGITS) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(best_v, o);
+      const int oi = __shfl_xor(best_i, o);
+      if (ov > best_v || (ov == best_v && oi < best_i)) {
+        best_v = ov;
+        best_i = oi;
+      }
+    }
+    if (lane == 0) a.argmax_part[blockIdx.x * 4 + wave] = make_float2(best_v, __int_as_float(best_i));
+  }
+}
+
+// ------------------------------------------------------------- dispatch ----
+
+namespace {
+
+struct Shape {
+  bool tile;
+  int S, KB;
+};
+
+int items_for(const GemvArgs& a, int S) {
+  if (a.pair) return (a.total_rows + S / 2 - 1) / (S / 2);
+  int n = 0;
+  for (int i = 0; i < a.nreg; ++i) n += (a.reg[i].rows + S - 1) / S;
+  return n;
+}
+
+// ROW when its 64-row items give every SIMD a wave.  Otherwise TILE, with
+// at most one 4-wave work group per CU: a second work group on a CU runs
+// mostly after the first (the oldest waves issue first), doubling the time of
+// that CU.  Among the (KB, S) whose items fit in 4*n_cu waves, the fewest
+// steps per wave, then the most items; if none fits, the fewest items.  S is
+// even where rows pair up (RoPE, gate/up), and S*nb <= 64*KB.
+// MCPM_GEMV_SHAPE="KB,S" overrides it and "0" forces ROW (a tuning aid for
+// measuring shapes against each other).
+Shape pick_shape(const GemvArgs& a, int epilogue, int n_cu) {
+  const int nb = a.nb;
+  const bool paired = a.pair || epilogue == EPI_QKV;
+  static const char* env = std::getenv("MCPM_GEMV_SHAPE");
+  if (env) {
+    const int kb = std::atoi(env);
+    const char* c = std::strchr(env, ',');
+    const int s = c ? std::atoi(c + 1) : 0;
+    if (kb == 0) return Shape{false, 64, nb};
+    if (kb > 0 && kb <= 4 && s >= 1 && s <= 64 && !(paired && s % 2) && s * nb <= 64 * kb)
+      return Shape{true, s, kb};
+  }
+  const int waves = 4 * n_cu;
+  if (items_for(a, 64) >= waves) return Shape{false, 64, nb};
+  Shape best{true, 0, 0};
+  int best_items = 0;
+  for (int kb = 1; kb <= 4 && best.S == 0; ++kb) {
+    for (int S = paired ? 2 : 1; S * nb <= 64 * kb && S <= 64; S += paired ? 2 : 1) {
+      const int items = items_for(a, S);
+      if (items <= waves && items > best_items) {
+        best = Shape{true, S, kb};
+        best_items = items;
+      }
+    }
+  }
+  if (best.S == 0) {  // nothing fits one round: the largest items
+    const int kb = 4, S = std::min(64, (64 * kb / nb) & (paired ? ~1 : ~0));
+    best = Shape{true, S, kb};
+  }
+  return best;
+}
+
+size_t lds_bytes(const GemvArgs& a, const Shape& sh, int prologue) {
+  const bool norm = (prologue == PRO_NORM_AWAY || prologue == PRO_NORM_EVEN);
+  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, norm).words) * 4;
+}
+
+template <int PRO, int EPI, bool TILE, int WT>
+int grid_for(int n_items, int n_cu, size_t lds) {
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_gemv<PRO, EPI, TILE, WT>),
+                                                   GEMV_THREADS, lds) != hipSuccess || occ < 1)
+    occ = 1;
+  // one resident round of work groups: more would queue behind the first
+  return std::min((n_items + 3) / 4, n_cu * occ);
+}
+
+// Items of the launch; in region mode also each region's first item.
+int n_items_of(GemvArgs& a, const Shape& sh) {
+  if (a.pair) return items_for(a, sh.S);
+  int n = 0;
+  for (int i = 0; i < a.nreg; ++i) {
+    a.reg[i].row0 = n;
+    n += (a.reg[i].rows + sh.S - 1) / sh.S;
+  }
+  return n;
+}
+
+template <int PRO, int EPI, bool TILE, int WT>
+hipError_t launch_one(const GemvArgs& a, int n_items, const Shape& sh, int n_cu, size_t lds, hipStream_t s) {
+  const int grid = grid_for<PRO, EPI, TILE, WT>(n_items, n_cu, lds);
+  if (grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL((k_gemv<PRO, EPI, TILE, WT>), dim3(grid), dim3(GEMV_THREADS), lds, s, a, n_items, sh.S, sh.KB);
+  return hipGetLastError();
+}
+
+// the weight types of the launch's regions
+int weight_kind(const GemvArgs& a) {
+  bool q4 = false, q6 = false;
+  for (int i = 0; i < a.nreg; ++i) (a.reg[i].w.type == MCPM_TYPE_Q4_K ? q4 : q6) = true;
+  return q4 && q6 ? WT_MIX : q4 ? WT_Q4 : WT_Q6;
+}
+
+template <int PRO, int EPI>
+hipError_t launch_pe(const GemvArgs& a0, const Shape& sh, int n_cu, hipStream_t s) {
+  GemvArgs a = a0;
+  const int n_items = n_items_of(a, sh);
+  const size_t lds = lds_bytes(a, sh, PRO);
+  const int wt = weight_kind(a);
+#define MCPM_WT(TT, WW) \
+  if (sh.tile == TT && wt == WW) return launch_one<PRO, EPI, TT, WW>(a, n_items, sh, n_cu, lds, s);
+  MCPM_WT(true, WT_Q4) MCPM_WT(true, WT_Q6) MCPM_WT(false, WT_Q4) MCPM_WT(false, WT_Q6)
+  if constexpr (EPI == EPI_QKV || EPI == EPI_STORE) {  // the QKV regions (fused, or the per-op entry)
+    MCPM_WT(true, WT_MIX) MCPM_WT(false, WT_MIX)
+  }
+#undef MCPM_WT
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+int gemv_grid(const GemvArgs& a0, int n_cu) {
+  // number of argmax partials the LM-head launch (PRO_NORM_EVEN, EPI_LOGITS)
+  // writes: 4 per work group
+  GemvArgs a = a0;
+  a.nreg = 1;
+  a.reg[0].rows = a.total_rows;
+  const Shape sh = pick_shape(a, EPI_LOGITS, n_cu);
+  const int n_items = n_items_of(a, sh);
+  const size_t lds = lds_bytes(a, sh, PRO_NORM_EVEN);
+  const bool q4 = weight_kind(a) == WT_Q4;
+  constexpr int P = PRO_NORM_EVEN, E = EPI_LOGITS;
+  const int grid = sh.tile ? (q4 ? grid_for<P, E, true, WT_Q4>(n_items, n_cu, lds)
+                                 : grid_for<P, E, true, WT_Q6>(n_items, n_cu, lds))
+                           : (q4 ? grid_for<P, E, false, WT_Q4>(n_items, n_cu, lds)
+                                 : grid_for<P, E, false, WT_Q6>(n_items, n_cu, lds));
+  return 4 * grid;
+}
+
+hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s) {
+  if (a.nb <= 0 || a.nb > MAX_NB) return hipErrorInvalidValue;
+  if (a.pair && a.reg[0].w.type != a.reg[1].w.type) return hipErrorInvalidValue;
+  GemvArgs b = a;
+  if (!b.pair && epilogue == EPI_LOGITS) {
+    b.nreg = 1;
+    b.reg[0].rows = b.total_rows;
+  }
+  const Shape sh = pick_shape(b, epilogue, n_cu);
+#define MCPM_PE(PP, EE) \
+  if (prologue == PP && epilogue == EE) return launch_pe<PP, EE>(b, sh, n_cu, s);
+  MCPM_PE(PRO_Q8K, EPI_STORE)
+  MCPM_PE(PRO_QUANT_EVEN, EPI_STORE)
+  MCPM_PE(PRO_QUANT_EVEN, EPI_RESID)
+  MCPM_PE(PRO_QUANT_AWAY, EPI_RESID)
+  MCPM_PE(PRO_NORM_AWAY, EPI_QKV)
+  MCPM_PE(PRO_NORM_AWAY, EPI_SWIGLU)
+  MCPM_PE(PRO_NORM_EVEN, EPI_LOGITS)
+  MCPM_PE(PRO_NORM_EVEN, EPI_STORE)
+#undef MCPM_PE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mcpm

@@ -2,6 +2,7 @@
 #include "mcpm_host.h"
 
 #include <cmath>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <vector>
@@ -42,45 +43,46 @@ void set_planes(DevTensor& t) {
   }
 }
 
-// Native row-major blocks -> block-column-major planes (see DevTensor).
+// Native row-major blocks <-> chunked planes (see DevTensor).  One routine
+// serves both directions: `to_dev` copies native -> image, else image -> native.
+static void repack_planes(int type, int64_t rows, int64_t cols, uint8_t* nat, uint8_t* img, bool to_dev) {
+  const int64_t nb = cols / type_block_elems(type);
+  const size_t R = static_cast<size_t>(rows), nblk = static_cast<size_t>(rows * nb);
+  auto mv = [&](uint8_t* native_bytes, uint8_t* image_bytes, size_t n) {
+    if (to_dev) std::memcpy(image_bytes, native_bytes, n);
+    else std::memcpy(native_bytes, image_bytes, n);
+  };
+  auto chunk = [&](uint8_t* plane, int nc, int64_t b, int c, int64_t r) {
+    return plane + ((static_cast<size_t>(b) * nc + c) * R + static_cast<size_t>(r)) * 16;
+  };
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t b = 0; b < nb; ++b) {
+      const size_t di = static_cast<size_t>(b) * R + static_cast<size_t>(r);
+      if (type == MCPM_TYPE_Q4_K) {
+        uint8_t* s = nat + (static_cast<size_t>(r * nb + b)) * sizeof(BlockQ4K);
+        for (int c = 0; c < 8; ++c) mv(s + offsetof(BlockQ4K, qs) + 16 * c, chunk(img, 8, b, c, r), 16);
+        mv(s, img + nblk * 128 + di * 16, 16);
+      } else if (type == MCPM_TYPE_Q6_K) {
+        uint8_t* s = nat + (static_cast<size_t>(r * nb + b)) * sizeof(BlockQ6K);
+        for (int c = 0; c < 8; ++c) mv(s + offsetof(BlockQ6K, ql) + 16 * c, chunk(img, 8, b, c, r), 16);
+        for (int c = 0; c < 4; ++c) mv(s + offsetof(BlockQ6K, qh) + 16 * c, chunk(img + nblk * 128, 4, b, c, r), 16);
+        mv(s + offsetof(BlockQ6K, scales), img + nblk * 192 + di * 16, 16);
+        mv(s + offsetof(BlockQ6K, d), img + nblk * 208 + di * 2, 2);
+      } else if (type == MCPM_TYPE_Q8_0) {
+        uint8_t* s = nat + (static_cast<size_t>(r * nb + b)) * sizeof(BlockQ8_0);
+        mv(s + offsetof(BlockQ8_0, qs), img + di * 32, 32);
+        mv(s + offsetof(BlockQ8_0, d), img + nblk * 32 + di * 2, 2);
+      }
+    }
+  }
+}
+
 void repack_to_device_image(int type, int64_t rows, int64_t cols, const uint8_t* nat, uint8_t* img) {
   if (type == MCPM_TYPE_F32) {
     std::memcpy(img, nat, static_cast<size_t>(rows * cols * 4));
     return;
   }
-  const int64_t nb = cols / type_block_elems(type);
-  const size_t nblk = static_cast<size_t>(rows * nb);
-  for (int64_t r = 0; r < rows; ++r) {
-    for (int64_t b = 0; b < nb; ++b) {
-      const size_t di = static_cast<size_t>(b * rows + r);
-      if (type == MCPM_TYPE_Q4_K) {
-        const BlockQ4K* s = reinterpret_cast<const BlockQ4K*>(nat) + r * nb + b;
-        uint32_t q[32];
-        std::memcpy(q, s->qs, 128);
-        uint32_t* dq = reinterpret_cast<uint32_t*>(img + di * 128);
-        for (int j = 0; j < 4; ++j)
-          for (int m = 0; m < 8; ++m) dq[m * 4 + j] = q[j * 8 + m];
-        std::memcpy(img + nblk * 128 + di * 16, s, 16);
-      } else if (type == MCPM_TYPE_Q6_K) {
-        const BlockQ6K* s = reinterpret_cast<const BlockQ6K*>(nat) + r * nb + b;
-        uint32_t ql[32], qh[16];
-        std::memcpy(ql, s->ql, 128);
-        std::memcpy(qh, s->qh, 64);
-        uint32_t* dql = reinterpret_cast<uint32_t*>(img + di * 128);
-        uint32_t* dqh = reinterpret_cast<uint32_t*>(img + nblk * 128 + di * 64);
-        for (int j = 0; j < 4; ++j)
-          for (int m = 0; m < 8; ++m) dql[m * 4 + j] = ql[j * 8 + m];
-        for (int h = 0; h < 2; ++h)
-          for (int m = 0; m < 8; ++m) dqh[m * 2 + h] = qh[h * 8 + m];
-        std::memcpy(img + nblk * 192 + di * 16, s->scales, 16);
-        std::memcpy(img + nblk * 208 + di * 2, &s->d, 2);
-      } else if (type == MCPM_TYPE_Q8_0) {
-        const BlockQ8_0* s = reinterpret_cast<const BlockQ8_0*>(nat) + r * nb + b;
-        std::memcpy(img + di * 32, s->qs, 32);
-        std::memcpy(img + nblk * 32 + di * 2, &s->d, 2);
-      }
-    }
-  }
+  repack_planes(type, rows, cols, const_cast<uint8_t*>(nat), img, true);
 }
 
 void repack_from_device_image(int type, int64_t rows, int64_t cols, const uint8_t* img, uint8_t* nat) {
@@ -88,39 +90,7 @@ void repack_from_device_image(int type, int64_t rows, int64_t cols, const uint8_
     std::memcpy(nat, img, static_cast<size_t>(rows * cols * 4));
     return;
   }
-  const int64_t nb = cols / type_block_elems(type);
-  const size_t nblk = static_cast<size_t>(rows * nb);
-  for (int64_t r = 0; r < rows; ++r) {
-    for (int64_t b = 0; b < nb; ++b) {
-      const size_t di = static_cast<size_t>(b * rows + r);
-      if (type == MCPM_TYPE_Q4_K) {
-        BlockQ4K* d = reinterpret_cast<BlockQ4K*>(nat) + r * nb + b;
-        const uint32_t* sq = reinterpret_cast<const uint32_t*>(img + di * 128);
-        uint32_t q[32];
-        for (int j = 0; j < 4; ++j)
-          for (int m = 0; m < 8; ++m) q[j * 8 + m] = sq[m * 4 + j];
-        std::memcpy(d, img + nblk * 128 + di * 16, 16);
-        std::memcpy(d->qs, q, 128);
-      } else if (type == MCPM_TYPE_Q6_K) {
-        BlockQ6K* d = reinterpret_cast<BlockQ6K*>(nat) + r * nb + b;
-        const uint32_t* sql = reinterpret_cast<const uint32_t*>(img + di * 128);
-        const uint32_t* sqh = reinterpret_cast<const uint32_t*>(img + nblk * 128 + di * 64);
-        uint32_t ql[32], qh[16];
-        for (int j = 0; j < 4; ++j)
-          for (int m = 0; m < 8; ++m) ql[j * 8 + m] = sql[m * 4 + j];
-        for (int h = 0; h < 2; ++h)
-          for (int m = 0; m < 8; ++m) qh[h * 8 + m] = sqh[m * 2 + h];
-        std::memcpy(d->ql, ql, 128);
-        std::memcpy(d->qh, qh, 64);
-        std::memcpy(d->scales, img + nblk * 192 + di * 16, 16);
-        std::memcpy(&d->d, img + nblk * 208 + di * 2, 2);
-      } else if (type == MCPM_TYPE_Q8_0) {
-        BlockQ8_0* d = reinterpret_cast<BlockQ8_0*>(nat) + r * nb + b;
-        std::memcpy(d->qs, img + di * 32, 32);
-        std::memcpy(&d->d, img + nblk * 32 + di * 2, 2);
-      }
-    }
-  }
+  repack_planes(type, rows, cols, nat, const_cast<uint8_t*>(img), false);
 }
 
 int upload_tensor(mcpm_ctx* ctx, const void* host, size_t bytes, int type, int64_t cols, int64_t rows,

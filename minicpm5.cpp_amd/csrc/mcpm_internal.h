@@ -90,18 +90,18 @@ __host__ __device__ inline float exp_f32(float x) {
   return __builtin_ldexpf(p, static_cast<int>(k));
 }
 
-// A weight matrix in HBM.  Blocks are stored block-column-major (block b of
-// row r at index b*rows + r) so the 8 rows a wave reads for one block column
-// are contiguous, and each block's bytes are split into planes:
-//   Q4_K  p0: 128 B quants per block, dword (j*8+m) moved to (m*4+j), so lane
-//             m of 8 reads its 16 B with one load;  p1: 16 B header (d, dmin,
-//             12 scale bytes) exactly as in the block.
-//   Q6_K  p0: 128 B ql, the same dword permutation;  p1: 64 B qh, dword
-//             (h*8+m) moved to (m*2+h);  p2: 16 B int8 scales;  p3: 2 B d.
-//   Q8_0  p0: 32 B quants;  p1: 2 B d.
+// A weight matrix in HBM.  Each block's bytes are split into planes, and a
+// plane is cut into 16-byte chunks stored chunk-major then row-major: chunk c
+// of block b of row r at ((b*nc + c)*rows + r)*16 (nc chunks per block), so
+// a load instruction over consecutive rows reads consecutive memory.
+//   Q4_K  p0: the 128 quant bytes, nc = 8;  p1: 16 B header (d, dmin, 12
+//             scale bytes) at (b*rows + r)*16.
+//   Q6_K  p0: 128 B ql, nc = 8;  p1: 64 B qh, nc = 4;  p2: 16 B int8 scales
+//             at (b*rows + r)*16;  p3: 2 B d at (b*rows + r)*2.
+//   Q8_0  p0: 32 B quants at (b*rows + r)*32;  p1: 2 B d at (b*rows + r)*2.
 //   F32   p0: row-major floats.
-// Bytes per block are unchanged (144 / 210 / 34), so dequantized values are
-// bit-identical to the GGUF blocks.
+// Chunks keep the block's native byte order and bytes per block are unchanged
+// (144 / 210 / 34), so dequantized values are bit-identical to the GGUF blocks.
 struct DevTensor {
   int type = -1;
   int64_t rows = 0, cols = 0;
