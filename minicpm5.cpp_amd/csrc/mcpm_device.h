@@ -8,6 +8,7 @@ namespace mcpm {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));  // native vectors: copies stay in registers
 
 __device__ __forceinline__ u32x4 ld_stream4(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

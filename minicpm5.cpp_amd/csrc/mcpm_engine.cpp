@@ -245,10 +245,10 @@ int ensure_staging(mcpm_engine* e, int n) {
   return MCPM_OK;
 }
 
-// Launch helper that brackets the launch with events when its class is timed.
+// Launch helper: when its class is timed, the launch records an event pair at
+// its kernel's start and end.
 template <class F>
 hipError_t timed(mcpm_engine* e, int kc, F&& launch) {
-  hipStream_t s = e->ctx->stream;
   if (kc != e->timing_class) return launch();
   if (e->events_used == e->events.size()) {
     TimedPair p;
@@ -258,9 +258,9 @@ hipError_t timed(mcpm_engine* e, int kc, F&& launch) {
     e->events.push_back(p);
   }
   TimedPair& p = e->events[e->events_used++];
-  hipError_t err = hipEventRecord(p.a, s);
-  if (err == hipSuccess) err = launch();
-  if (err == hipSuccess) err = hipEventRecord(p.b, s);
+  g_launch_timing = LaunchTiming{p.a, p.b};
+  const hipError_t err = launch();
+  g_launch_timing = LaunchTiming{};
   return err;
 }
 

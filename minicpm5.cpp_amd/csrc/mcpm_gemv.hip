@@ -31,7 +31,6 @@
 
 namespace mcpm {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x2 __attribute__((ext_vector_type(2)));
 
 // A copy of a wave-uniform value in a scalar register, so the compiler knows
@@ -746,7 +745,7 @@ template <int PRO, int EPI, bool TILE, int WT>
 hipError_t launch_one(const GemvArgs& a, int n_items, const Shape& sh, int n_cu, size_t lds, hipStream_t s) {
   const int grid = grid_for<PRO, EPI, TILE, WT>(n_items, n_cu, lds);
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((k_gemv<PRO, EPI, TILE, WT>), dim3(grid), dim3(GEMV_THREADS), lds, s, a, n_items, sh.S, sh.KB);
+  launch_kernel(k_gemv<PRO, EPI, TILE, WT>, dim3(grid), dim3(GEMV_THREADS), lds, s, a, n_items, sh.S, sh.KB);
   return hipGetLastError();
 }
 

@@ -9,6 +9,8 @@
 
 namespace mcpm {
 
+thread_local LaunchTiming g_launch_timing;
+
 namespace {
 thread_local std::string g_last_error;
 }

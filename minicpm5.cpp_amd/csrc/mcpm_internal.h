@@ -2,6 +2,7 @@
 // libmcpm_hip.so.  Not installed; the public surface is include/mcpm_hip.h.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -206,6 +207,25 @@ struct StepState {
 };
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s);
+
+// When `start` is set, the GEMV and attention launch helpers record these
+// events at their kernel's start and end (hipExtLaunchKernel), so the elapsed
+// time is the kernel's own duration.  Set around one launch by the engine's
+// per-class timing; launches are eager then.
+struct LaunchTiming {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+extern thread_local LaunchTiming g_launch_timing;
+
+template <typename K, typename... Args>
+void launch_kernel(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+  if (g_launch_timing.start)
+    hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), s, g_launch_timing.start,
+                          g_launch_timing.stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+}
 int gemv_grid(const GemvArgs& a, int n_cu);
 
 hipError_t launch_quantize_q8k(const float* x, const float* gamma, float eps, int dim, int mode, BlockQ8K* out,

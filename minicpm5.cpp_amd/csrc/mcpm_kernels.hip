@@ -138,23 +138,47 @@ hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc
 // and over the chunks, in order:
 //   m = max m_c; f_c = exp(m_c - m); Z = fma(z_c, f_c, Z); O_i = fma(o_c[i], f_c, O_i)
 //   out_i = O_i / Z
-// Up to ATTN_CPW chunks one split does it all and keeps o_c in registers.
-// Longer contexts use splits of ATTN_SPLIT_CHUNKS chunks that write
-// (m_c, z_c, o_c) to `part` ([n_heads][max_chunks][2 + head_dim] floats); the
-// last split of a kv head to finish (a counter per kv head, reset by that
-// split) combines them.  Every load of a chunk's K and V rows is issued at
-// once, one chunk ahead, and the rows are staged through LDS.
+// A split takes ceil(nch/16) consecutive chunks (at most ATTN_CPW), keeping
+// o_c in registers, so a kv head has at most 16 splits (up to 16*ATTN_CPW
+// chunks).  With one split it writes the output itself; otherwise the splits
+// write (m_c, z_c, o_c) to `part` ([n_heads][max_chunks][2 + head_dim] floats)
+// and the last split of a kv head to finish (a counter per kv head, reset by
+// that split) combines them.  Every load of a chunk's K and V rows is issued
+// at once, one chunk ahead, and the rows are staged through LDS.
 constexpr int ATTN_MAX_GROUP = 8;
 constexpr int ATTN_CPW = 8;
-constexpr int ATTN_SPLIT_CHUNKS = 4;
+constexpr int ATTN_MAX_SPLITS = 16;
 
-__host__ __device__ inline int attn_chunks_per_split(int nch) { return nch <= ATTN_CPW ? nch : ATTN_SPLIT_CHUNKS; }
+__host__ __device__ inline int attn_chunks_per_split(int nch) {
+  const int c = (nch + ATTN_MAX_SPLITS - 1) / ATTN_MAX_SPLITS;
+  return c < 1 ? 1 : (c > ATTN_CPW ? ATTN_CPW : c);
+}
 __host__ __device__ inline int attn_splits(int nch) {
   const int cps = attn_chunks_per_split(nch);
-  return cps > 0 ? (nch + cps - 1) / cps : 0;
+  return (nch + cps - 1) / cps;
 }
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));  // a native vector: copies stay in registers
+// Maximum over the wave (order-free): lane moves within rows of 16, then
+// across rows.
+__device__ __forceinline__ float wave_max_fast(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// wave_tree_sum with the same pairwise order (lane t += lane t+s for s =
+// 32..1; lane 0 holds the total): s = 32, 16 across rows, s <= 8 by DPP row
+// shifts (only lanes < s read, and those stay inside their row).
+__device__ __forceinline__ float wave_tree_sum_fast(float v) {
+  v = v + __shfl_down(v, 32);
+  v = v + __shfl_down(v, 16);
+  v = v + dpp_f<0x108>(v);  // row_shl:8
+  v = v + dpp_f<0x104>(v);  // row_shl:4
+  v = v + dpp_f<0x102>(v);  // row_shl:2
+  v = v + dpp_f<0x101>(v);  // row_shl:1
+  return v;
+}
 
 template <int NV>
 struct AttnRegs {
@@ -259,9 +283,9 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
         }
         const bool present = c * ATTN_CHUNK + lane < T;
         const float sv = present ? dot * scale : -1e9f;
-        const float mc = fmaxf(wave_max(sv), -1e9f);
+        const float mc = fmaxf(wave_max_fast(sv), -1e9f);
         const float e = present ? exp_f32(sv - mc) : 0.0f;
-        const float z = wave_tree_sum(e);
+        const float z = wave_tree_sum_fast(e);
         sE[hh * ATTN_CHUNK + lane] = e;
         if (lane == 0) sMZ[cc * ATTN_MAX_GROUP + hh] = make_float2(mc, z);
       }
@@ -385,11 +409,11 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, co
     return hipErrorInvalidValue;
   const dim3 grid(n_kv_heads, attn_splits(max_chunks));
   if (head_dim <= 64)
-    hipLaunchKernelGGL(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
-                       max_chunks, part, counters, out);
+    launch_kernel(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
+                  max_chunks, part, counters, out);
   else
-    hipLaunchKernelGGL(k_attention<128>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
-                       max_chunks, part, counters, out);
+    launch_kernel(k_attention<128>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
+                  max_chunks, part, counters, out);
   return hipGetLastError();
 }
 

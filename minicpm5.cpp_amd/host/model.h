@@ -1,0 +1,41 @@
+// model.h -- MiniCPM5Engine (include/model.h:37-45) served by the HIP engine:
+// the weights and the KV cache live in HBM, the per-token forward runs as one
+// graph replay, and forward() returns the logits in host memory like the
+// reference.  generate_greedy() is the device-side loop for callers that need
+// only token ids (no logits copy per token).
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "mcpm_hip.h"
+
+class MiniCPM5Engine {
+public:
+    MiniCPM5Engine();
+    ~MiniCPM5Engine();
+    MiniCPM5Engine(const MiniCPM5Engine&) = delete;
+    MiniCPM5Engine& operator=(const MiniCPM5Engine&) = delete;
+
+    void init_kv_cache(int max_seq_len);
+    bool load_model(const std::string& gguf_path, bool verbose = false);
+    // Logits of the token at position pos; the reference stays valid until
+    // the next call.  Past the KV capacity it warns and returns the previous
+    // logits (the reference's execute_attention warns and continues).
+    const std::vector<float>& forward(int token_id, int pos, int max_seq_len);
+
+    // Feeds prompt at positions 0.., then returns n_gen greedy tokens.
+    std::vector<int> generate_greedy(const std::vector<int>& prompt, int n_gen);
+    // A synthetic model image (seeded random weights, BASELINE shapes).
+    bool load_synthetic(const mcpm_model_config& cfg, uint64_t seed, int mix, bool verbose = false);
+    const mcpm_model_config& config() const { return cfg_; }
+
+private:
+    bool finish_load(int rc, bool verbose);
+
+    mcpm_ctx* ctx_ = nullptr;
+    mcpm_engine* engine_ = nullptr;
+    mcpm_model_config cfg_{};
+    int kv_capacity_ = 0;
+    std::vector<float> logits_;
+};

@@ -1,0 +1,141 @@
+"""The C++ mirror of the reference's host interfaces (minicpm5.cpp_amd/host/):
+ops.h functions and MiniCPM5Engine, driven from C++ programs and compared with
+the CPU oracle.  Bar: bit-identical to the oracle, as the C ABI they wrap."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import mcpm
+from conftest import P, announce
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CHECK = os.path.join(ROOT, "tests", "cpp", "ops_wrapper_check")
+DECODE = os.path.join(ROOT, "minicpm5.cpp_amd", "mcpm_decode")
+SEED = 99  # tests/cpp/ops_wrapper_check.cpp
+COLS = 512
+
+
+def test_programs_built_and_usage():
+    """Both programs exist and reject bad usage before touching a GPU."""
+    for path in (CHECK, DECODE):
+        assert os.access(path, os.X_OK), f"{path} not built (make -C minicpm5.cpp_amd host; make -C tests/cpp)"
+    assert subprocess.run([DECODE, "--help"], capture_output=True).returncode == 0
+    assert subprocess.run([DECODE, "--synth", "1", "--prompt-ids", "1,x"], capture_output=True).returncode == 2
+    assert subprocess.run([CHECK], capture_output=True).returncode == 2
+
+
+def _records(path):
+    out = {}
+    with open(path, "rb") as f:
+        data = f.read()
+    i = 0
+    while i < len(data):
+        n = int.from_bytes(data[i:i + 4], "little")
+        name = data[i + 4:i + 4 + n].decode()
+        i += 4 + n
+        nb = int.from_bytes(data[i:i + 8], "little")
+        out[name] = np.frombuffer(data[i + 8:i + 8 + nb], np.uint8).copy()
+        i += 8 + nb
+    return out
+
+
+def _normal(tid, n, mean=0.0, sd=1.0):
+    return mcpm.synth_normal(SEED, tid, n, mean, sd)
+
+
+def _weight(tid, gtype, rows, cols=COLS):
+    w = _normal(tid, rows * cols, 0.0, 0.02).reshape(rows, cols)
+    return w if gtype == mcpm.TYPE_F32 else mcpm.quantize_rows(gtype, w)
+
+
+def _f32(rec):
+    return rec.view(np.float32)
+
+
+@pytest.mark.gpu
+def test_ops_mirror_matches_oracle(orc, tmp_path):
+    out = str(tmp_path / "ops.bin")
+    announce("ops_wrapper_check")
+    r = subprocess.run([CHECK, out], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    got = _records(out)
+
+    x, gamma = _normal(5, COLS), _normal(6, COLS, 1.0, 0.1)
+    g, u = _normal(7, COLS), _normal(8, COLS)
+    want = np.empty(300, np.float32)
+    for name, gtype, tid in [("matmul_q4k", mcpm.TYPE_Q4_K, 1), ("matmul_q6k", mcpm.TYPE_Q6_K, 2),
+                             ("matmul_q8_0", mcpm.TYPE_Q8_0, 3)]:
+        orc.or_matmul(gtype, P(_weight(tid, gtype, 300)), P(x), P(want), 300, COLS)
+        np.testing.assert_array_equal(_f32(got[name]), want, err_msg=name)
+    wf = np.ascontiguousarray(_weight(4, mcpm.TYPE_F32, 40))
+    want40 = np.empty(40, np.float32)
+    orc.or_matmul(mcpm.TYPE_F32, P(wf), P(x), P(want40), 40, COLS)
+    np.testing.assert_array_equal(_f32(got["matmul_f32"]), want40)
+    np.testing.assert_array_equal(_f32(got["matmul_unsupported"]), np.full(300, 0.001, np.float32))
+
+    xq = np.zeros(COLS // 256 * 292, np.uint8)
+    orc.or_quantize_row_q8_K(P(x), COLS, P(xq), 0)
+    np.testing.assert_array_equal(got["quantize_row_q8_K"], xq)
+    for name, gtype, tid in [("matmul_q8k_q4k", mcpm.TYPE_Q4_K, 1), ("matmul_q8k_q6k", mcpm.TYPE_Q6_K, 2)]:
+        orc.or_matmul_q8k(gtype, P(_weight(tid, gtype, 300)), P(xq), P(want), 300, COLS)
+        np.testing.assert_array_equal(_f32(got[name]), want, err_msg=name)
+
+    q, k, v = np.empty(256, np.float32), np.empty(64, np.float32), np.empty(64, np.float32)
+    orc.or_gemv_qkv_q8_K(P(_weight(9, mcpm.TYPE_Q4_K, 256)), P(_weight(10, mcpm.TYPE_Q4_K, 64)),
+                         P(_weight(11, mcpm.TYPE_Q6_K, 64)), mcpm.TYPE_Q6_K, P(xq), P(q), P(k), P(v), 256, 64, COLS)
+    for name, arr in [("qkv_q", q), ("qkv_k", k), ("qkv_v", v)]:
+        np.testing.assert_array_equal(_f32(got[name]), arr, err_msg=name)
+    gate, up = np.empty(300, np.float32), np.empty(300, np.float32)
+    orc.or_gemv_gate_up_q4_K_q8_K(P(_weight(12, mcpm.TYPE_Q4_K, 300)), P(_weight(13, mcpm.TYPE_Q4_K, 300)), P(xq),
+                                  P(gate), P(up), 300, COLS)
+    np.testing.assert_array_equal(_f32(got["gate"]), gate)
+    np.testing.assert_array_equal(_f32(got["up"]), up)
+
+    rn = np.empty(COLS, np.float32)
+    orc.or_rmsnorm(P(rn), P(x), P(gamma), COLS, np.float32(1e-6))
+    np.testing.assert_array_equal(_f32(got["rmsnorm"]), rn)
+    nq = np.zeros_like(xq)
+    orc.or_rmsnorm_and_quantize_q8k(P(nq), P(x), P(gamma), COLS, np.float32(1e-6))
+    np.testing.assert_array_equal(got["rmsnorm_and_quantize_q8k"], nq)
+    sq = np.zeros_like(xq)
+    orc.or_swiglu_and_quantize_q8k(P(sq), P(g), P(u), COLS)
+    np.testing.assert_array_equal(got["swiglu_and_quantize_q8k"], sq)
+
+    rv = _normal(14, 4 * 64)
+    orc.or_apply_rope(P(rv[128:]), 17, 1, 64, np.float32(10000.0))  # head 2 only
+    np.testing.assert_array_equal(_f32(got["apply_rope"]), rv)
+
+    pos, max_seq, nh, nkv, hd = 70, 96, 8, 2, 64
+    kc_all, vc_all = _normal(18, max_seq * nkv * hd), _normal(19, max_seq * nkv * hd)
+    aq, kc, vc = _normal(15, nh * hd), _normal(16, nkv * hd), _normal(17, nkv * hd)
+    att = np.empty(nh * hd, np.float32)
+    assert orc.or_attention(P(att), P(aq), P(kc), P(vc), P(kc_all), P(vc_all), pos, max_seq, nh, nkv, hd) == 0
+    np.testing.assert_array_equal(_f32(got["attention"]), att)
+    np.testing.assert_array_equal(_f32(got["attention_kcache_row"]), kc)
+
+    emb = np.empty(COLS, np.float32)
+    orc.or_get_embedding(P(emb), mcpm.TYPE_Q6_K, P(_weight(20, mcpm.TYPE_Q6_K, 50)), COLS, 5)
+    np.testing.assert_array_equal(_f32(got["embedding"]), emb)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("device_loop", [False, True])
+def test_engine_mirror_greedy_matches_oracle(device_loop):
+    import oracle as O
+    cfg = mcpm.make_config(2, 2304, 32, 8, 64, 5760, 4096)
+    seed, prompt, n_gen = 7, [5, 1000, 77, 4095, 12], 12
+    announce(f"mcpm_decode device_loop={device_loop}")
+    cmd = [DECODE, "--synth", str(seed), "--layers", "2", "--vocab", "4096",
+           "--prompt-ids", ",".join(map(str, prompt)), "--tokens", str(n_gen)]
+    if device_loop:
+        cmd.append("--device-loop")
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    line = next(l for l in r.stdout.splitlines() if l.startswith("tokens:"))
+    got = [int(t) for t in line.split()[1:]]
+    om = O.OracleModel(mcpm.synth_gguf(cfg, seed=seed, mix=0))
+    want = om.generate_greedy(prompt, n_gen)
+    om.close()
+    assert got == list(want)
