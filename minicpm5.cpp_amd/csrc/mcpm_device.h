@@ -118,10 +118,12 @@ __device__ __forceinline__ void quant_block_row16(const float (&v)[16], bool awa
 }
 
 // 1/sqrt(sum/dim + eps) where sum is the 256-slot pairwise tree (slot t +=
-// slot t+s for s = 128..1) over the threads' partials p; every thread gets it.
+// slot t+s for s = 128..1) over the partials p of threads 0..255; every
+// thread of the work group (at least 256) gets it.
+// Threads 256 and up (in larger work groups) take no slot.
 __device__ __forceinline__ float block_rms_from_partials(float p, int dim, float eps, float* s_red) {
   const int tid = threadIdx.x;
-  s_red[tid] = p;
+  if (tid < 256) s_red[tid] = p;
   __syncthreads();
   if (tid < 128) s_red[tid] = s_red[tid] + s_red[tid + 128];
   __syncthreads();

@@ -25,6 +25,7 @@
 // Work groups share the activations (prologue) and nothing else.
 #include <algorithm>
 #include <cstdlib>
+#include <cstdio>
 #include <cstring>
 
 #include "mcpm_device.h"
@@ -58,15 +59,15 @@ __device__ __forceinline__ void wave_sync() {
 //   xbp  [nb][4]   (bsums[4i]+bsums[4i+1], bsums[4i+2]+bsums[4i+3]) as i16 pairs
 //   xbs  [nb][16]  bsums as ints
 //   red  [260]     reduction scratch
-//   vrow [4][64]   TILE: row values of each wave's current item
+//   vrow [NW][64]  TILE: row values of each wave's current item
 //   U              fp32 activations for the RMS partials (nb*256), later the
-//                  TILE chain areas (4 waves x nb*S*12)
+//                  TILE chain areas (NW waves x nb*S*12)
 // Every region starts on a 16-byte boundary.
 struct LdsPlan {
   int xs, xd, xbp, xbs, red, vrow, u, words;
 };
 
-__host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool norm) {
+__host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool norm, int NW) {
   LdsPlan L;
   L.xs = 0;
   L.xd = nb * 68;
@@ -74,16 +75,17 @@ __host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool norm)
   L.xbs = L.xbp + nb * 4;
   L.red = L.xbs + nb * 16;
   L.vrow = L.red + 260;
-  L.u = L.vrow + (tile ? 4 * 64 : 0);
-  const int usz = std::max(norm ? nb * QK_K : 0, tile ? 4 * nb * S * 12 : 0);
+  L.u = L.vrow + (tile ? NW * 64 : 0);
+  const int usz = std::max(norm ? nb * QK_K : 0, tile ? NW * nb * S * 12 : 0);
   L.words = L.u + usz;
   return L;
 }
 
 // ------------------------------------------------------------- prologue ----
-// Each row of 16 lanes takes one block: block 16r + 4*wave + row (round r,
-// row = lane/16), lane j = lane%16 holding values 16j..16j+15 (one Q8_K bsum
-// group).  Blocks past nb re-read block nb-1 (in bounds, results unused).
+// Each row of 16 lanes takes one block: block 4*NW*r + 4*wave + row (round r,
+// row = lane/16, NW >= 4 waves), lane j = lane%16 holding values 16j..16j+15
+// (one Q8_K bsum group).  Blocks past nb re-read block nb-1 (in bounds,
+// results unused).
 constexpr int NR = (MAX_NB + 15) / 16;
 
 struct ProRegs {
@@ -95,12 +97,12 @@ struct ProRegs {
 };
 
 template <int PRO>
-__device__ __forceinline__ void prologue_load(const GemvArgs& a, int wave, int lane, ProRegs& X) {
+__device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wave, int lane, ProRegs& X) {
   const int nb = a.nb, row = lane >> 4, j = lane & 15;
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
-    if (16 * r < nb) {  // uniform
-      const int b = min(16 * r + 4 * wave + row, nb - 1);
+    if (4 * NW * r < nb) {  // uniform
+      const int b = min(4 * NW * r + 4 * wave + row, nb - 1);
       if constexpr (PRO == PRO_Q8K) {
         const BlockQ8K* blk = a.xq + b;
         const uint32_t* q = reinterpret_cast<const uint32_t*>(blk->qs) + 4 * j;  // 4-byte aligned only
@@ -140,14 +142,14 @@ __device__ __forceinline__ void store_xblock(uint32_t* L, const LdsPlan& P, int 
 // quantized from fp32 (ties-even or ties-away), optionally after RMSNorm
 // (src/ops/ops.cpp:676-723, 745-789).  Ends with a work-group barrier.
 template <int PRO>
-__device__ __forceinline__ void prologue_compute(const GemvArgs& a, int wave, int lane, const ProRegs& X,
+__device__ __forceinline__ void prologue_compute(const GemvArgs& a, int NW, int wave, int lane, const ProRegs& X,
                                                  uint32_t* L, const LdsPlan& P) {
   const int nb = a.nb, row = lane >> 4, j = lane & 15;
   if constexpr (PRO == PRO_Q8K) {
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (16 * r < nb) {
-        const int b = 16 * r + 4 * wave + row;
+      if (4 * NW * r < nb) {
+        const int b = 4 * NW * r + 4 * wave + row;
         store_xblock(L, P, min(b, nb - 1), j, b < nb, X.q[r], X.d[r], X.bs[r]);
       }
     }
@@ -160,14 +162,14 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, int wave, in
       float* sx = reinterpret_cast<float*>(L + P.u);
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        const int b = 16 * r + 4 * wave + row;
-        if (16 * r < nb && b < nb) {
+        const int b = 4 * NW * r + 4 * wave + row;
+        if (4 * NW * r < nb && b < nb) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) *reinterpret_cast<f32x4*>(&sx[b * QK_K + 16 * j + 4 * i]) = X.x[r][i];
         }
       }
       __syncthreads();
-      const int tid = threadIdx.x;
+      const int tid = min(static_cast<int>(threadIdx.x), QK_K - 1);  // partial slots 0..255
       float p = 0.0f;
 #pragma unroll 8
       for (int jj = 0; jj < nb; ++jj) {
@@ -178,8 +180,8 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, int wave, in
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (16 * r < nb) {  // uniform
-        const int b = 16 * r + 4 * wave + row;
+      if (4 * NW * r < nb) {  // uniform
+        const int b = 4 * NW * r + 4 * wave + row;
         float v[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -440,20 +442,21 @@ __device__ __forceinline__ float hsum8(const float (&acc)[8]) {
 // ---------------------------------------------------------------- kernel ---
 // TILE: S slots per item, KB steps per item.  ROW: S = 64, KB = nb.
 template <int PRO, int EPI, bool TILE, int WT>
-__global__ void __launch_bounds__(GEMV_THREADS) k_gemv(const GemvArgs a, int n_items, int S, int KB) {
+__global__ void __launch_bounds__(64 * GEMV_MAX_WAVES) k_gemv(const GemvArgs a, int n_items, int S, int KB) {
   extern __shared__ uint32_t L[];
   const int lane = threadIdx.x & 63;
   const int wave = sgpr(static_cast<int>(threadIdx.x >> 6));
+  const int NW = static_cast<int>(blockDim.x >> 6);  // 4..8 waves
   const int nb = a.nb;
   constexpr bool norm = (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN);
-  const LdsPlan P = lds_plan(nb, S, TILE, norm);
-  const int stride = gridDim.x * 4;
+  const LdsPlan P = lds_plan(nb, S, TILE, norm, NW);
+  const int stride = gridDim.x * NW;
   const Region A = region_of(a.reg[0]), B = region_of(a.reg[1]), C = region_of(a.reg[2]);
 
   // This wave's steps: item first + (t / KB) * stride, step t % KB.  Steps
   // past the last re-read the last one (cached, results unused), so every
   // load is issued unconditionally and no wait depends on a branch.
-  const int first = blockIdx.x * 4 + wave;
+  const int first = blockIdx.x * NW + wave;
   const int n_mine = first < n_items ? (n_items - 1 - first) / stride + 1 : 0;
   const int n_steps = n_mine * KB;
   const float invS = 1.0f / static_cast<float>(S);
@@ -495,14 +498,14 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(const GemvArgs a, int n_i
   };
 
   ProRegs X;
-  prologue_load<PRO>(a, wave, lane, X);
+  prologue_load<PRO>(a, NW, wave, lane, X);
   Blk<WT> K0, K1;
   float2 e0 = make_float2(0.0f, 0.0f), e1 = make_float2(0.0f, 0.0f);
   int b0, s0, b1, s1;
   RowRef t0 = ref_at(0, b0, s0), t1;
   prefetch_epi(0, e0);
   load_blk(K0, t0, min(b0, nb - 1));  // in flight during the prologue
-  prologue_compute<PRO>(a, wave, lane, X, L, P);
+  prologue_compute<PRO>(a, NW, wave, lane, X, L, P);
 
   float acc[8], accm = 0.0f;
 #pragma unroll
@@ -655,7 +658,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(const GemvArgs a, int n_i
         best_i = oi;
       }
     }
-    if (lane == 0) a.argmax_part[blockIdx.x * 4 + wave] = make_float2(best_v, __int_as_float(best_i));
+    if (lane == 0) a.argmax_part[blockIdx.x * NW + wave] = make_float2(best_v, __int_as_float(best_i));
   }
 }
 
@@ -666,6 +669,7 @@ namespace {
 struct Shape {
   bool tile;
   int S, KB;
+  int NW;  // waves per work group
 };
 
 int items_for(const GemvArgs& a, int S) {
@@ -675,59 +679,71 @@ int items_for(const GemvArgs& a, int S) {
   return n;
 }
 
-// ROW when its 64-row items give every SIMD a wave.  Otherwise TILE, with
-// at most one 4-wave work group per CU: a second work group on a CU runs
-// mostly after the first (the oldest waves issue first), doubling the time of
-// that CU.  Among the (KB, S) whose items fit in 4*n_cu waves, the fewest
-// steps per wave, then the most items; if none fits, the fewest items.  S is
-// even where rows pair up (RoPE, gate/up), and S*nb <= 64*KB.
-// MCPM_GEMV_SHAPE="KB,S" overrides it and "0" forces ROW (a tuning aid for
-// measuring shapes against each other).
-Shape pick_shape(const GemvArgs& a, int epilogue, int n_cu) {
+// ROW: one work group per CU holding ceil(items / n_cu) waves (4..8), so
+// every CU gets the same load (a second work group on some CUs only would run
+// mostly after the first there, the oldest waves issuing first).
+int waves_for(int items, int n_cu) { return std::min(GEMV_MAX_WAVES, std::max(4, (items + n_cu - 1) / n_cu)); }
+
+// ROW when its 64-row items give every SIMD a wave.  Otherwise TILE with one
+// wave per SIMD (4 per work group, at most one work group per CU): a second
+// wave on a SIMD only adds its instructions to the first's, since a step's
+// time is its integer work.  The fewest steps per item (KB) whose items fit
+// 4*n_cu waves, then S a multiple of 4 (a step's rows of one block are 64-byte
+// runs of each chunk plane), then the smallest S (least work per wave).  S is
+// even where rows pair up (RoPE, gate/up) and S*nb <= 64*KB.
+//
+// MCPM_GEMV_SHAPE_<QKV|OPROJ|GATE_UP|DOWN|LM|OTHER>="KB,S,NW" (KB 0: ROW)
+// overrides the choice for one class of launch: a tuning aid for measuring
+// shapes against each other.
+const char* shape_env(int prologue, int epilogue) {
+  const char* name = "MCPM_GEMV_SHAPE_OTHER";
+  if (epilogue == EPI_QKV) name = "MCPM_GEMV_SHAPE_QKV";
+  else if (epilogue == EPI_SWIGLU) name = "MCPM_GEMV_SHAPE_GATE_UP";
+  else if (epilogue == EPI_LOGITS) name = "MCPM_GEMV_SHAPE_LM";
+  else if (epilogue == EPI_RESID) name = prologue == PRO_QUANT_AWAY ? "MCPM_GEMV_SHAPE_DOWN" : "MCPM_GEMV_SHAPE_OPROJ";
+  return std::getenv(name);
+}
+
+Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
   const int nb = a.nb;
   const bool paired = a.pair || epilogue == EPI_QKV;
-  static const char* env = std::getenv("MCPM_GEMV_SHAPE");
-  if (env) {
-    const int kb = std::atoi(env);
-    const char* c = std::strchr(env, ',');
-    const int s = c ? std::atoi(c + 1) : 0;
-    if (kb == 0) return Shape{false, 64, nb};
-    if (kb > 0 && kb <= 4 && s >= 1 && s <= 64 && !(paired && s % 2) && s * nb <= 64 * kb)
-      return Shape{true, s, kb};
-  }
-  const int waves = 4 * n_cu;
-  if (items_for(a, 64) >= waves) return Shape{false, 64, nb};
-  Shape best{true, 0, 0};
-  int best_items = 0;
-  for (int kb = 1; kb <= 4 && best.S == 0; ++kb) {
-    for (int S = paired ? 2 : 1; S * nb <= 64 * kb && S <= 64; S += paired ? 2 : 1) {
-      const int items = items_for(a, S);
-      if (items <= waves && items > best_items) {
-        best = Shape{true, S, kb};
-        best_items = items;
-      }
+  if (const char* env = shape_env(prologue, epilogue)) {
+    int kb = -1, s = 0, nw = 4;
+    if (std::sscanf(env, "%d,%d,%d", &kb, &s, &nw) >= 1 && nw >= 4 && nw <= GEMV_MAX_WAVES) {
+      if (kb == 0) return Shape{false, 64, nb, nw};
+      if (kb > 0 && kb <= 4 && s >= 1 && s <= 64 && !(paired && s % 2) && s * nb <= 64 * kb)
+        return Shape{true, s, kb, nw};
     }
   }
-  if (best.S == 0) {  // nothing fits one round: the largest items
-    const int kb = 4, S = std::min(64, (64 * kb / nb) & (paired ? ~1 : ~0));
-    best = Shape{true, S, kb};
+  const int cap = 4 * n_cu;
+  const int row_items = items_for(a, 64);
+  if (row_items >= cap) return Shape{false, 64, nb, waves_for(row_items, n_cu)};
+  for (int kb = 1; kb <= 4; ++kb) {
+    Shape best{true, 0, kb, 4};
+    for (int S = paired ? 2 : 1; S * nb <= 64 * kb && S <= 64; S += paired ? 2 : 1) {
+      if (items_for(a, S) > cap) continue;
+      if (best.S == 0 || (S % 4 == 0 && best.S % 4 != 0)) best.S = S;
+    }
+    if (best.S) return best;
   }
-  return best;
+  // nothing fits: the largest items, waves looping over them
+  const int S = std::min(64, (256 / nb) & (paired ? ~1 : ~0));
+  return Shape{true, std::max(S, paired ? 2 : 1), 4, GEMV_MAX_WAVES};
 }
 
 size_t lds_bytes(const GemvArgs& a, const Shape& sh, int prologue) {
   const bool norm = (prologue == PRO_NORM_AWAY || prologue == PRO_NORM_EVEN);
-  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, norm).words) * 4;
+  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, norm, sh.NW).words) * 4;
 }
 
 template <int PRO, int EPI, bool TILE, int WT>
-int grid_for(int n_items, int n_cu, size_t lds) {
+int grid_for(int n_items, const Shape& sh, int n_cu, size_t lds) {
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_gemv<PRO, EPI, TILE, WT>),
-                                                   GEMV_THREADS, lds) != hipSuccess || occ < 1)
+                                                   64 * sh.NW, lds) != hipSuccess || occ < 1)
     occ = 1;
   // one resident round of work groups: more would queue behind the first
-  return std::min((n_items + 3) / 4, n_cu * occ);
+  return std::min((n_items + sh.NW - 1) / sh.NW, n_cu * occ);
 }
 
 // Items of the launch; in region mode also each region's first item.
@@ -743,9 +759,9 @@ int n_items_of(GemvArgs& a, const Shape& sh) {
 
 template <int PRO, int EPI, bool TILE, int WT>
 hipError_t launch_one(const GemvArgs& a, int n_items, const Shape& sh, int n_cu, size_t lds, hipStream_t s) {
-  const int grid = grid_for<PRO, EPI, TILE, WT>(n_items, n_cu, lds);
+  const int grid = grid_for<PRO, EPI, TILE, WT>(n_items, sh, n_cu, lds);
   if (grid <= 0) return hipSuccess;
-  launch_kernel(k_gemv<PRO, EPI, TILE, WT>, dim3(grid), dim3(GEMV_THREADS), lds, s, a, n_items, sh.S, sh.KB);
+  launch_kernel(k_gemv<PRO, EPI, TILE, WT>, dim3(grid), dim3(64 * sh.NW), lds, s, a, n_items, sh.S, sh.KB);
   return hipGetLastError();
 }
 
@@ -776,20 +792,20 @@ hipError_t launch_pe(const GemvArgs& a0, const Shape& sh, int n_cu, hipStream_t 
 
 int gemv_grid(const GemvArgs& a0, int n_cu) {
   // number of argmax partials the LM-head launch (PRO_NORM_EVEN, EPI_LOGITS)
-  // writes: 4 per work group
+  // writes: one per wave
   GemvArgs a = a0;
   a.nreg = 1;
   a.reg[0].rows = a.total_rows;
-  const Shape sh = pick_shape(a, EPI_LOGITS, n_cu);
+  const Shape sh = pick_shape(a, PRO_NORM_EVEN, EPI_LOGITS, n_cu);
   const int n_items = n_items_of(a, sh);
   const size_t lds = lds_bytes(a, sh, PRO_NORM_EVEN);
   const bool q4 = weight_kind(a) == WT_Q4;
   constexpr int P = PRO_NORM_EVEN, E = EPI_LOGITS;
-  const int grid = sh.tile ? (q4 ? grid_for<P, E, true, WT_Q4>(n_items, n_cu, lds)
-                                 : grid_for<P, E, true, WT_Q6>(n_items, n_cu, lds))
-                           : (q4 ? grid_for<P, E, false, WT_Q4>(n_items, n_cu, lds)
-                                 : grid_for<P, E, false, WT_Q6>(n_items, n_cu, lds));
-  return 4 * grid;
+  const int grid = sh.tile ? (q4 ? grid_for<P, E, true, WT_Q4>(n_items, sh, n_cu, lds)
+                                 : grid_for<P, E, true, WT_Q6>(n_items, sh, n_cu, lds))
+                           : (q4 ? grid_for<P, E, false, WT_Q4>(n_items, sh, n_cu, lds)
+                                 : grid_for<P, E, false, WT_Q6>(n_items, sh, n_cu, lds));
+  return grid * sh.NW;
 }
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s) {
@@ -800,7 +816,7 @@ hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, 
     b.nreg = 1;
     b.reg[0].rows = b.total_rows;
   }
-  const Shape sh = pick_shape(b, epilogue, n_cu);
+  const Shape sh = pick_shape(b, prologue, epilogue, n_cu);
 #define MCPM_PE(PP, EE) \
   if (prologue == PP && epilogue == EE) return launch_pe<PP, EE>(b, sh, n_cu, s);
   MCPM_PE(PRO_Q8K, EPI_STORE)
