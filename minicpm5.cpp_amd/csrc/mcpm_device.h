@@ -107,7 +107,10 @@ __device__ __forceinline__ void quant_block_row16(const float (&v)[16], bool awa
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const float t = v[i] * mul;
-    float r = away ? roundf(t) : rintf(t);
+    // ties away: t + copysign(0.5 - 2^-25, t) truncates to roundf(t) for every
+    // |t| < 128 (|t| <= 127 here), so the clamp and the truncating conversion
+    // finish both roundings
+    float r = away ? t + __builtin_copysignf(0.49999997f, t) : rintf(t);
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     const int q = static_cast<int>(r);
     s += q;
@@ -115,6 +118,32 @@ __device__ __forceinline__ void quant_block_row16(const float (&v)[16], bool awa
   }
   packed = u32x4{w[0], w[1], w[2], w[3]};
   gsum = s;
+}
+
+// wave_tree_sum with the same pairwise order (lane t += lane t+s for s =
+// 32..1; lane 0 holds the total): s = 32, 16 across rows, s <= 8 by DPP row
+// shifts (only lanes < s read, and those stay inside their row).
+__device__ __forceinline__ float wave_tree_sum_fast(float v) {
+  v = v + __shfl_down(v, 32);
+  v = v + __shfl_down(v, 16);
+  v = v + dpp_f<0x108>(v);  // row_shl:8
+  v = v + dpp_f<0x104>(v);  // row_shl:4
+  v = v + dpp_f<0x102>(v);  // row_shl:2
+  v = v + dpp_f<0x101>(v);  // row_shl:1
+  return v;
+}
+
+// block_rms_from_partials with one barrier: every wave runs the tree over the
+// 256 slots itself (slots l, l+64, l+128, l+192 on lane l, then the wave tree),
+// so no second barrier hands the result out.  Same sums in the same order.
+__device__ __forceinline__ float block_rms_1sync(float p, int dim, float eps, float* s_red) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 256) s_red[tid] = p;
+  __syncthreads();
+  float v = (s_red[lane] + s_red[lane + 128]) + (s_red[lane + 64] + s_red[lane + 192]);
+  v = wave_tree_sum_fast(v);
+  v = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+  return 1.0f / sqrtf(v / static_cast<float>(dim) + eps);
 }
 
 // 1/sqrt(sum/dim + eps) where sum is the 256-slot pairwise tree (slot t +=

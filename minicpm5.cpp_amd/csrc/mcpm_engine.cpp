@@ -59,7 +59,7 @@ struct mcpm_engine {
   int max_chunks = 0;
   float2* rope = nullptr;
   float* attn_part = nullptr;
-  unsigned* attn_cnt = nullptr;
+  bool attn_fused = false;  // the O-projection's prologue combines the attention partials
   // graph
   bool use_graph = true;
   hipGraphExec_t graph = nullptr;
@@ -103,7 +103,7 @@ void free_engine(mcpm_engine* e) {
                   static_cast<void*>(e->h), static_cast<void*>(e->logits), static_cast<void*>(e->argmax_part),
                   static_cast<void*>(e->st), static_cast<void*>(e->out_tokens), static_cast<void*>(e->kc),
                   static_cast<void*>(e->vc), static_cast<void*>(e->rope), static_cast<void*>(e->attn_part),
-                  static_cast<void*>(e->attn_cnt)})
+                  })
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
   delete e;
@@ -169,6 +169,7 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
   auto* e = new mcpm_engine();
   e->ctx = ctx;
   e->cfg = c;
+  e->attn_fused = (qd / QK_K) % 4 == 0 && qd / QK_K <= 16 && c.head_dim % (qd / QK_K) == 0;
   int rc = MCPM_OK;
   int64_t wb = 0;
   auto T = [&](const std::string& n) { return f.find(n); };
@@ -213,7 +214,6 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
     rc = alloc_dev(reinterpret_cast<void**>(&e->argmax_part), e->lm_grid * sizeof(float2));
   }
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->st), sizeof(StepState));
-  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->attn_cnt), 256 * sizeof(unsigned));
   if (rc) {
     free_engine(e);
     return rc;
@@ -295,19 +295,31 @@ int enqueue_token(mcpm_engine* e) {
       a.kvd = kvd;
       MCPM_HIP(timed(e, MCPM_KC_QKV, [&] { return launch_gemv(a, PRO_NORM_AWAY, EPI_QKV, n_cu, s); }));
     }
+    const AttnPart part = attn_part_of(e->attn_part, c.n_heads, e->max_chunks, c.head_dim);
     MCPM_HIP(timed(e, MCPM_KC_ATTN, [&] {
-      return launch_attention(e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, e->attn_part,
-                              e->attn_cnt, e->att, s);
+      return launch_attention(e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part, s);
     }));
     {
+      // the attention output is combined from its chunk partials in this
+      // GEMV's prologue where the shape allows, else by its own kernel
       GemvArgs a{};
       a.reg[0] = GemvRegion{view_of(L.wo), nullptr, 0, c.dim};
       a.nreg = 1;
       a.total_rows = c.dim;
       a.nb = qd / QK_K;
-      a.x = e->att;
       a.resid = e->x;
-      MCPM_HIP(timed(e, MCPM_KC_OPROJ, [&] { return launch_gemv(a, PRO_QUANT_EVEN, EPI_RESID, n_cu, s); }));
+      if (e->attn_fused) {
+        a.x = part.o;
+        a.attn_mz = part.mz;
+        a.attn_max_chunks = e->max_chunks;
+        a.head_dim = c.head_dim;
+        a.state = st;
+        MCPM_HIP(timed(e, MCPM_KC_OPROJ, [&] { return launch_gemv(a, PRO_ATTN_EVEN, EPI_RESID, n_cu, s); }));
+      } else {
+        MCPM_HIP(launch_attn_combine(part, st, c.n_heads, c.head_dim, e->max_chunks, e->att, s));
+        a.x = e->att;
+        MCPM_HIP(timed(e, MCPM_KC_OPROJ, [&] { return launch_gemv(a, PRO_QUANT_EVEN, EPI_RESID, n_cu, s); }));
+      }
     }
     {
       GemvArgs a{};

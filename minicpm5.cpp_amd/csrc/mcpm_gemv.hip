@@ -18,7 +18,7 @@
 //   TILE  a wave covers S rows ("slots") of all nb blocks: pair q = lane +
 //         64k (k < KB steps) is block q / S of slot q % S.  The lanes leave
 //         (isum[8], d_x*d_w, d_x*dmin_w, minsum) per (block, slot) in LDS,
-//         then 8 lanes per row run the chain over the blocks in order.
+//         then 4 lanes per row run the chain over the blocks in order.
 // Each wave streams its (item, step) sequence through two register sets,
 // loading one step ahead.  Every load is unconditional: rows, blocks and
 // steps past the end are clamped into the tensor and their results masked.
@@ -60,14 +60,14 @@ __device__ __forceinline__ void wave_sync() {
 //   xbs  [nb][16]  bsums as ints
 //   red  [260]     reduction scratch
 //   vrow [NW][64]  TILE: row values of each wave's current item
-//   U              fp32 activations for the RMS partials (nb*256), later the
-//                  TILE chain areas (NW waves x nb*S*12)
+//   U              PRO_ATTN_EVEN: the combined fp32 activations (nb*256),
+//                  later the TILE chain areas (NW waves x nb*S*12)
 // Every region starts on a 16-byte boundary.
 struct LdsPlan {
   int xs, xd, xbp, xbs, red, vrow, u, words;
 };
 
-__host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool norm, int NW) {
+__host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool attn, int NW) {
   LdsPlan L;
   L.xs = 0;
   L.xd = nb * 68;
@@ -76,8 +76,8 @@ __host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool norm,
   L.red = L.xbs + nb * 16;
   L.vrow = L.red + 260;
   L.u = L.vrow + (tile ? NW * 64 : 0);
-  const int usz = std::max(norm ? nb * QK_K : 0, tile ? NW * nb * S * 12 : 0);
-  L.words = L.u + usz;
+  const int usz = tile ? NW * nb * S * 12 : 0;
+  L.words = L.u + (attn && nb * QK_K > usz ? nb * QK_K : usz);
   return L;
 }
 
@@ -88,9 +88,17 @@ __host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool norm,
 // results unused).
 constexpr int NR = (MAX_NB + 15) / 16;
 
+// PRO_ATTN_EVEN: thread t < 256 combines values t*nb .. t*nb+nb-1 (one head:
+// head_dim % nb == 0, nb <= 16) over the chunks, ATTN_RB chunks' o_c per load
+// batch, the (m_c, z_c) of the first ATTN_MZ chunks loaded with the first.
+constexpr int ATTN_RB = 4, ATTN_MZ = 8, ATTN_MAX_NB = 16;
+
 struct ProRegs {
   f32x4 x[NR][4];  // fp32 activations of the lane's 16 values
   f32x4 g[NR][4];  // RMSNorm weights, same layout
+  float xp[MAX_NB];  // RMSNorm: x[t], x[t+256], ... of thread t < 256 (its partial's terms)
+  f32x4 ao[ATTN_RB][4];  // PRO_ATTN_EVEN: o_c of thread t's nb values, chunks 0..ATTN_RB-1
+  float2 amz[ATTN_MZ];   // (m_c, z_c) of its head, chunks 0..ATTN_MZ-1
   u32x4 q[NR];     // Q8_K codes of the lane's 16 values
   int bs[NR];      // Q8_K bsums[j]
   float d[NR];     // Q8_K d
@@ -103,7 +111,9 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
   for (int r = 0; r < NR; ++r) {
     if (4 * NW * r < nb) {  // uniform
       const int b = min(4 * NW * r + 4 * wave + row, nb - 1);
-      if constexpr (PRO == PRO_Q8K) {
+      if constexpr (PRO == PRO_ATTN_EVEN) {
+        // the activations are formed in LDS by prologue_compute
+      } else if constexpr (PRO == PRO_Q8K) {
         const BlockQ8K* blk = a.xq + b;
         const uint32_t* q = reinterpret_cast<const uint32_t*>(blk->qs) + 4 * j;  // 4-byte aligned only
         X.q[r] = u32x4{q[0], q[1], q[2], q[3]};
@@ -118,6 +128,36 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
 #pragma unroll
           for (int i = 0; i < 4; ++i) X.g[r][i] = gp[i];
         }
+      }
+    }
+  }
+  if constexpr (PRO == PRO_ATTN_EVEN) {
+    const int t = min(static_cast<int>(threadIdx.x), QK_K - 1);
+    const int hd = a.head_dim, maxc = a.attn_max_chunks, nv4 = nb >> 2;
+    const int i0 = t * nb, h = i0 / hd, d0 = i0 - h * hd;
+    const int last = a.state[1] / ATTN_CHUNK;  // chunks 0..last
+    const float2* mz = a.attn_mz + static_cast<size_t>(h) * maxc;
+    // only the chunks present and the thread's own vectors (uniform branches)
+#pragma unroll
+    for (int c = 0; c < ATTN_MZ; ++c)
+      if (c <= last) X.amz[c] = mz[c];
+#pragma unroll
+    for (int c = 0; c < ATTN_RB; ++c) {
+      if (c <= last) {
+        const f32x4* o = reinterpret_cast<const f32x4*>(a.x + (static_cast<size_t>(h) * maxc + c) * hd + d0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (v < nv4) X.ao[c][v] = o[v];
+      }
+    }
+  }
+  if constexpr (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN) {
+    const int t = min(static_cast<int>(threadIdx.x), QK_K - 1);
+#pragma unroll
+    for (int g = 0; g < MAX_NB / 8; ++g) {
+      if (8 * g < nb) {  // uniform
+#pragma unroll
+        for (int k = 0; k < 8; ++k) X.xp[8 * g + k] = a.x[min(8 * g + k, nb - 1) * QK_K + t];
       }
     }
   }
@@ -138,6 +178,72 @@ __device__ __forceinline__ void store_xblock(uint32_t* L, const LdsPlan& P, int 
   }
 }
 
+// PRO_ATTN_EVEN: the attention output x[i] of threads' values (head h, dim
+// d) from the chunk partials, in chunk order (k_attn_combine's arithmetic):
+// m = max m_c; f_c = exp(m_c - m); Z = fma(z_c, f_c, Z); O = fma(o_c[d], f_c, O);
+// x = O / Z, into sx (fp32, nb*256), then a work-group barrier.
+__device__ __forceinline__ void attn_combine(const GemvArgs& a, const ProRegs& X, float* sx) {
+  const int nb = a.nb, hd = a.head_dim, maxc = a.attn_max_chunks, nv4 = nb >> 2;
+  const int t = min(static_cast<int>(threadIdx.x), QK_K - 1);
+  const int i0 = t * nb, h = i0 / hd, d0 = i0 - h * hd;
+  const int nch = a.state[1] / ATTN_CHUNK + 1;
+  const float2* mzp = a.attn_mz + static_cast<size_t>(h) * maxc;
+  float m = X.amz[0].x;
+#pragma unroll
+  for (int c = 1; c < ATTN_MZ; ++c)
+    if (c < nch) m = fmaxf(m, X.amz[c].x);
+  for (int c = ATTN_MZ; c < nch; ++c) m = fmaxf(m, mzp[c].x);
+  float Z = 0.0f;
+  f32x4 O[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) O[v] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto step = [&](float2 mz, const f32x4 (&o)[4]) {
+    const float f = exp_f32(mz.x - m);
+    Z = __builtin_fmaf(mz.y, f, Z);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (v < nv4) {
+        O[v].x = __builtin_fmaf(o[v].x, f, O[v].x);
+        O[v].y = __builtin_fmaf(o[v].y, f, O[v].y);
+        O[v].z = __builtin_fmaf(o[v].z, f, O[v].z);
+        O[v].w = __builtin_fmaf(o[v].w, f, O[v].w);
+      }
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < ATTN_RB; ++c)
+    if (c < nch) step(X.amz[c], X.ao[c]);
+  // further chunks, ATTN_RB at a time: loads first, then the steps in order
+  for (int c0 = ATTN_RB; c0 < nch; c0 += ATTN_RB) {
+    f32x4 ob[ATTN_RB][4];
+    float2 mb[ATTN_RB];
+#pragma unroll
+    for (int k = 0; k < ATTN_RB; ++k) {
+      if (c0 + k < nch) {
+        const int c = c0 + k;
+        mb[k] = mzp[c];
+        const f32x4* o = reinterpret_cast<const f32x4*>(a.x + (static_cast<size_t>(h) * maxc + c) * hd + d0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (v < nv4) ob[k][v] = o[v];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < ATTN_RB; ++k)
+      if (c0 + k < nch) step(mb[k], ob[k]);
+  }
+  if (threadIdx.x < QK_K) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (v < nv4) {
+        const f32x4 r = O[v];
+        *reinterpret_cast<f32x4*>(sx + i0 + 4 * v) = f32x4{r.x / Z, r.y / Z, r.z / Z, r.w / Z};
+      }
+    }
+  }
+  __syncthreads();
+}
+
 // Q8_K activations of the work group into LDS: as given (PRO_Q8K), or
 // quantized from fp32 (ties-even or ties-away), optionally after RMSNorm
 // (src/ops/ops.cpp:676-723, 745-789).  Ends with a work-group barrier.
@@ -156,39 +262,37 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, int NW, int 
   } else {
     constexpr bool norm = (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN);
     constexpr bool away = (PRO == PRO_QUANT_AWAY || PRO == PRO_NORM_AWAY);
+    constexpr bool attn = (PRO == PRO_ATTN_EVEN);
+    if constexpr (attn) attn_combine(a, X, reinterpret_cast<float*>(L + P.u));
     float rms = 1.0f;
     if constexpr (norm) {
       // thread t's partial runs over x[t], x[t+256], ... (multiply then add)
-      float* sx = reinterpret_cast<float*>(L + P.u);
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const int b = 4 * NW * r + 4 * wave + row;
-        if (4 * NW * r < nb && b < nb) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) *reinterpret_cast<f32x4*>(&sx[b * QK_K + 16 * j + 4 * i]) = X.x[r][i];
-        }
-      }
-      __syncthreads();
-      const int tid = min(static_cast<int>(threadIdx.x), QK_K - 1);  // partial slots 0..255
       float p = 0.0f;
-#pragma unroll 8
-      for (int jj = 0; jj < nb; ++jj) {
-        const float v = sx[jj * QK_K + tid];
-        p = p + v * v;
-      }
-      rms = block_rms_from_partials(p, nb * QK_K, a.eps, reinterpret_cast<float*>(L + P.red));
+#pragma unroll
+      for (int jj = 0; jj < MAX_NB; ++jj)
+        if (jj < nb) p = p + X.xp[jj] * X.xp[jj];
+      rms = block_rms_1sync(p, nb * QK_K, a.eps, reinterpret_cast<float*>(L + P.red));
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       if (4 * NW * r < nb) {  // uniform
         const int b = 4 * NW * r + 4 * wave + row;
         float v[16];
+        f32x4 xv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          v[4 * i] = X.x[r][i].x;
-          v[4 * i + 1] = X.x[r][i].y;
-          v[4 * i + 2] = X.x[r][i].z;
-          v[4 * i + 3] = X.x[r][i].w;
+          if constexpr (attn)
+            xv[i] = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(L + P.u) + min(b, nb - 1) * QK_K +
+                                                    16 * j + 4 * i);
+          else
+            xv[i] = X.x[r][i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[4 * i] = xv[i].x;
+          v[4 * i + 1] = xv[i].y;
+          v[4 * i + 2] = xv[i].z;
+          v[4 * i + 3] = xv[i].w;
         }
         if constexpr (norm) {
 #pragma unroll
@@ -324,8 +428,10 @@ __device__ __forceinline__ uint32_t dw(const u32x4* w, int i) {
 
 __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
 
-__device__ __forceinline__ int dot4(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), 0, false);
+// c + the four signed byte products of a and b (v_dot4c: the accumulator is
+// the destination, so a running sum costs no extra instruction)
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
 // bytes k and k+1 of w as a pair of (zero-extended) 16-bit lanes
@@ -341,6 +447,11 @@ __device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
 // block's min sum over the 8 sub-blocks of mn_g*(bsums[2g]+bsums[2g+1]) (xbp:
 // those pair sums as i16 pairs).  Native quant dword 8j+m holds, per byte,
 // sub-block 2j (low nibble) and 2j+1 (high nibble) at positions 4m..4m+3.
+//
+// isum[m] = sum_k sc_k*D_k over sub-blocks k (D_k: lane m's 4-byte dot) is
+// formed by summation by parts: with running dots P_k = D_0 + .. + D_k,
+// isum[m] = sum_{k<7} (sc_k - sc_{k+1})*P_k + sc_7*P_7, the same integer.  The
+// running dot is the dot instruction's own accumulator.
 template <int WT>
 __device__ __forceinline__ void q4k_rowblock(const Blk<WT>& K, const uint32_t* __restrict__ xs,
                                              const uint32_t* __restrict__ xbp, int (&is)[8], int& ms) {
@@ -350,13 +461,18 @@ __device__ __forceinline__ void q4k_rowblock(const Blk<WT>& K, const uint32_t* _
   const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
   const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
   const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+  int sc[8], cf[8];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) is[m] = 0;
+  for (int k = 0; k < 4; ++k) {
+    sc[k] = static_cast<int>(__builtin_amdgcn_ubfe(sc_lo, 8 * k, 8));
+    sc[4 + k] = static_cast<int>(__builtin_amdgcn_ubfe(sc_hi, 8 * k, 8));
+  }
+#pragma unroll
+  for (int k = 0; k < 7; ++k) cf[k] = sc[k] - sc[k + 1];
+  cf[7] = sc[7];
+  int P[8];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t sw = (j < 2) ? sc_lo : sc_hi;
-    const int sce = (sw >> (16 * (j & 1))) & 0xff;      // sc[2j]
-    const int sco = (sw >> (16 * (j & 1) + 8)) & 0xff;  // sc[2j+1]
     const u32x4 xe0 = *reinterpret_cast<const u32x4*>(xs + 16 * j);
     const u32x4 xe1 = *reinterpret_cast<const u32x4*>(xs + 16 * j + 4);
     const u32x4 xo0 = *reinterpret_cast<const u32x4*>(xs + 16 * j + 8);
@@ -366,8 +482,10 @@ __device__ __forceinline__ void q4k_rowblock(const Blk<WT>& K, const uint32_t* _
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       const uint32_t q = dw(K.w, 8 * j + m);
-      is[m] = mad24(sce, dot4(q & 0x0f0f0f0fu, xe[m]), is[m]);
-      is[m] = mad24(sco, dot4((q >> 4) & 0x0f0f0f0fu, xo[m]), is[m]);
+      P[m] = dot4(q & 0x0f0f0f0fu, xe[m], j == 0 ? 0 : P[m]);
+      is[m] = j == 0 ? __mul24(cf[0], P[m]) : mad24(cf[2 * j], P[m], is[m]);
+      P[m] = dot4((q >> 4) & 0x0f0f0f0fu, xo[m], P[m]);
+      is[m] = mad24(cf[2 * j + 1], P[m], is[m]);
     }
   }
   const u32x4 bp = *reinterpret_cast<const u32x4*>(xbp);
@@ -380,16 +498,24 @@ __device__ __forceinline__ void q4k_rowblock(const Blk<WT>& K, const uint32_t* _
 // Eight lane sums of a Q6_K block (codes kept in [0, 63], the -32 applied as
 // 32*(bsums[2m]*sc[2m] + bsums[2m+1]*sc[2m+1])).  For half h and lane m:
 // ql dwords 16h+m, 16h+8+m, qh dword 8h+m, activations 32h+8g+m (g = 0..3),
-// scale 8h+2g+(m>=4).
+// scale 8h+2g+(m>=4).  Lane m's eight terms (h, g) in that order are summed
+// by parts over running dots as in q4k_rowblock, with the scale sequence of
+// its half of the lanes (m < 4 or m >= 4).
 template <int WT>
 __device__ __forceinline__ void q6k_rowblock(const Blk<WT>& K, const uint32_t* __restrict__ xs,
                                              const uint32_t* __restrict__ xbs, int (&is)[8]) {
   int sc[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    sc[i] = static_cast<int>(static_cast<int8_t>((dw(&K.w[12], i >> 2) >> (8 * (i & 3))) & 0xffu));
+  for (int i = 0; i < 16; ++i) sc[i] = __builtin_amdgcn_sbfe(static_cast<int>(dw(&K.w[12], i >> 2)), 8 * (i & 3), 8);
+  // cf[hi][k]: term k = 4h+g has scale sc[8h+2g+hi]
+  int cf[2][8];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) is[m] = 0;
+  for (int hi = 0; hi < 2; ++hi) {
+#pragma unroll
+    for (int k = 0; k < 7; ++k) cf[hi][k] = sc[8 * (k >> 2) + 2 * (k & 3) + hi] - sc[8 * ((k + 1) >> 2) + 2 * ((k + 1) & 3) + hi];
+    cf[hi][7] = sc[8 + 6 + hi];
+  }
+  int P[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     uint32_t xv[4][8];
@@ -414,12 +540,14 @@ __device__ __forceinline__ void q6k_rowblock(const Blk<WT>& K, const uint32_t* _
       const uint32_t q1 = (a1 & 0x0f0f0f0fu) | ((hb << 2) & 0x30303030u);
       const uint32_t q2 = ((a0 >> 4) & 0x0f0f0f0fu) | (hb & 0x30303030u);
       const uint32_t q3 = ((a1 >> 4) & 0x0f0f0f0fu) | ((hb >> 2) & 0x30303030u);
-      int v = is[m];
-      v = mad24(sc[8 * h + 0 + hi], dot4(q0, xv[0][m]), v);
-      v = mad24(sc[8 * h + 2 + hi], dot4(q1, xv[1][m]), v);
-      v = mad24(sc[8 * h + 4 + hi], dot4(q2, xv[2][m]), v);
-      v = mad24(sc[8 * h + 6 + hi], dot4(q3, xv[3][m]), v);
-      is[m] = v;
+      P[m] = dot4(q0, xv[0][m], h == 0 ? 0 : P[m]);
+      int v = h == 0 ? __mul24(cf[hi][0], P[m]) : mad24(cf[hi][4], P[m], is[m]);
+      P[m] = dot4(q1, xv[1][m], P[m]);
+      v = mad24(cf[hi][4 * h + 1], P[m], v);
+      P[m] = dot4(q2, xv[2][m], P[m]);
+      v = mad24(cf[hi][4 * h + 2], P[m], v);
+      P[m] = dot4(q3, xv[3][m], P[m]);
+      is[m] = mad24(cf[hi][4 * h + 3], P[m], v);
     }
   }
   int bsv[16];
@@ -448,8 +576,7 @@ __global__ void __launch_bounds__(64 * GEMV_MAX_WAVES) k_gemv(const GemvArgs a, 
   const int wave = sgpr(static_cast<int>(threadIdx.x >> 6));
   const int NW = static_cast<int>(blockDim.x >> 6);  // 4..8 waves
   const int nb = a.nb;
-  constexpr bool norm = (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN);
-  const LdsPlan P = lds_plan(nb, S, TILE, norm, NW);
+  const LdsPlan P = lds_plan(nb, S, TILE, PRO == PRO_ATTN_EVEN, NW);
   const int stride = gridDim.x * NW;
   const Region A = region_of(a.reg[0]), B = region_of(a.reg[1]), C = region_of(a.reg[2]);
 
@@ -499,12 +626,16 @@ __global__ void __launch_bounds__(64 * GEMV_MAX_WAVES) k_gemv(const GemvArgs a, 
 
   ProRegs X;
   prologue_load<PRO>(a, NW, wave, lane, X);
+  // A CU's vector loads return in issue order, so an activation load queued
+  // behind weight loads (HBM) waits for them.  Every wave's activation loads
+  // go first: a bare barrier (no wait for the data) before any weight load.
+  __builtin_amdgcn_s_barrier();
   Blk<WT> K0, K1;
   float2 e0 = make_float2(0.0f, 0.0f), e1 = make_float2(0.0f, 0.0f);
   int b0, s0, b1, s1;
   RowRef t0 = ref_at(0, b0, s0), t1;
-  prefetch_epi(0, e0);
   load_blk(K0, t0, min(b0, nb - 1));  // in flight during the prologue
+  prefetch_epi(0, e0);
   prologue_compute<PRO>(a, NW, wave, lane, X, L, P);
 
   float acc[8], accm = 0.0f;
@@ -602,26 +733,43 @@ __global__ void __launch_bounds__(64 * GEMV_MAX_WAVES) k_gemv(const GemvArgs a, 
       }
       if (k == KB - 1) {
         wave_sync();
-        // 8 lanes per row (lane = 8*row + m, S/8 passes) run the chain; the
-        // row values go to vrow for the epilogue's RoPE and gate/up partners
-        const int m = lane & 7;
+        // 4 lanes per row (lane = 4*row + c, S/16 passes) run the chain, lane c
+        // the accumulators of lane sums c and c+4; the row values go to vrow
+        // for the epilogue's RoPE and gate/up partners
+        const int c = lane & 3;
         float* vrow = reinterpret_cast<float*>(L + P.vrow) + wave * 64;
 #pragma unroll 1
-        for (int pass = 0; pass * 8 < S; ++pass) {
-          const int sr = pass * 8 + (lane >> 3);
+        for (int pass = 0; pass * 16 < S; ++pass) {
+          const int sr = pass * 16 + (lane >> 2);
           const int src = min(sr, S - 1);
-          float ac = 0.0f, am = 0.0f;
-#pragma unroll 4
-          for (int bb = 0; bb < nb; ++bb) {
-            const uint32_t* e = chain + (bb * S + src) * 12;
-            ac = __builtin_fmaf(__uint_as_float(e[8]), static_cast<float>(static_cast<int>(e[m])), ac);
-            am = __builtin_fmaf(-__uint_as_float(e[9]), static_cast<float>(static_cast<int>(e[10])), am);
+          float a0 = 0.0f, a1 = 0.0f, am = 0.0f;
+          // four blocks' entries read at once, then their fma steps in order
+#pragma unroll 1
+          for (int bq = 0; bq < nb; bq += 4) {
+            int i0[4], i1[4];
+            f32x4 dv[4];  // (d_x*d_w, d_x*dmin_w, minsum, -)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const uint32_t* e = chain + (min(bq + k, nb - 1) * S + src) * 12;
+              i0[k] = static_cast<int>(e[c]);
+              i1[k] = static_cast<int>(e[c + 4]);
+              dv[k] = *reinterpret_cast<const f32x4*>(e + 8);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              if (bq + k < nb) {
+                a0 = __builtin_fmaf(dv[k].x, static_cast<float>(i0[k]), a0);
+                a1 = __builtin_fmaf(dv[k].x, static_cast<float>(i1[k]), a1);
+                am = __builtin_fmaf(-dv[k].y, static_cast<float>(__float_as_int(dv[k].z)), am);
+              }
+            }
           }
-          float v = ac + __shfl_down(ac, 4);
+          // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) on lane c == 0
+          float v = a0 + a1;
           v = v + __shfl_down(v, 2);
           v = v + __shfl_down(v, 1);
           if (t.q4) v = v + am;
-          if (m == 0 && sr < S) vrow[sr] = v;
+          if (c == 0 && sr < S) vrow[sr] = v;
         }
         wave_sync();
         const int se = min(lane, S - 1);
@@ -732,8 +880,7 @@ Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
 }
 
 size_t lds_bytes(const GemvArgs& a, const Shape& sh, int prologue) {
-  const bool norm = (prologue == PRO_NORM_AWAY || prologue == PRO_NORM_EVEN);
-  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, norm, sh.NW).words) * 4;
+  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, prologue == PRO_ATTN_EVEN, sh.NW).words) * 4;
 }
 
 template <int PRO, int EPI, bool TILE, int WT>
@@ -810,6 +957,8 @@ int gemv_grid(const GemvArgs& a0, int n_cu) {
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s) {
   if (a.nb <= 0 || a.nb > MAX_NB) return hipErrorInvalidValue;
+  if (prologue == PRO_ATTN_EVEN && (a.nb > ATTN_MAX_NB || a.nb % 4 || a.head_dim <= 0 || a.head_dim % a.nb))
+    return hipErrorInvalidValue;
   if (a.pair && a.reg[0].w.type != a.reg[1].w.type) return hipErrorInvalidValue;
   GemvArgs b = a;
   if (!b.pair && epilogue == EPI_LOGITS) {
@@ -822,6 +971,7 @@ hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, 
   MCPM_PE(PRO_Q8K, EPI_STORE)
   MCPM_PE(PRO_QUANT_EVEN, EPI_STORE)
   MCPM_PE(PRO_QUANT_EVEN, EPI_RESID)
+  MCPM_PE(PRO_ATTN_EVEN, EPI_RESID)
   MCPM_PE(PRO_QUANT_AWAY, EPI_RESID)
   MCPM_PE(PRO_NORM_AWAY, EPI_QKV)
   MCPM_PE(PRO_NORM_AWAY, EPI_SWIGLU)

@@ -215,8 +215,6 @@ int mcpm_init(int device, mcpm_ctx** out) {
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&c->d_state, sizeof(StepState));
   if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c->h_state), sizeof(StepState), hipHostMallocDefault);
-  if (e == hipSuccess) e = hipMalloc(&c->d_attn_cnt, 256 * sizeof(unsigned));
-  if (e == hipSuccess) e = hipMemset(c->d_attn_cnt, 0, 256 * sizeof(unsigned));
   if (e == hipSuccess) e = hipMalloc(&c->d_rope, 512 * sizeof(float2));
   if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c->h_rope), 512 * sizeof(float2), hipHostMallocDefault);
   if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -238,7 +236,6 @@ void mcpm_destroy(mcpm_ctx* c) {
   if (c->d_rope) (void)hipFree(c->d_rope);
   if (c->h_rope) (void)hipHostFree(c->h_rope);
   if (c->d_attn_part) (void)hipFree(c->d_attn_part);
-  if (c->d_attn_cnt) (void)hipFree(c->d_attn_cnt);
   if (c->d_argmax_part) (void)hipFree(c->d_argmax_part);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
@@ -514,8 +511,9 @@ int mcpm_execute_attention(mcpm_ctx* c, float* out, const float* q, const float*
   const int kvd = n_kv_heads * head_dim;
   const int* st = reinterpret_cast<const int*>(c->d_state);
   MCPM_HIP(launch_kv_append(k_cur, v_cur, k_cache, v_cache, st, kvd, c->stream));
-  MCPM_HIP(launch_attention(q, k_cache, v_cache, st, n_heads, n_kv_heads, head_dim, max_chunks, c->d_attn_part,
-                            c->d_attn_cnt, out, c->stream));
+  const AttnPart part = attn_part_of(c->d_attn_part, n_heads, max_chunks, head_dim);
+  MCPM_HIP(launch_attention(q, k_cache, v_cache, st, n_heads, n_kv_heads, head_dim, max_chunks, part, c->stream));
+  MCPM_HIP(launch_attn_combine(part, st, n_heads, head_dim, max_chunks, out, c->stream));
   MCPM_HIP(hipStreamSynchronize(c->stream));
   return MCPM_OK;
 }

@@ -18,7 +18,6 @@ struct mcpm_ctx {
   int rope_cap = 0;
   float* d_attn_part = nullptr;
   size_t attn_part_cap = 0;
-  unsigned* d_attn_cnt = nullptr;      // zero-initialised, reset by the kernel
   float2* d_argmax_part = nullptr;
   int argmax_cap = 0;
 };

@@ -157,6 +157,7 @@ enum Prologue : int {
   PRO_QUANT_AWAY = 2, // quantize an fp32 vector, ties away (lround)
   PRO_NORM_AWAY = 3,  // RMSNorm then quantize, ties away (rmsnorm_and_quantize_q8k)
   PRO_NORM_EVEN = 4,  // RMSNorm then quantize, ties to even (rmsnorm + matmul)
+  PRO_ATTN_EVEN = 5,  // combine the attention partials, then quantize ties to even
 };
 
 // Epilogue modes.
@@ -175,6 +176,17 @@ struct GemvRegion {
   int rows;
 };
 
+// Per-chunk attention partials of every head (see k_attention): o_c values
+// [n_heads][max_chunks][head_dim] and (m_c, z_c) [n_heads][max_chunks], in
+// one allocation of n_heads*max_chunks*(head_dim+2) floats, o first.
+struct AttnPart {
+  float* o;
+  float2* mz;
+};
+inline AttnPart attn_part_of(float* base, int n_heads, int max_chunks, int head_dim) {
+  return AttnPart{base, reinterpret_cast<float2*>(base + static_cast<size_t>(n_heads) * max_chunks * head_dim)};
+}
+
 struct GemvArgs {
   GemvRegion reg[3];
   int nreg;
@@ -186,6 +198,8 @@ struct GemvArgs {
   const float* x;
   const float* gamma;
   float eps;
+  const float2* attn_mz;  // PRO_ATTN_EVEN: x is the partials' o, these their (m, z)
+  int attn_max_chunks;
   // epilogue inputs
   const int* state;      // [0] token, [1] pos
   const float2* rope_cs; // [max_seq][head_dim/2] (cos, sin)
@@ -236,8 +250,9 @@ hipError_t launch_rope(float* vec, const float2* cs, int n_heads, int head_dim, 
 hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc, const int* state, int kvd,
                             hipStream_t s);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, const int* state, int n_heads,
-                            int n_kv_heads, int head_dim, int max_chunks, float* part, unsigned* counters,
-                            float* out, hipStream_t s);
+                            int n_kv_heads, int head_dim, int max_chunks, const AttnPart& part, hipStream_t s);
+hipError_t launch_attn_combine(const AttnPart& part, const int* state, int n_heads, int head_dim, int max_chunks,
+                               float* out, hipStream_t s);
 hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s);
 hipError_t launch_dequant_rows(const WView& w, int row0, int n_rows, int cols, float* out, hipStream_t s);
 hipError_t launch_gemv_f32(const float* w, const float* x, float* out, int rows, int cols, hipStream_t s);

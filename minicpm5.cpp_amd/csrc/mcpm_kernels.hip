@@ -140,11 +140,12 @@ hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc
 //   out_i = O_i / Z
 // A split takes ceil(nch/16) consecutive chunks (at most ATTN_CPW), keeping
 // o_c in registers, so a kv head has at most 16 splits (up to 16*ATTN_CPW
-// chunks).  With one split it writes the output itself; otherwise the splits
-// write (m_c, z_c, o_c) to `part` ([n_heads][max_chunks][2 + head_dim] floats)
-// and the last split of a kv head to finish (a counter per kv head, reset by
-// that split) combines them.  Every load of a chunk's K and V rows is issued
-// at once, one chunk ahead, and the rows are staged through LDS.
+// chunks).  Every split writes its chunks' partials; the combine over the
+// chunks runs in the consumer (the O-projection's prologue, or
+// k_attn_combine), after the kernel boundary, so no split waits for another.
+// Partials (AttnPart): o_c at o[(h*max_chunks + c)*head_dim + i], (m_c, z_c)
+// at mz[h*max_chunks + c].  Every load of a chunk's K and V rows is issued at
+// once, one chunk ahead, and the rows are staged through LDS.
 constexpr int ATTN_MAX_GROUP = 8;
 constexpr int ATTN_CPW = 8;
 constexpr int ATTN_MAX_SPLITS = 16;
@@ -164,19 +165,6 @@ __device__ __forceinline__ float wave_max_fast(float v) {
   v = row16_max(v);
   v = fmaxf(v, __shfl_xor(v, 16));
   v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
-}
-
-// wave_tree_sum with the same pairwise order (lane t += lane t+s for s =
-// 32..1; lane 0 holds the total): s = 32, 16 across rows, s <= 8 by DPP row
-// shifts (only lanes < s read, and those stay inside their row).
-__device__ __forceinline__ float wave_tree_sum_fast(float v) {
-  v = v + __shfl_down(v, 32);
-  v = v + __shfl_down(v, 16);
-  v = v + dpp_f<0x108>(v);  // row_shl:8
-  v = v + dpp_f<0x104>(v);  // row_shl:4
-  v = v + dpp_f<0x102>(v);  // row_shl:2
-  v = v + dpp_f<0x101>(v);  // row_shl:1
   return v;
 }
 
@@ -208,8 +196,7 @@ template <int HDM>
 __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, const int* __restrict__ state,
                                                    int n_heads, int n_kv_heads, int hd, int max_chunks,
-                                                   float* __restrict__ part, unsigned* __restrict__ counters,
-                                                   float* __restrict__ out) {
+                                                   float* __restrict__ part_o, float2* __restrict__ part_mz) {
   constexpr int NV = HDM / 16;                      // float4 of a chunk's K (or V) per thread, at most
   constexpr int OPT = ATTN_MAX_GROUP * HDM / 256;   // outputs per thread, at most
   constexpr int NQ = ATTN_MAX_GROUP * HDM / 256;    // query values per thread, at most
@@ -219,7 +206,6 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
   __shared__ float sQ[ATTN_MAX_GROUP * HDM];
   __shared__ float sE[ATTN_MAX_GROUP * ATTN_CHUNK];
   __shared__ float2 sMZ[ATTN_CPW * ATTN_MAX_GROUP];
-  __shared__ int sLast;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kvh = blockIdx.x, split = blockIdx.y;
   const int T = state[1] + 1;
@@ -233,7 +219,6 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
   const int r4 = hd / 4;              // float4 per K/V row
   const int nf4 = ATTN_CHUNK * r4;    // float4 per chunk
   const int gh = group * hd;          // outputs of the work group
-  const int stride = 2 + hd;
   const float scale = 1.0f / sqrtf(static_cast<float>(hd));
   const size_t head_off = static_cast<size_t>(kvh) * hd;
 
@@ -307,113 +292,67 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
     }
   }
 
-  if (nsplit == 1) {
-#pragma unroll
-    for (int u = 0; u < OPT; ++u) {
-      const int oi = tid + 256 * u;
-      if (oi < gh) {
-        const int hh = oi / hd, i = oi - hh * hd;
-        float m = sMZ[hh].x;
-#pragma unroll
-        for (int cc = 1; cc < ATTN_CPW; ++cc)
-          if (cc < n) m = fmaxf(m, sMZ[cc * ATTN_MAX_GROUP + hh].x);
-        float Z = 0.0f, O = 0.0f;
-#pragma unroll
-        for (int cc = 0; cc < ATTN_CPW; ++cc) {
-          if (cc < n) {
-            const float2 mz = sMZ[cc * ATTN_MAX_GROUP + hh];
-            const float f = exp_f32(mz.x - m);
-            Z = __builtin_fmaf(mz.y, f, Z);
-            O = __builtin_fmaf(oc[u][cc], f, O);
-          }
-        }
-        out[static_cast<size_t>(kvh * group + hh) * hd + i] = O / Z;
-      }
-    }
-    return;
-  }
-
-  // this split's chunks to `part`
+  // this split's chunks to the partials
 #pragma unroll
   for (int u = 0; u < OPT; ++u) {
     const int oi = tid + 256 * u;
     if (oi < gh) {
       const int hh = oi / hd, i = oi - hh * hd;
-      float* ph = part + (static_cast<size_t>(kvh * group + hh) * max_chunks + c0) * stride + 2 + i;
+      float* ph = part_o + (static_cast<size_t>(kvh * group + hh) * max_chunks + c0) * hd + i;
 #pragma unroll
       for (int cc = 0; cc < ATTN_CPW; ++cc)
-        if (cc < n) ph[cc * stride] = oc[u][cc];
+        if (cc < n) ph[static_cast<size_t>(cc) * hd] = oc[u][cc];
     }
   }
   if (tid < ATTN_CPW * ATTN_MAX_GROUP) {
     const int cc = tid / ATTN_MAX_GROUP, hh = tid % ATTN_MAX_GROUP;
-    if (cc < n && hh < group) {
-      float* ph = part + (static_cast<size_t>(kvh * group + hh) * max_chunks + c0 + cc) * stride;
-      const float2 mz = sMZ[cc * ATTN_MAX_GROUP + hh];
-      ph[0] = mz.x;
-      ph[1] = mz.y;
-    }
+    if (cc < n && hh < group) part_mz[static_cast<size_t>(kvh * group + hh) * max_chunks + c0 + cc] = sMZ[cc * ATTN_MAX_GROUP + hh];
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) sLast = (atomicAdd(&counters[kvh], 1u) == static_cast<unsigned>(nsplit - 1));
-  __syncthreads();
-  if (!sLast) return;
-  __threadfence();
-  // combine all chunks of the kv head, loads in batches of 8
-#pragma unroll
-  for (int u = 0; u < OPT; ++u) {
-    const int oi = tid + 256 * u;
-    if (oi < gh) {
-      const int hh = oi / hd, i = oi - hh * hd;
-      const float* ph = part + static_cast<size_t>(kvh * group + hh) * max_chunks * stride;
-      float m = ph[0];
-      for (int b = 0; b < nch; b += 8) {
-        float mv[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) mv[k] = ph[static_cast<size_t>(min(b + k, nch - 1)) * stride];
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (b + k < nch) m = fmaxf(m, mv[k]);
-      }
-      float Z = 0.0f, O = 0.0f;
-      for (int b = 0; b < nch; b += 8) {
-        float mv[8], zv[8], ov[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float* pc = ph + static_cast<size_t>(min(b + k, nch - 1)) * stride;
-          mv[k] = pc[0];
-          zv[k] = pc[1];
-          ov[k] = pc[2 + i];
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          if (b + k < nch) {
-            const float f = exp_f32(mv[k] - m);
-            Z = __builtin_fmaf(zv[k], f, Z);
-            O = __builtin_fmaf(ov[k], f, O);
-          }
-        }
-      }
-      out[static_cast<size_t>(kvh * group + hh) * hd + i] = O / Z;
-    }
+}
+
+// The combine over a head's chunks for output i (head h, dim d), in chunk
+// order: m = max m_c; f_c = exp(m_c - m); Z = fma(z_c, f_c, Z);
+// O = fma(o_c[d], f_c, O); out = O / Z.
+__global__ void k_attn_combine(const float* __restrict__ part_o, const float2* __restrict__ part_mz,
+                               const int* __restrict__ state, int n_out, int hd, int max_chunks,
+                               float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_out) return;
+  const int nch = state[1] / ATTN_CHUNK + 1;
+  const int h = i / hd, d = i - h * hd;
+  const float2* mz = part_mz + static_cast<size_t>(h) * max_chunks;
+  const float* o = part_o + static_cast<size_t>(h) * max_chunks * hd + d;
+  float m = mz[0].x;
+  for (int c = 1; c < nch; ++c) m = fmaxf(m, mz[c].x);
+  float Z = 0.0f, O = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    const float f = exp_f32(mz[c].x - m);
+    Z = __builtin_fmaf(mz[c].y, f, Z);
+    O = __builtin_fmaf(o[static_cast<size_t>(c) * hd], f, O);
   }
-  if (tid == 0) counters[kvh] = 0u;
+  out[i] = O / Z;
 }
 
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, const int* state, int n_heads,
-                            int n_kv_heads, int head_dim, int max_chunks, float* part, unsigned* counters,
-                            float* out, hipStream_t s) {
+                            int n_kv_heads, int head_dim, int max_chunks, const AttnPart& part, hipStream_t s) {
   if (head_dim <= 0 || head_dim > 128 || head_dim % 4 || n_heads % n_kv_heads ||
       n_heads / n_kv_heads > ATTN_MAX_GROUP)
     return hipErrorInvalidValue;
   const dim3 grid(n_kv_heads, attn_splits(max_chunks));
   if (head_dim <= 64)
     launch_kernel(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
-                  max_chunks, part, counters, out);
+                  max_chunks, part.o, part.mz);
   else
     launch_kernel(k_attention<128>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
-                  max_chunks, part, counters, out);
+                  max_chunks, part.o, part.mz);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_combine(const AttnPart& part, const int* state, int n_heads, int head_dim, int max_chunks,
+                               float* out, hipStream_t s) {
+  const int n = n_heads * head_dim;
+  hipLaunchKernelGGL(k_attn_combine, dim3((n + 255) / 256), dim3(256), 0, s, part.o, part.mz, state, n, head_dim,
+                     max_chunks, out);
   return hipGetLastError();
 }
 
