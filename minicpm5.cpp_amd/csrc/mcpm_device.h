@@ -102,8 +102,7 @@ __device__ __forceinline__ void quant_block_row16(const float (&v)[16], bool awa
   const bool zero = (amax == 0.0f);
   d = zero ? 0.0f : amax * (1.0f / 127.0f);
   const float mul = zero ? 0.0f : 127.0f / amax;
-  int s = 0;
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  int q[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const float t = v[i] * mul;
@@ -112,9 +111,18 @@ __device__ __forceinline__ void quant_block_row16(const float (&v)[16], bool awa
     // finish both roundings
     float r = away ? t + __builtin_copysignf(0.49999997f, t) : rintf(t);
     r = fminf(fmaxf(r, -127.0f), 127.0f);
-    const int q = static_cast<int>(r);
-    s += q;
-    w[i >> 2] |= (static_cast<uint32_t>(q) & 0xffu) << (8 * (i & 3));
+    q[i] = static_cast<int>(r);
+  }
+  // low bytes of four codes into a dword (three byte permutes), and the code
+  // sum as byte dots against 1s
+  uint32_t w[4];
+  int s = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t lo = __builtin_amdgcn_perm(static_cast<uint32_t>(q[4 * k + 1]), static_cast<uint32_t>(q[4 * k]), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(static_cast<uint32_t>(q[4 * k + 3]), static_cast<uint32_t>(q[4 * k + 2]), 0x0c0c0400u);
+    w[k] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w[k]), 0x01010101, s, false);
   }
   packed = u32x4{w[0], w[1], w[2], w[3]};
   gsum = s;

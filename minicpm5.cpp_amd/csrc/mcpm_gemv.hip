@@ -109,7 +109,7 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
   const int nb = a.nb, row = lane >> 4, j = lane & 15;
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
-    if (4 * NW * r < nb) {  // uniform
+    if (4 * NW * r + 4 * wave < nb) {  // uniform in the wave: waves past the blocks skip
       const int b = min(4 * NW * r + 4 * wave + row, nb - 1);
       if constexpr (PRO == PRO_ATTN_EVEN) {
         // the activations are formed in LDS by prologue_compute
@@ -132,7 +132,8 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
     }
   }
   if constexpr (PRO == PRO_ATTN_EVEN) {
-    const int t = min(static_cast<int>(threadIdx.x), QK_K - 1);
+    if (wave >= 4) return;  // threads 0..255 form the activations
+    const int t = static_cast<int>(threadIdx.x);
     const int hd = a.head_dim, maxc = a.attn_max_chunks, nv4 = nb >> 2;
     const int i0 = t * nb, h = i0 / hd, d0 = i0 - h * hd;
     const int last = a.state[1] / ATTN_CHUNK;  // chunks 0..last
@@ -152,7 +153,8 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
     }
   }
   if constexpr (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN) {
-    const int t = min(static_cast<int>(threadIdx.x), QK_K - 1);
+    if (wave >= 4) return;  // threads 0..255 hold the RMS partials
+    const int t = static_cast<int>(threadIdx.x);
 #pragma unroll
     for (int g = 0; g < MAX_NB / 8; ++g) {
       if (8 * g < nb) {  // uniform
@@ -184,7 +186,11 @@ __device__ __forceinline__ void store_xblock(uint32_t* L, const LdsPlan& P, int 
 // x = O / Z, into sx (fp32, nb*256), then a work-group barrier.
 __device__ __forceinline__ void attn_combine(const GemvArgs& a, const ProRegs& X, float* sx) {
   const int nb = a.nb, hd = a.head_dim, maxc = a.attn_max_chunks, nv4 = nb >> 2;
-  const int t = min(static_cast<int>(threadIdx.x), QK_K - 1);
+  if (threadIdx.x >= QK_K) {  // waves 4 and up take no values
+    __syncthreads();
+    return;
+  }
+  const int t = static_cast<int>(threadIdx.x);
   const int i0 = t * nb, h = i0 / hd, d0 = i0 - h * hd;
   const int nch = a.state[1] / ATTN_CHUNK + 1;
   const float2* mzp = a.attn_mz + static_cast<size_t>(h) * maxc;
@@ -232,13 +238,11 @@ __device__ __forceinline__ void attn_combine(const GemvArgs& a, const ProRegs& X
     for (int k = 0; k < ATTN_RB; ++k)
       if (c0 + k < nch) step(mb[k], ob[k]);
   }
-  if (threadIdx.x < QK_K) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      if (v < nv4) {
-        const f32x4 r = O[v];
-        *reinterpret_cast<f32x4*>(sx + i0 + 4 * v) = f32x4{r.x / Z, r.y / Z, r.z / Z, r.w / Z};
-      }
+  for (int v = 0; v < 4; ++v) {
+    if (v < nv4) {
+      const f32x4 r = O[v];
+      *reinterpret_cast<f32x4*>(sx + i0 + 4 * v) = f32x4{r.x / Z, r.y / Z, r.z / Z, r.w / Z};
     }
   }
   __syncthreads();
@@ -254,7 +258,7 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, int NW, int 
   if constexpr (PRO == PRO_Q8K) {
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (4 * NW * r < nb) {
+      if (4 * NW * r + 4 * wave < nb) {  // uniform in the wave
         const int b = 4 * NW * r + 4 * wave + row;
         store_xblock(L, P, min(b, nb - 1), j, b < nb, X.q[r], X.d[r], X.bs[r]);
       }
@@ -268,14 +272,16 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, int NW, int 
     if constexpr (norm) {
       // thread t's partial runs over x[t], x[t+256], ... (multiply then add)
       float p = 0.0f;
+      if (wave < 4) {
 #pragma unroll
-      for (int jj = 0; jj < MAX_NB; ++jj)
-        if (jj < nb) p = p + X.xp[jj] * X.xp[jj];
+        for (int jj = 0; jj < MAX_NB; ++jj)
+          if (jj < nb) p = p + X.xp[jj] * X.xp[jj];
+      }
       rms = block_rms_1sync(p, nb * QK_K, a.eps, reinterpret_cast<float*>(L + P.red));
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (4 * NW * r < nb) {  // uniform
+      if (4 * NW * r + 4 * wave < nb) {  // uniform in the wave: waves past the blocks skip
         const int b = 4 * NW * r + 4 * wave + row;
         float v[16];
         f32x4 xv[4];
