@@ -27,6 +27,9 @@ sys.path.insert(0, os.path.join(ROOT, "minicpm5.cpp_amd", "python"))
 import mcpm  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per launch by kernel class from rocprofv3 FETCH_SIZE / WRITE_SIZE
+# runs, scaled by the same counters on a device copy of known size
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_2p4b_traffic.json")
 SEED = 20260105  # BASELINE seed 20260101 + configuration index 4
 PROMPT = 32
 
@@ -89,6 +92,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mix", type=int, default=0, help="0: Q6_K v/down in every layer; 1: llama.cpp layers")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of a graph replay")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="also run device-to-device copies of this many MB (the reference kernel of known "
+                         "size for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -132,6 +138,23 @@ def main():
         log(f"  {k:8s} {v['avg_us']:8.2f} us x {v['launches_per_token']:.0f}/token "
             f"= {v['us_per_token']:8.1f} us/token  {v['bytes_per_launch'] / (v['avg_us'] * 1e-6) / 1e9 if v['bytes_per_launch'] else 0:7.1f} GB/s")
 
+    if args.copy_calibration_mb > 0:
+        nbytes = args.copy_calibration_mb << 20
+        src, dst = mcpm.DeviceBuffer(ctx, nbytes), mcpm.DeviceBuffer(ctx, nbytes)
+        ctx.lib.mcpm_fill_device(ctx.h, src.ptr, 1, nbytes)
+        for _ in range(4):
+            mcpm.check(ctx.lib.mcpm_copy_device(ctx.h, dst.ptr, src.ptr, nbytes))
+        src.free()
+        dst.free()
+        log(f"copy calibration: 4 device copies of {args.copy_calibration_mb} MiB")
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            tr = json.load(f).get("classes", {}).get(dom)
+        if tr:
+            traffic = int(tr["fetch_bytes"] + tr["write_bytes"])
+
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
@@ -159,7 +182,7 @@ def main():
                    "token_roofline_frac": round(wbytes * tps / 1e9 / HBM_PEAK_GBPS, 4),
                    "kernels_us_per_token": {k: round(v["us_per_token"], 2) for k, v in bd.items()}},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 3)},
         "cpu_baseline": cpu,
     }

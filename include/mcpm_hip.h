@@ -68,6 +68,9 @@ int mcpm_device_free(mcpm_ctx *ctx, void *dptr);
 /* Synchronous copies on the context stream. */
 int mcpm_copy_to_device(mcpm_ctx *ctx, void *dst, const void *src, size_t bytes);
 int mcpm_copy_to_host(mcpm_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Device-to-device copy (reads and writes `bytes`: the kernel of known size
+ * that scales the HBM byte counters in the measurements). */
+int mcpm_copy_device(mcpm_ctx *ctx, void *dst, const void *src, size_t bytes);
 int mcpm_fill_device(mcpm_ctx *ctx, void *dst, int byte_value, size_t bytes);
 
 /* ------------------------------------------------------------ weights ---- */

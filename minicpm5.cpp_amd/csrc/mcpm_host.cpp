@@ -280,6 +280,13 @@ int mcpm_copy_to_host(mcpm_ctx* c, void* dst, const void* src, size_t bytes) {
   return MCPM_OK;
 }
 
+int mcpm_copy_device(mcpm_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c || (!dst && bytes) || (!src && bytes)) return fail(MCPM_ERR_ARG, "mcpm_copy_device: null argument");
+  MCPM_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream));
+  MCPM_HIP(hipStreamSynchronize(c->stream));
+  return MCPM_OK;
+}
+
 int mcpm_fill_device(mcpm_ctx* c, void* dst, int v, size_t bytes) {
   if (!c || (!dst && bytes)) return fail(MCPM_ERR_ARG, "mcpm_fill_device: null argument");
   MCPM_HIP(hipMemsetAsync(dst, v, bytes, c->stream));

@@ -73,6 +73,7 @@ _SIGS = {
     "mcpm_device_free": (_I, [_P, _P]),
     "mcpm_copy_to_device": (_I, [_P, _P, _P, _SZ]),
     "mcpm_copy_to_host": (_I, [_P, _P, _P, _SZ]),
+    "mcpm_copy_device": (_I, [_P, _P, _P, _SZ]),
     "mcpm_fill_device": (_I, [_P, _P, _I, _SZ]),
     "mcpm_tensor_upload": (_I, [_P, _P, _SZ, _I, _I64, _I64, C.POINTER(_P)]),
     "mcpm_tensor_download": (_I, [_P, _P, _P, _SZ]),
