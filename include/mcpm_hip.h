@@ -201,6 +201,19 @@ int mcpm_sample_logits(const float *logits, int n, float temperature, float top_
 /* 1: replay each token as one captured hipGraph (default); 0: eager launches. */
 int mcpm_engine_set_graph(mcpm_engine *e, int enable);
 
+/* Processes tokens[0..n) at positions pos0.. through every layer together
+ * (MFMA GEMMs), leaving the KV cache exactly as n calls of
+ * mcpm_engine_forward would; produces no logits.  Replaces the reference's
+ * per-token prompt loop (src/chat_session.cpp:154-160). */
+int mcpm_engine_prefill(mcpm_engine *e, const int *tokens, int n, int pos0);
+/* 1 (default): generate calls send all prompt tokens but the last through
+ * mcpm_engine_prefill; 0: one forward per prompt token.  Results are the same. */
+int mcpm_engine_set_prefill(mcpm_engine *e, int enable);
+int mcpm_engine_uses_prefill(const mcpm_engine *e);
+/* Copies K and V cache rows [pos0, pos0+n) of one layer (n * n_kv_heads *
+ * head_dim floats each) to host memory; k or v may be NULL. */
+int mcpm_engine_read_kv(mcpm_engine *e, int layer, int pos0, int n, float *k, float *v);
+
 /* Kernel-level timing for measurement.  Kernel classes: */
 #define MCPM_KC_QKV 0
 #define MCPM_KC_ATTN 1

@@ -34,6 +34,16 @@ struct TimedPair {
   hipEvent_t a, b;
 };
 
+// Scratch of the batched prompt path, for `cap` tokens at a time.
+struct PrefillBufs {
+  int cap = 0, max_chunks = 0;
+  int* tokens = nullptr;
+  float *x = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *g = nullptr, *u = nullptr, *part = nullptr;
+  _Float16 *xh = nullptr, *xbs = nullptr;
+  float* xd = nullptr;
+};
+constexpr int PREFILL_MAX_TOKENS = 256;  // tokens per batched pass
+
 }  // namespace
 
 struct mcpm_engine {
@@ -68,6 +78,9 @@ struct mcpm_engine {
   std::vector<TimedPair> events;
   size_t events_used = 0;
   int64_t weight_bytes = 0;
+  // batched prompt processing
+  bool use_prefill = true;
+  PrefillBufs pf;
 };
 
 namespace {
@@ -81,6 +94,15 @@ int alloc_dev(void** p, size_t bytes) {
 void drop_graph(mcpm_engine* e) {
   if (e->graph) (void)hipGraphExecDestroy(e->graph);
   e->graph = nullptr;
+}
+
+void free_prefill(PrefillBufs& b) {
+  for (void* p : {static_cast<void*>(b.tokens), static_cast<void*>(b.x), static_cast<void*>(b.qkv),
+                  static_cast<void*>(b.q), static_cast<void*>(b.att), static_cast<void*>(b.g),
+                  static_cast<void*>(b.u), static_cast<void*>(b.part), static_cast<void*>(b.xh),
+                  static_cast<void*>(b.xbs), static_cast<void*>(b.xd)})
+    if (p) (void)hipFree(p);
+  b = PrefillBufs{};
 }
 
 void free_engine(mcpm_engine* e) {
@@ -106,6 +128,7 @@ void free_engine(mcpm_engine* e) {
                   })
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
+  free_prefill(e->pf);
   delete e;
 }
 
@@ -400,9 +423,112 @@ int queue_state(mcpm_engine* e, int slot, int token, int pos, int step) {
   return MCPM_OK;
 }
 
+int ensure_prefill(mcpm_engine* e, int cap) {
+  PrefillBufs& b = e->pf;
+  if (cap <= b.cap && b.max_chunks == e->max_chunks) return MCPM_OK;
+  free_prefill(b);
+  const mcpm_model_config& c = e->cfg;
+  const size_t qd = static_cast<size_t>(c.n_heads) * c.head_dim, kvd = static_cast<size_t>(c.n_kv_heads) * c.head_dim;
+  const size_t kmax = std::max<size_t>({static_cast<size_t>(c.dim), qd, static_cast<size_t>(c.ffn_pad)});
+  const size_t n = static_cast<size_t>(cap);
+  int rc = alloc_dev(reinterpret_cast<void**>(&b.tokens), n * sizeof(int));
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.x), n * c.dim * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.qkv), n * (qd + 2 * kvd) * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.q), n * qd * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.att), n * qd * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.g), n * c.ffn * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.u), n * c.ffn * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.part), n * c.n_heads * e->max_chunks * (c.head_dim + 2) * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.xh), n * kmax * 2);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.xd), n * (kmax / QK_K) * 4);
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.xbs), n * (kmax / QK_K) * 16 * 2);
+  if (rc) {
+    free_prefill(b);
+    return rc;
+  }
+  b.cap = cap;
+  b.max_chunks = e->max_chunks;
+  return MCPM_OK;
+}
+
+// Every layer for tokens at positions pos0 .. pos0+n-1 (n <= the scratch
+// capacity), leaving their K and V rows in the cache exactly as per-token
+// decode leaves them.  The last layer stops after its K/V rows.
+int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
+  const mcpm_model_config& c = e->cfg;
+  hipStream_t s = e->ctx->stream;
+  PrefillBufs& b = e->pf;
+  const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim, nqkv = qd + 2 * kvd;
+  const QuantBatch qb{b.xh, b.xd, b.xbs};
+  MCPM_HIP(hipMemcpyAsync(b.tokens, tokens, n * sizeof(int), hipMemcpyHostToDevice, s));
+  MCPM_HIP(launch_embed_batch(view_of(e->embd), b.tokens, n, c.dim, b.x, s));
+  const AttnPart part = attn_part_of(b.part, n * c.n_heads, e->max_chunks, c.head_dim);
+  const size_t tok_o = static_cast<size_t>(c.n_heads) * e->max_chunks * c.head_dim;
+  const size_t tok_mz = static_cast<size_t>(c.n_heads) * e->max_chunks;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const Layer& L = e->L[l];
+    float* kc = e->kc + static_cast<size_t>(l) * e->max_seq * kvd;
+    float* vc = e->vc + static_cast<size_t>(l) * e->max_seq * kvd;
+    const int nbd = c.dim / QK_K;
+    MCPM_HIP(launch_quant_batch(b.x, nullptr, c.dim, L.attn_norm, c.eps, c.dim, c.dim, PRO_NORM_AWAY, n, qb, s));
+    MCPM_HIP(launch_gemm_q8k(view_of(L.wq), qd, nbd, n, qb, b.qkv, nqkv, false, s));
+    MCPM_HIP(launch_gemm_q8k(view_of(L.wk), kvd, nbd, n, qb, b.qkv + qd, nqkv, false, s));
+    MCPM_HIP(launch_gemm_q8k(view_of(L.wv), kvd, nbd, n, qb, b.qkv + qd + kvd, nqkv, false, s));
+    MCPM_HIP(launch_rope_kv_batch(b.qkv, n, qd, kvd, c.head_dim, e->rope, pos0, b.q, kc, vc, s));
+    if (l == c.n_layers - 1) break;  // nothing after the last K/V rows reaches the cache
+    MCPM_HIP(launch_attention_batch(b.q, kc, vc, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part, tok_o,
+                                    tok_mz, pos0, n, s));
+    MCPM_HIP(launch_attn_combine_batch(part, tok_o, tok_mz, pos0, n, c.n_heads, c.head_dim, e->max_chunks, b.att, s));
+    MCPM_HIP(launch_quant_batch(b.att, nullptr, qd, nullptr, 0.0f, qd, qd, PRO_QUANT_EVEN, n, qb, s));
+    MCPM_HIP(launch_gemm_q8k(view_of(L.wo), c.dim, qd / QK_K, n, qb, b.x, c.dim, true, s));
+    MCPM_HIP(launch_quant_batch(b.x, nullptr, c.dim, L.ffn_norm, c.eps, c.dim, c.dim, PRO_NORM_AWAY, n, qb, s));
+    MCPM_HIP(launch_gemm_q8k(view_of(L.wg), c.ffn, nbd, n, qb, b.g, c.ffn, false, s));
+    MCPM_HIP(launch_gemm_q8k(view_of(L.wu), c.ffn, nbd, n, qb, b.u, c.ffn, false, s));
+    MCPM_HIP(launch_quant_batch_swiglu(b.g, b.u, c.ffn, c.ffn, c.ffn_pad, n, qb, s));
+    MCPM_HIP(launch_gemm_q8k(view_of(L.wd), c.dim, c.ffn_pad / QK_K, n, qb, b.x, c.dim, true, s));
+  }
+  return MCPM_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int mcpm_engine_prefill(mcpm_engine* e, const int* tokens, int n, int pos0) {
+  if (!e || (!tokens && n) || n < 0 || pos0 < 0) return fail(MCPM_ERR_ARG, "mcpm_engine_prefill: bad argument");
+  if (!e->kc) return fail(MCPM_ERR_CONTEXT, "mcpm_engine_prefill: KV cache not initialised");
+  if (pos0 + n > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
+  for (int i = 0; i < n; ++i)
+    if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab) return fail(MCPM_ERR_ARG, "prefill token out of range");
+  if (n == 0) return MCPM_OK;
+  int rc = ensure_prefill(e, std::min(n, PREFILL_MAX_TOKENS));
+  if (rc) return rc;
+  for (int i = 0; i < n && !rc; i += PREFILL_MAX_TOKENS)
+    rc = prefill_pass(e, tokens + i, std::min(PREFILL_MAX_TOKENS, n - i), pos0 + i);
+  if (rc) return rc;
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  return MCPM_OK;
+}
+
+int mcpm_engine_set_prefill(mcpm_engine* e, int enable) {
+  if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_set_prefill: null engine");
+  e->use_prefill = enable != 0;
+  return MCPM_OK;
+}
+
+int mcpm_engine_uses_prefill(const mcpm_engine* e) { return e && e->use_prefill ? 1 : 0; }
+
+int mcpm_engine_read_kv(mcpm_engine* e, int layer, int pos0, int n, float* k, float* v) {
+  if (!e || layer < 0 || layer >= e->cfg.n_layers || pos0 < 0 || n < 0)
+    return fail(MCPM_ERR_ARG, "mcpm_engine_read_kv: bad argument");
+  if (!e->kc || pos0 + n > e->max_seq) return fail(MCPM_ERR_CONTEXT, "mcpm_engine_read_kv: rows outside the cache");
+  const size_t kvd = static_cast<size_t>(e->cfg.n_kv_heads) * e->cfg.head_dim;
+  const size_t off = (static_cast<size_t>(layer) * e->max_seq + pos0) * kvd, bytes = n * kvd * sizeof(float);
+  if (k) MCPM_HIP(hipMemcpyAsync(k, e->kc + off, bytes, hipMemcpyDeviceToHost, e->ctx->stream));
+  if (v) MCPM_HIP(hipMemcpyAsync(v, e->vc + off, bytes, hipMemcpyDeviceToHost, e->ctx->stream));
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  return MCPM_OK;
+}
 
 int mcpm_engine_load_gguf(mcpm_ctx* ctx, const char* path, mcpm_engine** out) {
   if (!ctx || !path || !out) return fail(MCPM_ERR_ARG, "mcpm_engine_load_gguf: null argument");
@@ -507,7 +633,11 @@ int mcpm_engine_generate_greedy(mcpm_engine* e, const int* prompt, int n_prompt,
   if (!rc) rc = ensure_staging(e, n_prompt);
   if (rc) return rc;
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-  for (int p = 0; p < n_prompt && !rc; ++p) {
+  // all but the last prompt token in batched passes, the last one (whose
+  // argmax is the first generated token) through the per-token graph
+  const int first = (e->use_prefill && n_prompt > 1) ? n_prompt - 1 : 0;
+  if (first) rc = mcpm_engine_prefill(e, prompt, first, 0);
+  for (int p = first; p < n_prompt && !rc; ++p) {
     rc = queue_state(e, p, prompt[p], p, 0);
     if (!rc) rc = run_token(e);
   }

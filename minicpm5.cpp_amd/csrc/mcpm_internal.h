@@ -253,6 +253,29 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, co
                             int n_kv_heads, int head_dim, int max_chunks, const AttnPart& part, hipStream_t s);
 hipError_t launch_attn_combine(const AttnPart& part, const int* state, int n_heads, int head_dim, int max_chunks,
                                float* out, hipStream_t s);
+
+// ---- prefill (batched prompt tokens; csrc/mcpm_prefill.hip) ----
+// Per-token Q8_K activations: fp16 codes [t][dim], d [t][dim/256], fp16
+// bsums [t][dim/256][16].
+struct QuantBatch {
+  _Float16* xh;
+  float* xd;
+  _Float16* xbs;
+};
+hipError_t launch_embed_batch(const WView& w, const int* tokens, int n_tok, int dim, float* x, hipStream_t s);
+hipError_t launch_quant_batch(const float* x, const float* u, int ld_x, const float* gamma, float eps, int dim,
+                              int n_valid, int mode, int n_tok, QuantBatch q, hipStream_t s);
+hipError_t launch_quant_batch_swiglu(const float* g, const float* u, int ld, int n_valid, int dim, int n_tok,
+                                     QuantBatch q, hipStream_t s);
+hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const QuantBatch& q, float* out, int ld_out,
+                           bool add, hipStream_t s);
+hipError_t launch_rope_kv_batch(const float* qkv, int n_tok, int qd, int kvd, int head_dim, const float2* rope,
+                                int pos0, float* q_out, float* kc, float* vc, hipStream_t s);
+hipError_t launch_attention_batch(const float* q, const float* kc, const float* vc, int n_heads, int n_kv_heads,
+                                  int head_dim, int max_chunks, const AttnPart& part, size_t tok_o, size_t tok_mz,
+                                  int pos0, int n_tok, hipStream_t s);
+hipError_t launch_attn_combine_batch(const AttnPart& part, size_t tok_stride_o, size_t tok_stride_mz, int pos0,
+                                     int n_tok, int n_heads, int head_dim, int max_chunks, float* out, hipStream_t s);
 hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s);
 hipError_t launch_dequant_rows(const WView& w, int row0, int n_rows, int cols, float* out, hipStream_t s);
 hipError_t launch_gemv_f32(const float* w, const float* x, float* out, int rows, int cols, hipStream_t s);

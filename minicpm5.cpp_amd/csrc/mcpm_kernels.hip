@@ -12,6 +12,8 @@
 //  * Sums of squares: 256 strided partials, then a pairwise tree.
 //  * Everything is compiled with -ffp-contract=off; fused multiply-adds are
 //    explicit.
+#include <algorithm>
+
 #include "mcpm_device.h"
 
 namespace mcpm {
@@ -196,7 +198,8 @@ template <int HDM>
 __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, const int* __restrict__ state,
                                                    int n_heads, int n_kv_heads, int hd, int max_chunks,
-                                                   float* __restrict__ part_o, float2* __restrict__ part_mz) {
+                                                   float* __restrict__ part_o, float2* __restrict__ part_mz,
+                                                   int pos0, size_t tok_q, size_t tok_o, size_t tok_mz) {
   constexpr int NV = HDM / 16;                      // float4 of a chunk's K (or V) per thread, at most
   constexpr int OPT = ATTN_MAX_GROUP * HDM / 256;   // outputs per thread, at most
   constexpr int NQ = ATTN_MAX_GROUP * HDM / 256;    // query values per thread, at most
@@ -208,7 +211,17 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
   __shared__ float2 sMZ[ATTN_CPW * ATTN_MAX_GROUP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kvh = blockIdx.x, split = blockIdx.y;
-  const int T = state[1] + 1;
+  // decode: the position from the step state; prefill (pos0 >= 0): token
+  // blockIdx.z at position pos0 + z, with its own q and partials
+  int T;
+  if (pos0 >= 0) {
+    T = pos0 + static_cast<int>(blockIdx.z) + 1;
+    q += blockIdx.z * tok_q;
+    part_o += blockIdx.z * tok_o;
+    part_mz += blockIdx.z * tok_mz;
+  } else {
+    T = state[1] + 1;
+  }
   const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
   const int cps = attn_chunks_per_split(nch);
   const int nsplit = attn_splits(nch);
@@ -341,10 +354,32 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, co
   const dim3 grid(n_kv_heads, attn_splits(max_chunks));
   if (head_dim <= 64)
     launch_kernel(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
-                  max_chunks, part.o, part.mz);
+                  max_chunks, part.o, part.mz, -1, size_t{0}, size_t{0}, size_t{0});
   else
     launch_kernel(k_attention<128>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
-                  max_chunks, part.o, part.mz);
+                  max_chunks, part.o, part.mz, -1, size_t{0}, size_t{0}, size_t{0});
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_batch(const float* q, const float* kc, const float* vc, int n_heads, int n_kv_heads,
+                                  int head_dim, int max_chunks, const AttnPart& part, size_t tok_o, size_t tok_mz,
+                                  int pos0, int n_tok, hipStream_t s) {
+  if (head_dim <= 0 || head_dim > 128 || head_dim % 4 || n_heads % n_kv_heads ||
+      n_heads / n_kv_heads > ATTN_MAX_GROUP || pos0 < 0)
+    return hipErrorInvalidValue;
+  // enough splits for every token's chunk count (the split count is not
+  // monotonic in it); a token's surplus splits return at once
+  int max_splits = 1;
+  for (int n = pos0 / ATTN_CHUNK + 1; n <= (pos0 + n_tok - 1) / ATTN_CHUNK + 1; ++n)
+    max_splits = std::max(max_splits, attn_splits(n));
+  const dim3 grid(n_kv_heads, max_splits, n_tok);
+  const size_t tok_q = static_cast<size_t>(n_heads) * head_dim;
+  if (head_dim <= 64)
+    hipLaunchKernelGGL(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, nullptr, n_heads, n_kv_heads, head_dim,
+                       max_chunks, part.o, part.mz, pos0, tok_q, tok_o, tok_mz);
+  else
+    hipLaunchKernelGGL(k_attention<128>, grid, dim3(256), 0, s, q, kc, vc, nullptr, n_heads, n_kv_heads, head_dim,
+                       max_chunks, part.o, part.mz, pos0, tok_q, tok_o, tok_mz);
   return hipGetLastError();
 }
 

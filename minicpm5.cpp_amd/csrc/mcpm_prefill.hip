@@ -1,0 +1,423 @@
+// mcpm_prefill.hip -- batched prompt processing (prefill) for gfx950.
+//
+// The reference prefills by calling forward() once per prompt token
+// (src/chat_session.cpp:154-160).  Here the prompt's tokens go through each
+// layer together, and every number that reaches the KV cache is the one the
+// per-token decode path produces:
+//  * activations are quantized per token exactly as the GEMV prologues do
+//    (same RMS tree, same Q8_K rounding), into fp16 copies of the int8 codes;
+//  * a row dot keeps the reference's AVX2 structure: per 256-block the eight
+//    integer lane sums isum[m] (lane m: bytes 4m..4m+3 of every 32-byte
+//    group), then acc[m] = fma(d_x*d_w, float(isum[m]), acc[m]) over blocks in
+//    order, Q4_K's min chain, and ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7));
+//  * isum[m] for 16 rows x 16 tokens is one v_mfma_f32_16x16x32_f16: K runs
+//    over lane m's 32 bytes (8 sub-blocks x 4) with A = sub-block scale x
+//    weight code and B = activation code.  Every product is an integer of at
+//    most 2048 in magnitude (exact in fp16) and every sum stays below 2^24
+//    (exact in fp32), so the MFMA result is isum[m] itself.  Q4_K: sc*q <= 945.
+//    Q6_K: the reference sums sc*q*x over lane m's bytes (q in 0..63, low 4
+//    bits ql, high 2 bits qh) and subtracts 32*(sc[2m]*bsums[2m] +
+//    sc[2m+1]*bsums[2m+1]) -- sub-block m's offset, added into lane m.  Three
+//    MFMAs give sum(sc*ql*x) (|sc*ql| <= 1920), sum(sc*qh*x) (|sc*qh| <= 384)
+//    and sc[2m]*bsums[2m] + sc[2m+1]*bsums[2m+1] exactly; they are combined
+//    in int32 (16*hi + lo - 32*c) and converted to float as the reference's
+//    int32 lane sum is.
+//  * Q4_K's min sum (sum over sub-blocks of mn * pair-sum of bsums) is one
+//    more MFMA: A = mn[k/2] for k < 16, B = bsums[k].
+// Attention per token is the decode kernel at that token's position.
+#include "mcpm_device.h"
+
+namespace mcpm {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+// ------------------------------------------------------------- embedding ---
+// Row tokens[t] of the embedding, dequantized into x[t] (grid: blocks x tokens).
+__global__ void __launch_bounds__(256) k_embed_batch(const WView w, const int* __restrict__ tokens, int dim,
+                                                     float* __restrict__ x) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * QK_K + threadIdx.x;
+  if (i < dim) x[static_cast<size_t>(t) * dim + i] = dequant_value(w, tokens[t], blockIdx.x, threadIdx.x);
+}
+
+// ------------------------------------------------------------- quantize ----
+// Per token (one work group each): the Q8_K quantization of the GEMV
+// prologues, written as fp16 codes [t][K], d [t][nb] and fp16 bsums
+// [t][nb][16].  mode: PRO_QUANT_EVEN / PRO_QUANT_AWAY / PRO_NORM_AWAY /
+// PRO_NORM_EVEN, or QB_SWIGLU: v = silu(g)*u (decode's gate/up epilogue) for
+// i < n_valid and 0 beyond, then ties-away (decode's down prologue).
+constexpr int QB_SWIGLU = 100;
+
+__global__ void __launch_bounds__(256) k_quant_batch(const float* __restrict__ x, const float* __restrict__ u,
+                                                     int ld_x, const float* __restrict__ gamma, float eps, int dim,
+                                                     int n_valid, int mode, _Float16* __restrict__ xh,
+                                                     float* __restrict__ xd, _Float16* __restrict__ xbs) {
+  __shared__ float red[260];
+  const int t = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const float* xt = x + static_cast<size_t>(t) * ld_x;
+  const float* ut = u ? u + static_cast<size_t>(t) * ld_x : nullptr;
+  const bool norm = (mode == PRO_NORM_AWAY || mode == PRO_NORM_EVEN);
+  const bool away = (mode == PRO_QUANT_AWAY || mode == PRO_NORM_AWAY || mode == QB_SWIGLU);
+  float rms = 1.0f;
+  if (norm) rms = block_rms_scale(xt, dim, eps, red);
+  const int nb = dim / QK_K;
+  for (int b = wave; b < nb; b += 4) {
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = b * QK_K + 4 * lane + k;
+      if (mode == QB_SWIGLU) {
+        float h = 0.0f;
+        if (i < n_valid) {
+          const float g = xt[i];
+          const float silu = g / (1.0f + exp_f32(-g));
+          h = silu * ut[i];
+        }
+        v[k] = h;
+      } else {
+        v[k] = xt[i];
+        if (norm) v[k] = (v[k] * rms) * gamma[i];
+      }
+    }
+    uint32_t packed;
+    float d;
+    int gsum;
+    quant_block_wave(v, away, packed, d, gsum);
+    _Float16* o = xh + static_cast<size_t>(t) * dim + b * QK_K + 4 * lane;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((packed >> (8 * k)) & 0xffu)));
+    if ((lane & 3) == 0) xbs[(static_cast<size_t>(t) * nb + b) * 16 + (lane >> 2)] = static_cast<_Float16>(gsum);
+    if (lane == 0) xd[static_cast<size_t>(t) * nb + b] = d;
+  }
+}
+
+// ------------------------------------------------------------------ GEMM ----
+struct GemmArgs {
+  WView w;
+  int rows, nb, n_tok;
+  const _Float16* xh;   // [n_tok][nb*256] activation codes
+  const float* xd;      // [n_tok][nb] Q8_K d
+  const _Float16* xbs;  // [n_tok][nb][16] bsums
+  float* out;           // out[t*ld_out + r]
+  int ld_out;
+  int add;              // 1: out += v (residual), 0: out = v
+};
+
+__device__ __forceinline__ uint32_t h2bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// fp16 pair (1024 + byte) from bytes of t picked by sel (0x64 high bytes),
+// minus off: small integers, exact
+__device__ __forceinline__ h2 byte_pair_h(uint32_t t, uint32_t sel, h2 off) {
+  return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t, sel)) - off;
+}
+constexpr uint32_t SEL01 = 0x04010400u, SEL23 = 0x04030402u;
+
+// Eight halves of lane m's A operand: the low (j < 4) and high (j >= 4)
+// K-halves, each four byte values (< 1024) of ta / tb minus off, times sa / sb.
+__device__ __forceinline__ h8 a_operand(uint32_t ta, uint32_t tb, h2 sa, h2 sb, h2 off) {
+  const u32x4 r{h2bits(byte_pair_h(ta, SEL01, off) * sa), h2bits(byte_pair_h(ta, SEL23, off) * sa),
+                h2bits(byte_pair_h(tb, SEL01, off) * sb), h2bits(byte_pair_h(tb, SEL23, off) * sb)};
+  return __builtin_bit_cast(h8, r);
+}
+
+__device__ __forceinline__ h2 splat_h(int v) {
+  const _Float16 h = static_cast<_Float16>(static_cast<float>(v));
+  return h2{h, h};
+}
+
+// A wave computes 16 rows x 16*NT tokens over all blocks.  MFMA operand
+// layout (v_mfma_f32_16x16x32_f16): lane l feeds A row l%16 and B column
+// l%16 with K = 8*(l/16) .. +7; D lane l register i is row 4*(l/16)+i,
+// column l%16.  With K index k = 4*s + i over sub-blocks s and bytes i,
+// lane l's K range is sub-blocks 2g and 2g+1 (g = l/16): element 64g + 4m + i
+// (low) and 64g + 32 + 4m + i (high) of the block for lane group m.
+template <int WT, int NT>
+__global__ void __launch_bounds__(256) k_gemm_q8k(const GemmArgs a) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  const int n_rt = (a.rows + 15) >> 4;
+  const int n_tg = (a.n_tok + 16 * NT - 1) / (16 * NT);
+  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= n_rt * n_tg) return;
+  const int r0 = (tile % n_rt) * 16, t0 = (tile / n_rt) * (16 * NT);
+  const size_t rows = static_cast<size_t>(a.rows);
+  const int ra = min(r0 + c16, a.rows - 1);  // A operand row of this lane
+  const int K = a.nb * QK_K;
+
+  float acc[NT][8][4], accm[NT][4];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      accm[n][i] = 0.0f;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) acc[n][m][i] = 0.0f;
+    }
+  }
+  int tok[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) tok[n] = min(t0 + 16 * n + c16, a.n_tok - 1);
+
+  const h2 off1024{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  const f32x4 zero4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int b = 0; b < a.nb; ++b) {
+    // d (and dmin) of the four D rows of this lane
+    float dw[4], dmw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const size_t r = static_cast<size_t>(min(r0 + 4 * g + i, a.rows - 1));
+      if constexpr (WT == 0) {
+        const uint32_t hd = *reinterpret_cast<const uint32_t*>(a.w.p1 + (static_cast<size_t>(b) * rows + r) * 16);
+        dw[i] = fp16_to_fp32(static_cast<uint16_t>(hd & 0xffffu));
+        dmw[i] = fp16_to_fp32(static_cast<uint16_t>(hd >> 16));
+      } else {
+        dw[i] = fp16_to_fp32(*reinterpret_cast<const uint16_t*>(a.w.p3 + (static_cast<size_t>(b) * rows + r) * 2));
+        dmw[i] = 0.0f;
+      }
+    }
+    // A operands of the eight lane groups (and Q4_K's min operand)
+    h8 A[8], AH[8], AM, AC[8];
+    if constexpr (WT == 0) {
+      const u32x4 hdr = *reinterpret_cast<const u32x4*>(a.w.p1 + (static_cast<size_t>(b) * rows + ra) * 16);
+      const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+      const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+      const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+      const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+      const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+      const uint32_t sw = g < 2 ? sc_lo : sc_hi;
+      const int sh = 16 * (g & 1);
+      const h2 sa = splat_h(static_cast<int>((sw >> sh) & 0xffu));        // sc[2g]
+      const h2 sb = splat_h(static_cast<int>((sw >> (sh + 8)) & 0xffu));  // sc[2g+1]
+      const uint8_t* q = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
+      const u32x4 q0 = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g) * rows * 16);
+      const u32x4 q1 = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g + 1) * rows * 16);
+      const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        A[m] = a_operand(qw[m] & 0x0f0f0f0fu, (qw[m] >> 4) & 0x0f0f0f0fu, sa, sb, off1024);
+      // min operand: k = 8g + j < 16 -> mn[k/2]
+      const uint32_t mw = (g & 1) ? mn_hi : mn_lo;
+      const u32x4 mr{h2bits(byte_pair_h(mw, 0x04000400u, off1024)), h2bits(byte_pair_h(mw, 0x04010401u, off1024)),
+                     h2bits(byte_pair_h(mw, 0x04020402u, off1024)), h2bits(byte_pair_h(mw, 0x04030403u, off1024))};
+      AM = g < 2 ? __builtin_bit_cast(h8, mr) : h8{};
+    } else {
+      const int h = g >> 1, nib = 4 * (g & 1);
+      const u32x4 scr = *reinterpret_cast<const u32x4*>(a.w.p2 + (static_cast<size_t>(b) * rows + ra) * 16);
+      // scales 4g .. 4g+3 (signed bytes) = dword g of the 16 scales
+      const uint32_t scw = g == 0 ? scr.x : g == 1 ? scr.y : g == 2 ? scr.z : scr.w;
+      // the offset operand: K entries 0, 1 (lanes 0..15, halves 0, 1) are
+      // sc[2m], sc[2m+1] of this lane's row
+      const uint32_t scall[4] = {scr.x, scr.y, scr.z, scr.w};
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const uint32_t w2 = scall[m >> 1];
+        const int lo = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1), 8);
+        const int hi = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1) + 8, 8);
+        const h2 pair{static_cast<_Float16>(static_cast<float>(lo)), static_cast<_Float16>(static_cast<float>(hi))};
+        AC[m] = g == 0 ? __builtin_bit_cast(h8, u32x4{h2bits(pair), 0u, 0u, 0u}) : h8{};
+      }
+      h2 sc[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sc[k] = splat_h(__builtin_amdgcn_sbfe(static_cast<int>(scw), 8 * k, 8));
+      const uint8_t* ql = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
+      const uint8_t* qh = a.w.p1 + (static_cast<size_t>(b) * 4 * rows + ra) * 16;
+      uint32_t lw[16], hw[8];
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ql + static_cast<size_t>(4 * h + cc) * rows * 16);
+        lw[4 * cc] = v.x;
+        lw[4 * cc + 1] = v.y;
+        lw[4 * cc + 2] = v.z;
+        lw[4 * cc + 3] = v.w;
+      }
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(qh + static_cast<size_t>(2 * h + cc) * rows * 16);
+        hw[4 * cc] = v.x;
+        hw[4 * cc + 1] = v.y;
+        hw[4 * cc + 2] = v.z;
+        hw[4 * cc + 3] = v.w;
+      }
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)];
+        A[m] = a_operand((lw[m] >> nib) & 0x0f0f0f0fu, (lw[8 + m] >> nib) & 0x0f0f0f0fu, sa, sb, off1024);
+        AH[m] = a_operand((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, off1024);
+      }
+    }
+
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const size_t tk = static_cast<size_t>(tok[n]);
+      const u32x4* xp = reinterpret_cast<const u32x4*>(a.xh + tk * K + b * QK_K + 64 * g);
+      uint32_t xw[32];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const u32x4 x4 = xp[v];
+        xw[4 * v] = x4.x;
+        xw[4 * v + 1] = x4.y;
+        xw[4 * v + 2] = x4.z;
+        xw[4 * v + 3] = x4.w;
+      }
+      const float xdv = a.xd[tk * a.nb + b];
+      uint32_t bsw[8];  // Q6_K: bsums of the token's block as fp16 pairs (lanes 0..15 use them)
+      if constexpr (WT == 1) {
+        const u32x4* bp = reinterpret_cast<const u32x4*>(a.xbs + (tk * a.nb + b) * 16);
+        const u32x4 b0 = bp[0], b1 = bp[1];
+        bsw[0] = b0.x;
+        bsw[1] = b0.y;
+        bsw[2] = b0.z;
+        bsw[3] = b0.w;
+        bsw[4] = b1.x;
+        bsw[5] = b1.y;
+        bsw[6] = b1.z;
+        bsw[7] = b1.w;
+      }
+      float ds[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ds[i] = xdv * dw[i];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const h8 B = __builtin_bit_cast(h8, u32x4{xw[2 * m], xw[2 * m + 1], xw[16 + 2 * m], xw[17 + 2 * m]});
+        f32x4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[m], B, zero4, 0, 0, 0);
+        if constexpr (WT == 1) {
+          const f32x4 DH = __builtin_amdgcn_mfma_f32_16x16x32_f16(AH[m], B, zero4, 0, 0, 0);
+          const h8 BC = g == 0 ? __builtin_bit_cast(h8, u32x4{bsw[m], 0u, 0u, 0u}) : h8{};
+          const f32x4 DC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC[m], BC, zero4, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int isum = (static_cast<int>(DH[i]) << 4) + static_cast<int>(D[i]) - 32 * static_cast<int>(DC[i]);
+            D[i] = static_cast<float>(isum);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[n][m][i] = __builtin_fmaf(ds[i], D[i], acc[n][m][i]);
+      }
+      if constexpr (WT == 0) {
+        const h8 BM = *reinterpret_cast<const h8*>(a.xbs + (tk * a.nb + b) * 16 + 8 * (g & 1));
+        const f32x4 DM = __builtin_amdgcn_mfma_f32_16x16x32_f16(AM, BM, zero4, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) accm[n][i] = __builtin_fmaf(-(xdv * dmw[i]), DM[i], accm[n][i]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int t = t0 + 16 * n + c16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = r0 + 4 * g + i;
+      float v = ((acc[n][0][i] + acc[n][4][i]) + (acc[n][2][i] + acc[n][6][i])) +
+                ((acc[n][1][i] + acc[n][5][i]) + (acc[n][3][i] + acc[n][7][i]));
+      if constexpr (WT == 0) v = v + accm[n][i];
+      if (r < a.rows && t < a.n_tok) {
+        float* o = a.out + static_cast<size_t>(t) * a.ld_out + r;
+        *o = a.add ? *o + v : v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------- RoPE and KV ----
+// qkv[t] = (q | k | v) rows of token t (position pos0 + t): q rotated into
+// q_out[t], k rotated and v copied into the KV cache rows (decode's QKV
+// epilogue, src/ops/ops.cpp:502-516).
+__global__ void k_rope_kv_batch(const float* __restrict__ qkv, int qd, int kvd, int head_dim,
+                                const float2* __restrict__ rope, int pos0, float* __restrict__ q_out,
+                                float* __restrict__ kc, float* __restrict__ vc) {
+  const int t = blockIdx.y;
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  const int n = qd + 2 * kvd;
+  if (r >= n) return;
+  const int pos = pos0 + t;
+  const float* src = qkv + static_cast<size_t>(t) * n;
+  const float v = src[r];
+  if (r < qd + kvd) {
+    const int i = (r < qd ? r : r - qd) % head_dim;
+    const float partner = src[r ^ 1];
+    const float2 cs = rope[static_cast<size_t>(pos) * (head_dim / 2) + (i >> 1)];
+    float o;
+    if ((i & 1) == 0) o = v * cs.x - partner * cs.y;
+    else o = partner * cs.y + v * cs.x;
+    if (r < qd) q_out[static_cast<size_t>(t) * qd + r] = o;
+    else kc[static_cast<size_t>(pos) * kvd + (r - qd)] = o;
+  } else {
+    vc[static_cast<size_t>(pos) * kvd + (r - qd - kvd)] = v;
+  }
+}
+
+// ------------------------------------------------------- attention combine --
+// k_attn_combine for token t (position pos0 + t) with per-token partials.
+__global__ void k_attn_combine_batch(const float* __restrict__ part_o, const float2* __restrict__ part_mz,
+                                     size_t tok_stride_o, size_t tok_stride_mz, int pos0, int n_out, int hd,
+                                     int max_chunks, float* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_out) return;
+  const int nch = (pos0 + t) / ATTN_CHUNK + 1;
+  const int h = i / hd, d = i - h * hd;
+  const float2* mz = part_mz + t * tok_stride_mz + static_cast<size_t>(h) * max_chunks;
+  const float* o = part_o + t * tok_stride_o + static_cast<size_t>(h) * max_chunks * hd + d;
+  float m = mz[0].x;
+  for (int c = 1; c < nch; ++c) m = fmaxf(m, mz[c].x);
+  float Z = 0.0f, O = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    const float f = exp_f32(mz[c].x - m);
+    Z = __builtin_fmaf(mz[c].y, f, Z);
+    O = __builtin_fmaf(o[static_cast<size_t>(c) * hd], f, O);
+  }
+  out[static_cast<size_t>(t) * n_out + i] = O / Z;
+}
+
+// -------------------------------------------------------------- launchers --
+hipError_t launch_embed_batch(const WView& w, const int* tokens, int n_tok, int dim, float* x, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed_batch, dim3((dim + QK_K - 1) / QK_K, n_tok), dim3(QK_K), 0, s, w, tokens, dim, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_batch(const float* x, const float* u, int ld_x, const float* gamma, float eps, int dim,
+                              int n_valid, int mode, int n_tok, QuantBatch q, hipStream_t s) {
+  if (dim % QK_K) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_quant_batch, dim3(n_tok), dim3(256), 0, s, x, u, ld_x, gamma, eps, dim, n_valid, mode,
+                     q.xh, q.xd, q.xbs);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_batch_swiglu(const float* g, const float* u, int ld, int n_valid, int dim, int n_tok,
+                                     QuantBatch q, hipStream_t s) {
+  return launch_quant_batch(g, u, ld, nullptr, 0.0f, dim, n_valid, QB_SWIGLU, n_tok, q, s);
+}
+
+hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const QuantBatch& q, float* out, int ld_out,
+                           bool add, hipStream_t s) {
+  if (w.type != MCPM_TYPE_Q4_K && w.type != MCPM_TYPE_Q6_K) return hipErrorInvalidValue;
+  GemmArgs a{w, rows, nb, n_tok, q.xh, q.xd, q.xbs, out, ld_out, add ? 1 : 0};
+  constexpr int NT = 2;
+  const int n_tiles = ((rows + 15) / 16) * ((n_tok + 16 * NT - 1) / (16 * NT));
+  const dim3 grid((n_tiles + 3) / 4);
+  if (w.type == MCPM_TYPE_Q4_K) launch_kernel(k_gemm_q8k<0, NT>, grid, dim3(256), 0, s, a);
+  else launch_kernel(k_gemm_q8k<1, NT>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_batch(const float* qkv, int n_tok, int qd, int kvd, int head_dim, const float2* rope,
+                                int pos0, float* q_out, float* kc, float* vc, hipStream_t s) {
+  const int n = qd + 2 * kvd;
+  hipLaunchKernelGGL(k_rope_kv_batch, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, qkv, qd, kvd, head_dim, rope,
+                     pos0, q_out, kc, vc);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_combine_batch(const AttnPart& part, size_t tok_stride_o, size_t tok_stride_mz, int pos0,
+                                     int n_tok, int n_heads, int head_dim, int max_chunks, float* out, hipStream_t s) {
+  const int n = n_heads * head_dim;
+  hipLaunchKernelGGL(k_attn_combine_batch, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, part.o, part.mz,
+                     tok_stride_o, tok_stride_mz, pos0, n, head_dim, max_chunks, out);
+  return hipGetLastError();
+}
+
+}  // namespace mcpm

@@ -69,7 +69,13 @@ int mcpm_engine_generate_sampled(mcpm_engine* e, const int* prompt, int n_prompt
   std::uniform_real_distribution<float> dist(0.0f, 1.0f);
   std::vector<float> logits(static_cast<size_t>(c.vocab));
   int next = -1;
-  for (int p = 0; p < n_prompt; ++p) {
+  // all but the last prompt token in batched passes (when enabled)
+  const int first = (mcpm_engine_uses_prefill(e) && n_prompt > 1) ? n_prompt - 1 : 0;
+  if (first) {
+    rc = mcpm_engine_prefill(e, prompt, first, 0);
+    if (rc) return rc;
+  }
+  for (int p = first; p < n_prompt; ++p) {
     const bool last = (p == n_prompt - 1);
     rc = mcpm_engine_forward(e, prompt[p], p, 1 << 30, last ? logits.data() : nullptr, nullptr);
     if (rc) return rc;

@@ -74,6 +74,10 @@ _SIGS = {
     "mcpm_copy_to_device": (_I, [_P, _P, _P, _SZ]),
     "mcpm_copy_to_host": (_I, [_P, _P, _P, _SZ]),
     "mcpm_copy_device": (_I, [_P, _P, _P, _SZ]),
+    "mcpm_engine_prefill": (_I, [_P, C.POINTER(C.c_int), _I, _I]),
+    "mcpm_engine_set_prefill": (_I, [_P, _I]),
+    "mcpm_engine_uses_prefill": (_I, [_P]),
+    "mcpm_engine_read_kv": (_I, [_P, _I, _I, _I, _P, _P]),
     "mcpm_fill_device": (_I, [_P, _P, _I, _SZ]),
     "mcpm_tensor_upload": (_I, [_P, _P, _SZ, _I, _I64, _I64, C.POINTER(_P)]),
     "mcpm_tensor_download": (_I, [_P, _P, _P, _SZ]),
@@ -345,6 +349,20 @@ class Engine:
 
     def set_graph(self, enable: bool):
         check(self.lib.mcpm_engine_set_graph(self.h, int(enable)))
+
+    def set_prefill(self, enable: bool):
+        check(self.lib.mcpm_engine_set_prefill(self.h, int(enable)))
+
+    def prefill(self, tokens, pos0: int = 0):
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        check(self.lib.mcpm_engine_prefill(self.h, t.ctypes.data_as(C.POINTER(C.c_int)), t.size, pos0))
+
+    def read_kv(self, layer: int, pos0: int, n: int):
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        k = np.empty((n, kvd), np.float32)
+        v = np.empty((n, kvd), np.float32)
+        check(self.lib.mcpm_engine_read_kv(self.h, layer, pos0, n, k.ctypes.data, v.ctypes.data))
+        return k, v
 
     def set_kernel_timing(self, kc: int):
         check(self.lib.mcpm_engine_set_kernel_timing(self.h, kc))

@@ -116,13 +116,18 @@ def test_sampled_matches_oracle_sampler(small_engine, small_image):
     np.testing.assert_array_equal(got, np.array(out, np.int32))
 
 
-def test_kernel_timing_counts(small_engine):
+@pytest.mark.parametrize("prefill", [False, True])
+def test_kernel_timing_counts(small_engine, prefill):
+    small_engine.set_prefill(prefill)
     small_engine.set_kernel_timing(mcpm.KC_GATE_UP)
     small_engine.generate_greedy(np.array([1, 2, 3], np.int32), 2)
     t, n = small_engine.kernel_time()
-    # 3 prompt positions + 1 decode step, one gate/up launch per layer each
-    assert n == 4 * small_engine.cfg.n_layers and t > 0
     small_engine.set_kernel_timing(-1)
+    small_engine.set_prefill(True)
+    # per-token path: 3 prompt positions + 1 decode step, one gate/up launch
+    # per layer each; with prefill the first two prompt tokens go through the
+    # batched GEMMs (not timed classes)
+    assert n == (2 if prefill else 4) * small_engine.cfg.n_layers and t > 0
 
 
 def _sha(a):
