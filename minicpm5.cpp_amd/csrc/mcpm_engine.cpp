@@ -14,6 +14,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 #include <vector>
 
@@ -42,7 +43,15 @@ struct PrefillBufs {
   _Float16 *xh = nullptr, *xbs = nullptr;
   float* xd = nullptr;
 };
-constexpr int PREFILL_MAX_TOKENS = 256;  // tokens per batched pass
+// Tokens per batched pass (MCPM_PREFILL_CHUNK overrides, a tuning aid).
+int prefill_chunk() {
+  static const int v = [] {
+    const char* e = std::getenv("MCPM_PREFILL_CHUNK");
+    const int n = e ? std::atoi(e) : 0;
+    return n >= 16 && n <= 4096 ? n : 1024;
+  }();
+  return v;
+}
 
 }  // namespace
 
@@ -501,10 +510,10 @@ int mcpm_engine_prefill(mcpm_engine* e, const int* tokens, int n, int pos0) {
   for (int i = 0; i < n; ++i)
     if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab) return fail(MCPM_ERR_ARG, "prefill token out of range");
   if (n == 0) return MCPM_OK;
-  int rc = ensure_prefill(e, std::min(n, PREFILL_MAX_TOKENS));
+  int rc = ensure_prefill(e, std::min(n, prefill_chunk()));
   if (rc) return rc;
-  for (int i = 0; i < n && !rc; i += PREFILL_MAX_TOKENS)
-    rc = prefill_pass(e, tokens + i, std::min(PREFILL_MAX_TOKENS, n - i), pos0 + i);
+  for (int i = 0; i < n && !rc; i += prefill_chunk())
+    rc = prefill_pass(e, tokens + i, std::min(prefill_chunk(), n - i), pos0 + i);
   if (rc) return rc;
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
   return MCPM_OK;

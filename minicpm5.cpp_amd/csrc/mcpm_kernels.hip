@@ -160,6 +160,13 @@ __host__ __device__ inline int attn_splits(int nch) {
   const int cps = attn_chunks_per_split(nch);
   return (nch + cps - 1) / cps;
 }
+// The split count is not monotonic in the chunk count (16 chunks take 16
+// splits, 18 take 9): a launch covers the most any count in [lo, hi] needs.
+inline int attn_max_splits(int lo, int hi) {
+  int m = 1;
+  for (int n = std::max(lo, 1); n <= hi; ++n) m = std::max(m, attn_splits(n));
+  return m;
+}
 
 // Maximum over the wave (order-free): lane moves within rows of 16, then
 // across rows.
@@ -351,7 +358,7 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, co
   if (head_dim <= 0 || head_dim > 128 || head_dim % 4 || n_heads % n_kv_heads ||
       n_heads / n_kv_heads > ATTN_MAX_GROUP)
     return hipErrorInvalidValue;
-  const dim3 grid(n_kv_heads, attn_splits(max_chunks));
+  const dim3 grid(n_kv_heads, attn_max_splits(1, max_chunks));
   if (head_dim <= 64)
     launch_kernel(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
                   max_chunks, part.o, part.mz, -1, size_t{0}, size_t{0}, size_t{0});
@@ -367,12 +374,9 @@ hipError_t launch_attention_batch(const float* q, const float* kc, const float* 
   if (head_dim <= 0 || head_dim > 128 || head_dim % 4 || n_heads % n_kv_heads ||
       n_heads / n_kv_heads > ATTN_MAX_GROUP || pos0 < 0)
     return hipErrorInvalidValue;
-  // enough splits for every token's chunk count (the split count is not
-  // monotonic in it); a token's surplus splits return at once
-  int max_splits = 1;
-  for (int n = pos0 / ATTN_CHUNK + 1; n <= (pos0 + n_tok - 1) / ATTN_CHUNK + 1; ++n)
-    max_splits = std::max(max_splits, attn_splits(n));
-  const dim3 grid(n_kv_heads, max_splits, n_tok);
+  // enough splits for every token's chunk count; a token's surplus splits
+  // return at once
+  const dim3 grid(n_kv_heads, attn_max_splits(pos0 / ATTN_CHUNK + 1, (pos0 + n_tok - 1) / ATTN_CHUNK + 1), n_tok);
   const size_t tok_q = static_cast<size_t>(n_heads) * head_dim;
   if (head_dim <= 64)
     hipLaunchKernelGGL(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, nullptr, n_heads, n_kv_heads, head_dim,

@@ -15,16 +15,21 @@
 //    weight code and B = activation code.  Every product is an integer of at
 //    most 2048 in magnitude (exact in fp16) and every sum stays below 2^24
 //    (exact in fp32), so the MFMA result is isum[m] itself.  Q4_K: sc*q <= 945.
-//    Q6_K: the reference sums sc*q*x over lane m's bytes (q in 0..63, low 4
-//    bits ql, high 2 bits qh) and subtracts 32*(sc[2m]*bsums[2m] +
-//    sc[2m+1]*bsums[2m+1]) -- sub-block m's offset, added into lane m.  Three
-//    MFMAs give sum(sc*ql*x) (|sc*ql| <= 1920), sum(sc*qh*x) (|sc*qh| <= 384)
-//    and sc[2m]*bsums[2m] + sc[2m+1]*bsums[2m+1] exactly; they are combined
-//    in int32 (16*hi + lo - 32*c) and converted to float as the reference's
-//    int32 lane sum is.
+//    Q6_K: the reference sums sc*q*x over lane m's bytes (q in 0..63) and
+//    subtracts 32*(sc[2m]*bsums[2m] + sc[2m+1]*bsums[2m+1]) -- sub-block m's
+//    offset, added into lane m -- then converts the int32 sum to float.
+//    Written as P + 32*(E - C): P = sum over lane m of sc*(q-32)*x (q - 32 =
+//    ql + 16*(qh - 2), ql the low 4 bits, qh the high 2: two MFMAs with
+//    |sc*ql| <= 1920 and |sc*(qh-2)| <= 256, joined by one fma; |P| < 2^24 so
+//    it is exact), E = sum over lane m of sc*x and C = sub-block m's
+//    sc*bsums pair (one MFMA each, C fed in as E's accumulator, |E - C| <
+//    2^20).  The final fp32 add rounds P + 32*(E - C) once, to nearest even,
+//    as the reference's int32 -> float conversion of the same integer does.
 //  * Q4_K's min sum (sum over sub-blocks of mn * pair-sum of bsums) is one
 //    more MFMA: A = mn[k/2] for k < 16, B = bsums[k].
 // Attention per token is the decode kernel at that token's position.
+#include <cstdlib>
+
 #include "mcpm_device.h"
 
 namespace mcpm {
@@ -161,6 +166,7 @@ __global__ void __launch_bounds__(256) k_gemm_q8k(const GemmArgs a) {
   for (int n = 0; n < NT; ++n) tok[n] = min(t0 + 16 * n + c16, a.n_tok - 1);
 
   const h2 off1024{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  const h2 off1026{static_cast<_Float16>(1026.0f), static_cast<_Float16>(1026.0f)};
   const f32x4 zero4{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int b = 0; b < a.nb; ++b) {
@@ -179,7 +185,7 @@ __global__ void __launch_bounds__(256) k_gemm_q8k(const GemmArgs a) {
       }
     }
     // A operands of the eight lane groups (and Q4_K's min operand)
-    h8 A[8], AH[8], AM, AC[8];
+    h8 A[8], AH[8], AM, AC[8], AS[8];
     if constexpr (WT == 0) {
       const u32x4 hdr = *reinterpret_cast<const u32x4*>(a.w.p1 + (static_cast<size_t>(b) * rows + ra) * 16);
       const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
@@ -216,7 +222,7 @@ __global__ void __launch_bounds__(256) k_gemm_q8k(const GemmArgs a) {
         const uint32_t w2 = scall[m >> 1];
         const int lo = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1), 8);
         const int hi = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1) + 8, 8);
-        const h2 pair{static_cast<_Float16>(static_cast<float>(lo)), static_cast<_Float16>(static_cast<float>(hi))};
+        const h2 pair{static_cast<_Float16>(static_cast<float>(-lo)), static_cast<_Float16>(static_cast<float>(-hi))};
         AC[m] = g == 0 ? __builtin_bit_cast(h8, u32x4{h2bits(pair), 0u, 0u, 0u}) : h8{};
       }
       h2 sc[4];
@@ -245,7 +251,8 @@ __global__ void __launch_bounds__(256) k_gemm_q8k(const GemmArgs a) {
       for (int m = 0; m < 8; ++m) {
         const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)];
         A[m] = a_operand((lw[m] >> nib) & 0x0f0f0f0fu, (lw[8 + m] >> nib) & 0x0f0f0f0fu, sa, sb, off1024);
-        AH[m] = a_operand((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, off1024);
+        AH[m] = a_operand((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, off1026);
+        AS[m] = __builtin_bit_cast(h8, u32x4{h2bits(sa), h2bits(sa), h2bits(sb), h2bits(sb)});
       }
     }
 
@@ -286,12 +293,10 @@ __global__ void __launch_bounds__(256) k_gemm_q8k(const GemmArgs a) {
         if constexpr (WT == 1) {
           const f32x4 DH = __builtin_amdgcn_mfma_f32_16x16x32_f16(AH[m], B, zero4, 0, 0, 0);
           const h8 BC = g == 0 ? __builtin_bit_cast(h8, u32x4{bsw[m], 0u, 0u, 0u}) : h8{};
-          const f32x4 DC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC[m], BC, zero4, 0, 0, 0);
+          const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC[m], BC, zero4, 0, 0, 0);  // -C
+          const f32x4 EC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AS[m], B, NC, 0, 0, 0);      // E - C
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int isum = (static_cast<int>(DH[i]) << 4) + static_cast<int>(D[i]) - 32 * static_cast<int>(DC[i]);
-            D[i] = static_cast<float>(isum);
-          }
+          for (int i = 0; i < 4; ++i) D[i] = __builtin_fmaf(32.0f, EC[i], __builtin_fmaf(16.0f, DH[i], D[i]));
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[n][m][i] = __builtin_fmaf(ds[i], D[i], acc[n][m][i]);
@@ -396,11 +401,21 @@ hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const Qu
                            bool add, hipStream_t s) {
   if (w.type != MCPM_TYPE_Q4_K && w.type != MCPM_TYPE_Q6_K) return hipErrorInvalidValue;
   GemmArgs a{w, rows, nb, n_tok, q.xh, q.xd, q.xbs, out, ld_out, add ? 1 : 0};
-  constexpr int NT = 2;
+  // token tiles per wave (MCPM_PREFILL_NT=2|4 overrides, a tuning aid)
+  static const int nt_env = [] {
+    const char* v = std::getenv("MCPM_PREFILL_NT");
+    return v ? std::atoi(v) : 0;
+  }();
+  const int NT = nt_env == 2 || nt_env == 4 ? nt_env : 2;
   const int n_tiles = ((rows + 15) / 16) * ((n_tok + 16 * NT - 1) / (16 * NT));
   const dim3 grid((n_tiles + 3) / 4);
-  if (w.type == MCPM_TYPE_Q4_K) launch_kernel(k_gemm_q8k<0, NT>, grid, dim3(256), 0, s, a);
-  else launch_kernel(k_gemm_q8k<1, NT>, grid, dim3(256), 0, s, a);
+  if (NT == 4) {
+    if (w.type == MCPM_TYPE_Q4_K) launch_kernel(k_gemm_q8k<0, 4>, grid, dim3(256), 0, s, a);
+    else launch_kernel(k_gemm_q8k<1, 4>, grid, dim3(256), 0, s, a);
+  } else {
+    if (w.type == MCPM_TYPE_Q4_K) launch_kernel(k_gemm_q8k<0, 2>, grid, dim3(256), 0, s, a);
+    else launch_kernel(k_gemm_q8k<1, 2>, grid, dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 

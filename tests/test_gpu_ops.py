@@ -219,12 +219,18 @@ def test_rope(ctx, orc, pos):
     assert_bits(ctx.download(vd, np.float32, 2048), want)
 
 
-@pytest.mark.parametrize("ctxlen", [0, 1, 63, 64, 65, 511, 2048, 4096])
+# (position, KV capacity): the launch covers the splits of every chunk count
+# up to the capacity's, which is not monotonic (16 chunks take 16 splits, 18
+# take 9), so positions well below a capacity of 17-32 chunks are included
+ATTN_CASES = [(c, c + 3) for c in (0, 1, 63, 64, 65, 511, 2048, 4096)] + [(700, 1152), (1000, 1536), (960, 2000)]
+
+
+@pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: f"pos{c[0]}-cap{c[1]}")
 @pytest.mark.parametrize("heads", [(32, 8, 64), (16, 2, 128)])
-def test_attention(ctx, orc, ctxlen, heads):
+def test_attention(ctx, orc, case, heads):
     nh, nkv, hd = heads
+    ctxlen, ms = case
     rng = np.random.default_rng(ctxlen * 3 + nh)
-    ms = ctxlen + 3
     q = rand_act(rng, nh * hd)
     k = rand_act(rng, nkv * hd)
     v = rand_act(rng, nkv * hd)

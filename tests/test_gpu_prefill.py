@@ -16,8 +16,9 @@ pytestmark = pytest.mark.gpu
 CASES = [
     (2, 2304, 32, 8, 64, 5760, 4096, 0, 100),   # 2.4B layer shape, Q6_K v/down, crosses a 64-position chunk
     (3, 2304, 32, 8, 64, 5760, 4096, 1, 40),    # llama-style mix: Q4_K down in some layers
-    (2, 512, 8, 2, 64, 1400, 2000, 0, 300),     # q-dim 512 (2 blocks); two batched passes (256 + 44)
+    (2, 512, 8, 2, 64, 1400, 2000, 0, 300),     # q-dim 512 (2 blocks), 5 attention chunks
     (2, 256, 4, 2, 64, 512, 300, 0, 130),       # q-dim 256 (1 block), ffn padded 512
+    (2, 512, 8, 2, 64, 1400, 2000, 0, 1100),    # two batched passes (1024 + 75 tokens), 18 chunks
 ]
 
 
