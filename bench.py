@@ -27,6 +27,7 @@ sys.path.insert(0, os.path.join(ROOT, "minicpm5.cpp_amd", "python"))
 import mcpm  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16
 # HBM bytes per launch by kernel class from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # runs, scaled by the same counters on a device copy of known size
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_2p4b_traffic.json")
@@ -53,6 +54,41 @@ def kernel_breakdown(eng, n_tokens=8):
                      "us_per_token": per_launch_us * launches_per_token,
                      "bytes_per_launch": eng.kernel_bytes(kc)}
     return out
+
+
+def prefill_measure(eng, cfg, n_prompt=1024, reps=3):
+    """The long-context configuration's prompt: n_prompt random token ids
+    through the batched prefill (MFMA GEMMs).  Times the prefill of the first
+    n_prompt-1 tokens (KV cache only) and the time to the first token (that
+    prefill plus the last prompt token's forward and argmax)."""
+    eng.init_kv_cache(1536)
+    prompt = np.random.default_rng(SEED + 1).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    eng.prefill(prompt[:n_prompt - 1])
+    eng.sync()
+    t_pf, t_ttft = [], []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        eng.prefill(prompt[:n_prompt - 1])
+        eng.sync()
+        t_pf.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        eng.generate_greedy(prompt, 1)
+        eng.sync()
+        t_ttft.append(time.perf_counter() - t0)
+    pf, ttft = float(np.median(t_pf)), float(np.median(t_ttft))
+    # algorithmic GEMM work: every layer's projections for n_prompt-1 tokens,
+    # the last layer's q/k/v only (nothing after them reaches the KV cache)
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    qkv = (qd + 2 * kvd) * cfg.dim
+    layer = qkv + cfg.dim * qd + 2 * cfg.ffn * cfg.dim + cfg.dim * cfg.ffn
+    macs = (n_prompt - 1) * ((cfg.n_layers - 1) * layer + qkv)
+    tflops = 2.0 * macs / pf / 1e12
+    return {"prompt_tokens": n_prompt, "prefill_ms": round(pf * 1e3, 2),
+            "prefill_tokens_per_s": round((n_prompt - 1) / pf, 1),
+            "time_to_first_token_ms": round(ttft * 1e3, 2),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": FP16_MFMA_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4),
+                         "flop_per_pass": 2 * macs}}
 
 
 def cpu_baseline(image, cfg_vocab, budget_s=15.0):
@@ -92,6 +128,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mix", type=int, default=0, help="0: Q6_K v/down in every layer; 1: llama.cpp layers")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of a graph replay")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 1024-token prefill measurement")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run device-to-device copies of this many MB (the reference kernel of known "
                          "size for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -148,6 +185,13 @@ def main():
         dst.free()
         log(f"copy calibration: 4 device copies of {args.copy_calibration_mb} MiB")
 
+    prefill = None
+    if not args.no_prefill:
+        prefill = prefill_measure(eng, cfg)
+        log(f"prefill: {prefill['prompt_tokens'] - 1} tokens in {prefill['prefill_ms']:.1f} ms -> "
+            f"{prefill['prefill_tokens_per_s']:.0f} tok/s ({prefill['roofline']['achieved']:.1f} TFLOP/s), "
+            f"first token after {prefill['time_to_first_token_ms']:.1f} ms")
+
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -185,6 +229,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 3)},
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(res), flush=True)
     eng.free()

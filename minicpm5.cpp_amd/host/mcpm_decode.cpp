@@ -2,10 +2,11 @@
 // the reference's driver calls forward() (src/chat_session.cpp:154-186):
 // every prompt token at positions 0.., then the argmax of each step's logits
 // fed back.  --device-loop runs the same decode with the argmax on the GPU
-// (no logits copy per token).
+// (no logits copy per token); --prefill sends all prompt tokens but the last
+// through the batched prefill before the per-token loop.
 //
 //   mcpm_decode (--gguf FILE | --synth SEED [--layers N] [--vocab N])
-//               [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--verbose]
+//               [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--prefill] [--verbose]
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -19,14 +20,14 @@
 static void usage() {
     std::fprintf(stderr,
                  "usage: mcpm_decode (--gguf FILE | --synth SEED [--layers N] [--vocab N])\n"
-                 "                   [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--verbose]\n");
+                 "                   [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--prefill] [--verbose]\n");
 }
 
 int main(int argc, char** argv) {
     std::string gguf;
     long long synth_seed = -1;
     int layers = 40, vocab = 130560, n_prompt = 32, n_tokens = 64;
-    bool device_loop = false, verbose = false;
+    bool device_loop = false, verbose = false, use_prefill = false;
     std::vector<int> prompt_ids;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
@@ -56,6 +57,7 @@ int main(int argc, char** argv) {
         }
         else if (a == "--tokens") n_tokens = std::atoi(next());
         else if (a == "--device-loop") device_loop = true;
+        else if (a == "--prefill") use_prefill = true;
         else if (a == "--verbose") verbose = true;
         else {
             usage();
@@ -120,7 +122,12 @@ int main(int argc, char** argv) {
             return static_cast<int>(b);
         };
         int pos = 0, next = 0;
-        for (int t : prompt) next = argmax(engine.forward(t, pos++, max_seq));
+        if (use_prefill && prompt.size() > 1) {
+            engine.prefill(std::vector<int>(prompt.begin(), prompt.end() - 1), 0);
+            pos = static_cast<int>(prompt.size()) - 1;
+        }
+        for (size_t i = static_cast<size_t>(pos); i < prompt.size(); ++i)
+            next = argmax(engine.forward(prompt[i], pos++, max_seq));
         const auto t1 = std::chrono::steady_clock::now();
         out.push_back(next);
         while (static_cast<int>(out.size()) < n_tokens) {

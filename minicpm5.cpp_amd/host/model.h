@@ -24,8 +24,14 @@ public:
     // logits (the reference's execute_attention warns and continues).
     const std::vector<float>& forward(int token_id, int pos, int max_seq_len);
 
-    // Feeds prompt at positions 0.., then returns n_gen greedy tokens.
+    // Feeds prompt at positions 0.., then returns n_gen greedy tokens (all
+    // prompt tokens but the last go through prefill()).
     std::vector<int> generate_greedy(const std::vector<int>& prompt, int n_gen);
+    // Fills the KV cache for tokens at positions pos0.. in batched passes
+    // (MFMA GEMMs), exactly as forward() per token would, without logits.  A
+    // chat driver keeps the cache across turns and prefills only the new
+    // tokens (pos0 = tokens already cached) instead of re-running the history.
+    void prefill(const std::vector<int>& tokens, int pos0);
     // A synthetic model image (seeded random weights, BASELINE shapes).
     bool load_synthetic(const mcpm_model_config& cfg, uint64_t seed, int mix, bool verbose = false);
     const mcpm_model_config& config() const { return cfg_; }

@@ -75,6 +75,11 @@ const std::vector<float>& MiniCPM5Engine::forward(int token_id, int pos, int max
     return logits_;
 }
 
+void MiniCPM5Engine::prefill(const std::vector<int>& tokens, int pos0) {
+    if (!engine_) throw std::runtime_error("prefill: no model loaded");
+    check(mcpm_engine_prefill(engine_, tokens.data(), static_cast<int>(tokens.size()), pos0), "mcpm_engine_prefill");
+}
+
 std::vector<int> MiniCPM5Engine::generate_greedy(const std::vector<int>& prompt, int n_gen) {
     if (!engine_) throw std::runtime_error("generate_greedy: no model loaded");
     std::vector<int> out(static_cast<size_t>(n_gen > 0 ? n_gen : 0));

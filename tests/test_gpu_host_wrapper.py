@@ -121,16 +121,16 @@ def test_ops_mirror_matches_oracle(orc, tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("device_loop", [False, True])
-def test_engine_mirror_greedy_matches_oracle(device_loop):
+@pytest.mark.parametrize("mode", ["forward", "prefill", "device-loop"])
+def test_engine_mirror_greedy_matches_oracle(mode):
     import oracle as O
     cfg = mcpm.make_config(2, 2304, 32, 8, 64, 5760, 4096)
     seed, prompt, n_gen = 7, [5, 1000, 77, 4095, 12], 12
-    announce(f"mcpm_decode device_loop={device_loop}")
+    announce(f"mcpm_decode {mode}")
     cmd = [DECODE, "--synth", str(seed), "--layers", "2", "--vocab", "4096",
            "--prompt-ids", ",".join(map(str, prompt)), "--tokens", str(n_gen)]
-    if device_loop:
-        cmd.append("--device-loop")
+    if mode != "forward":
+        cmd.append("--" + mode)
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr
     line = next(l for l in r.stdout.splitlines() if l.startswith("tokens:"))
