@@ -20,8 +20,9 @@
 //         (isum[8], d_x*d_w, d_x*dmin_w, minsum) per (block, slot) in LDS,
 //         then 4 lanes per row run the chain over the blocks in order.
 // Each wave streams its (item, step) sequence through two register sets,
-// loading one step ahead.  Every load is unconditional: rows, blocks and
-// steps past the end are clamped into the tensor and their results masked.
+// loading one step ahead.  Loads are unconditional within a path: rows and
+// blocks past the end are clamped into the tensor and their results masked;
+// waves of one or two steps load no step past their last.
 // Work groups share the activations (prologue) and nothing else.
 #include <algorithm>
 #include <cstdlib>
@@ -574,13 +575,16 @@ __device__ __forceinline__ float hsum8(const float (&acc)[8]) {
 }
 
 // ---------------------------------------------------------------- kernel ---
-// TILE: S slots per item, KB steps per item.  ROW: S = 64, KB = nb.
+// TILE: S slots per item, KB steps per item, 4 waves.  ROW: S = 64, KB = nb,
+// 4..8 waves.  TILE's bound of 4 waves lets a wave hold up to 512 registers
+// (VGPRs and AGPRs), so its step registers never go to scratch.
 template <int PRO, int EPI, bool TILE, int WT>
-__global__ void __launch_bounds__(64 * GEMV_MAX_WAVES) k_gemv(const GemvArgs a, int n_items, int S, int KB) {
+__global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES))
+    k_gemv(const GemvArgs a, int n_items, int S, int KB) {
   extern __shared__ uint32_t L[];
   const int lane = threadIdx.x & 63;
   const int wave = sgpr(static_cast<int>(threadIdx.x >> 6));
-  const int NW = static_cast<int>(blockDim.x >> 6);  // 4..8 waves
+  const int NW = TILE ? GEMV_TILE_WAVES : static_cast<int>(blockDim.x >> 6);
   const int nb = a.nb;
   const LdsPlan P = lds_plan(nb, S, TILE, PRO == PRO_ATTN_EVEN, NW);
   const int stride = gridDim.x * NW;
@@ -788,18 +792,33 @@ __global__ void __launch_bounds__(64 * GEMV_MAX_WAVES) k_gemv(const GemvArgs a, 
     }
   };
 
-  // two register sets used in turn: a copy between them would wait for the
-  // loads still landing in the source
-  for (int t = 0; t < n_steps; t += 2) {
-    t1 = ref_at(t + 1, b1, s1);
-    prefetch_epi(t + 1, e1);
+  // TILE waves of one or two steps (every launch whose items fit the grid)
+  // take straight-line paths that load nothing past their last step: issuing
+  // a block's 9-13 vector loads holds a wave for ~0.6-1 us, so a re-read of
+  // a clamped step is not free.  (Loads under a branch inside the loop would
+  // make the compiler's wait at the join cover the loads of both paths.)
+  if (TILE && n_steps == 1) {
+    consume(K0, e0, t0, 0, b0, s0);
+  } else if (TILE && n_steps == 2) {
+    t1 = ref_at(1, b1, s1);
+    prefetch_epi(1, e1);
     load_blk(K1, t1, min(b1, nb - 1));
-    consume(K0, e0, t0, t, b0, s0);
-    if (t + 1 >= n_steps) break;
-    t0 = ref_at(t + 2, b0, s0);
-    prefetch_epi(t + 2, e0);
-    load_blk(K0, t0, min(b0, nb - 1));
-    consume(K1, e1, t1, t + 1, b1, s1);
+    consume(K0, e0, t0, 0, b0, s0);
+    consume(K1, e1, t1, 1, b1, s1);
+  } else {
+    // two register sets used in turn: a copy between them would wait for the
+    // loads still landing in the source
+    for (int t = 0; t < n_steps; t += 2) {
+      t1 = ref_at(t + 1, b1, s1);
+      prefetch_epi(t + 1, e1);
+      load_blk(K1, t1, min(b1, nb - 1));
+      consume(K0, e0, t0, t, b0, s0);
+      if (t + 1 >= n_steps) break;
+      t0 = ref_at(t + 2, b0, s0);
+      prefetch_epi(t + 2, e0);
+      load_blk(K0, t0, min(b0, nb - 1));
+      consume(K1, e1, t1, t + 1, b1, s1);
+    }
   }
 
   if constexpr (EPI == EPI_LOGITS) {
@@ -846,9 +865,9 @@ int waves_for(int items, int n_cu) { return std::min(GEMV_MAX_WAVES, std::max(4,
 // runs of each chunk plane), then the smallest S (least work per wave).  S is
 // even where rows pair up (RoPE, gate/up) and S*nb <= 64*KB.
 //
-// MCPM_GEMV_SHAPE_<QKV|OPROJ|GATE_UP|DOWN|LM|OTHER>="KB,S,NW" (KB 0: ROW)
-// overrides the choice for one class of launch: a tuning aid for measuring
-// shapes against each other.
+// MCPM_GEMV_SHAPE_<QKV|OPROJ|GATE_UP|DOWN|LM|OTHER>="KB,S,NW" (KB 0: ROW;
+// NW counts for ROW only, TILE always runs 4 waves) overrides the choice for
+// one class of launch: a tuning aid for measuring shapes against each other.
 const char* shape_env(int prologue, int epilogue) {
   const char* name = "MCPM_GEMV_SHAPE_OTHER";
   if (epilogue == EPI_QKV) name = "MCPM_GEMV_SHAPE_QKV";
@@ -866,14 +885,14 @@ Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
     if (std::sscanf(env, "%d,%d,%d", &kb, &s, &nw) >= 1 && nw >= 4 && nw <= GEMV_MAX_WAVES) {
       if (kb == 0) return Shape{false, 64, nb, nw};
       if (kb > 0 && kb <= 4 && s >= 1 && s <= 64 && !(paired && s % 2) && s * nb <= 64 * kb)
-        return Shape{true, s, kb, nw};
+        return Shape{true, s, kb, GEMV_TILE_WAVES};
     }
   }
   const int cap = 4 * n_cu;
   const int row_items = items_for(a, 64);
   if (row_items >= cap) return Shape{false, 64, nb, waves_for(row_items, n_cu)};
   for (int kb = 1; kb <= 4; ++kb) {
-    Shape best{true, 0, kb, 4};
+    Shape best{true, 0, kb, GEMV_TILE_WAVES};
     for (int S = paired ? 2 : 1; S * nb <= 64 * kb && S <= 64; S += paired ? 2 : 1) {
       if (items_for(a, S) > cap) continue;
       if (best.S == 0 || (S % 4 == 0 && best.S % 4 != 0)) best.S = S;
@@ -882,7 +901,7 @@ Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
   }
   // nothing fits: the largest items, waves looping over them
   const int S = std::min(64, (256 / nb) & (paired ? ~1 : ~0));
-  return Shape{true, std::max(S, paired ? 2 : 1), 4, GEMV_MAX_WAVES};
+  return Shape{true, std::max(S, paired ? 2 : 1), 4, GEMV_TILE_WAVES};
 }
 
 size_t lds_bytes(const GemvArgs& a, const Shape& sh, int prologue) {
@@ -912,6 +931,7 @@ int n_items_of(GemvArgs& a, const Shape& sh) {
 
 template <int PRO, int EPI, bool TILE, int WT>
 hipError_t launch_one(const GemvArgs& a, int n_items, const Shape& sh, int n_cu, size_t lds, hipStream_t s) {
+  if (TILE && sh.NW != GEMV_TILE_WAVES) return hipErrorInvalidValue;  // the kernel's launch bound
   const int grid = grid_for<PRO, EPI, TILE, WT>(n_items, sh, n_cu, lds);
   if (grid <= 0) return hipSuccess;
   launch_kernel(k_gemv<PRO, EPI, TILE, WT>, dim3(grid), dim3(64 * sh.NW), lds, s, a, n_items, sh.S, sh.KB);
