@@ -578,22 +578,27 @@ __device__ __forceinline__ float hsum8(const float (&acc)[8]) {
 // TILE: S slots per item, KB steps per item, 4 waves.  ROW: S = 64, KB = nb,
 // 4..8 waves.  TILE's bound of 4 waves lets a wave hold up to 512 registers
 // (VGPRs and AGPRs), so its step registers never go to scratch.
-template <int PRO, int EPI, bool TILE, int WT>
+// GRP (with TILE): the item belongs to the work group, its pairs spread over
+// the 4 waves (pair q = lane + 64*wave + 256*k), one chain area in LDS that
+// wave 0 runs after a work-group barrier.  It gives each SIMD one step where
+// a wave-sized item would need two (the down projection: 23 blocks).
+template <int PRO, int EPI, bool TILE, int WT, bool GRP = false>
 __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES))
     k_gemv(const GemvArgs a, int n_items, int S, int KB) {
+  static_assert(TILE || !GRP, "GRP is a TILE shape");
   extern __shared__ uint32_t L[];
   const int lane = threadIdx.x & 63;
   const int wave = sgpr(static_cast<int>(threadIdx.x >> 6));
   const int NW = TILE ? GEMV_TILE_WAVES : static_cast<int>(blockDim.x >> 6);
   const int nb = a.nb;
-  const LdsPlan P = lds_plan(nb, S, TILE, PRO == PRO_ATTN_EVEN, NW);
-  const int stride = gridDim.x * NW;
+  const LdsPlan P = lds_plan(nb, S, TILE, PRO == PRO_ATTN_EVEN, GRP ? 1 : NW);
+  const int stride = GRP ? gridDim.x : gridDim.x * NW;
   const Region A = region_of(a.reg[0]), B = region_of(a.reg[1]), C = region_of(a.reg[2]);
 
   // This wave's steps: item first + (t / KB) * stride, step t % KB.  Steps
   // past the last re-read the last one (cached, results unused), so every
   // load is issued unconditionally and no wait depends on a branch.
-  const int first = blockIdx.x * NW + wave;
+  const int first = GRP ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) * NW + wave;
   const int n_mine = first < n_items ? (n_items - 1 - first) / stride + 1 : 0;
   const int n_steps = n_mine * KB;
   const float invS = 1.0f / static_cast<float>(S);
@@ -601,7 +606,7 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
   // slot and block of this lane at step k of an item
   auto slot_at = [&](int k, int& s, int& b) {
     if constexpr (TILE) {
-      const int q = lane + 64 * k;
+      const int q = GRP ? lane + 64 * wave + 256 * k : lane + 64 * k;
       const int bq = static_cast<int>((static_cast<float>(q) + 0.5f) * invS);  // q / S, exact for q < 2^16
       s = q - bq * S;
       b = bq;
@@ -653,7 +658,7 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
   for (int m = 0; m < 8; ++m) acc[m] = 0.0f;
   float best_v = -__builtin_inff();
   int best_i = 0x7fffffff;
-  uint32_t* chain = L + P.u + wave * (nb * S * 12);  // TILE: entry (b, s) at (b*S + s)*12
+  uint32_t* chain = L + P.u + (GRP ? 0 : wave * (nb * S * 12));  // TILE: entry (b, s) at (b*S + s)*12
 
   // the epilogue for row value v of slot s of item `it`; lanes with s >= S
   // or an invalid row only take part in the shuffles before it
@@ -742,52 +747,57 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
         e[2] = u32x4{__float_as_uint(ds), __float_as_uint(dm), static_cast<uint32_t>(ms), 0u};
       }
       if (k == KB - 1) {
-        wave_sync();
-        // 4 lanes per row (lane = 4*row + c, S/16 passes) run the chain, lane c
-        // the accumulators of lane sums c and c+4; the row values go to vrow
-        // for the epilogue's RoPE and gate/up partners
-        const int c = lane & 3;
-        float* vrow = reinterpret_cast<float*>(L + P.vrow) + wave * 64;
+        // GRP: every wave's entries are in before wave 0 runs the chain
+        if constexpr (GRP) __syncthreads();
+        else wave_sync();
+        if (!GRP || wave == 0) {
+          // 4 lanes per row (lane = 4*row + c, S/16 passes) run the chain, lane c
+          // the accumulators of lane sums c and c+4; the row values go to vrow
+          // for the epilogue's RoPE and gate/up partners
+          const int c = lane & 3;
+          float* vrow = reinterpret_cast<float*>(L + P.vrow) + wave * 64;
 #pragma unroll 1
-        for (int pass = 0; pass * 16 < S; ++pass) {
-          const int sr = pass * 16 + (lane >> 2);
-          const int src = min(sr, S - 1);
-          float a0 = 0.0f, a1 = 0.0f, am = 0.0f;
-          // four blocks' entries read at once, then their fma steps in order
+          for (int pass = 0; pass * 16 < S; ++pass) {
+            const int sr = pass * 16 + (lane >> 2);
+            const int src = min(sr, S - 1);
+            float a0 = 0.0f, a1 = 0.0f, am = 0.0f;
+            // four blocks' entries read at once, then their fma steps in order
 #pragma unroll 1
-          for (int bq = 0; bq < nb; bq += 4) {
-            int i0[4], i1[4];
-            f32x4 dv[4];  // (d_x*d_w, d_x*dmin_w, minsum, -)
+            for (int bq = 0; bq < nb; bq += 4) {
+              int i0[4], i1[4];
+              f32x4 dv[4];  // (d_x*d_w, d_x*dmin_w, minsum, -)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              const uint32_t* e = chain + (min(bq + k, nb - 1) * S + src) * 12;
-              i0[k] = static_cast<int>(e[c]);
-              i1[k] = static_cast<int>(e[c + 4]);
-              dv[k] = *reinterpret_cast<const f32x4*>(e + 8);
-            }
+              for (int k = 0; k < 4; ++k) {
+                const uint32_t* e = chain + (min(bq + k, nb - 1) * S + src) * 12;
+                i0[k] = static_cast<int>(e[c]);
+                i1[k] = static_cast<int>(e[c + 4]);
+                dv[k] = *reinterpret_cast<const f32x4*>(e + 8);
+              }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              if (bq + k < nb) {
-                a0 = __builtin_fmaf(dv[k].x, static_cast<float>(i0[k]), a0);
-                a1 = __builtin_fmaf(dv[k].x, static_cast<float>(i1[k]), a1);
-                am = __builtin_fmaf(-dv[k].y, static_cast<float>(__float_as_int(dv[k].z)), am);
+              for (int k = 0; k < 4; ++k) {
+                if (bq + k < nb) {
+                  a0 = __builtin_fmaf(dv[k].x, static_cast<float>(i0[k]), a0);
+                  a1 = __builtin_fmaf(dv[k].x, static_cast<float>(i1[k]), a1);
+                  am = __builtin_fmaf(-dv[k].y, static_cast<float>(__float_as_int(dv[k].z)), am);
+                }
               }
             }
+            // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) on lane c == 0
+            float v = a0 + a1;
+            v = v + __shfl_down(v, 2);
+            v = v + __shfl_down(v, 1);
+            if (t.q4) v = v + am;
+            if (c == 0 && sr < S) vrow[sr] = v;
           }
-          // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) on lane c == 0
-          float v = a0 + a1;
-          v = v + __shfl_down(v, 2);
-          v = v + __shfl_down(v, 1);
-          if (t.q4) v = v + am;
-          if (c == 0 && sr < S) vrow[sr] = v;
+          wave_sync();
+          const int se = min(lane, S - 1);
+          const float v = vrow[se];
+          const float partner = vrow[(se ^ 1) < S ? (se ^ 1) : se];
+          const float up = vrow[(se + S / 2) % S];
+          wave_sync();  // every read of the chain area precedes the next item's entries
+          epilogue(it, lane, v, partner, up, e);
         }
-        wave_sync();
-        const int se = min(lane, S - 1);
-        const float v = vrow[se];
-        const float partner = vrow[(se ^ 1) < S ? (se ^ 1) : se];
-        const float up = vrow[(se + S / 2) % S];
-        wave_sync();  // every read of the chain area precedes the next item's entries
-        epilogue(it, lane, v, partner, up, e);
+        if constexpr (GRP) __syncthreads();  // wave 0's chain reads precede the next item's entries
       }
     }
   };
@@ -842,7 +852,8 @@ namespace {
 struct Shape {
   bool tile;
   int S, KB;
-  int NW;  // waves per work group
+  int NW;            // waves per work group
+  bool grp = false;  // TILE items of a whole work group
 };
 
 int items_for(const GemvArgs& a, int S) {
@@ -865,9 +876,14 @@ int waves_for(int items, int n_cu) { return std::min(GEMV_MAX_WAVES, std::max(4,
 // runs of each chunk plane), then the smallest S (least work per wave).  S is
 // even where rows pair up (RoPE, gate/up) and S*nb <= 64*KB.
 //
-// MCPM_GEMV_SHAPE_<QKV|OPROJ|GATE_UP|DOWN|LM|OTHER>="KB,S,NW" (KB 0: ROW;
-// NW counts for ROW only, TILE always runs 4 waves) overrides the choice for
-// one class of launch: a tuning aid for measuring shapes against each other.
+// GRP when those TILE items need two or more steps but work-group items (S
+// rows, S*nb <= 256 pairs, one step per wave) fit one work group per CU; for
+// launches whose epilogue needs no row pairs (residual, store).
+//
+// MCPM_GEMV_SHAPE_<QKV|OPROJ|GATE_UP|DOWN|LM|OTHER>="KB,S,NW" (KB 0: ROW; KB
+// < 0: GRP with -KB steps; NW counts for ROW only, TILE always runs 4 waves)
+// overrides the choice for one class of launch: a tuning aid for measuring
+// shapes against each other.
 const char* shape_env(int prologue, int epilogue) {
   const char* name = "MCPM_GEMV_SHAPE_OTHER";
   if (epilogue == EPI_QKV) name = "MCPM_GEMV_SHAPE_QKV";
@@ -880,12 +896,15 @@ const char* shape_env(int prologue, int epilogue) {
 Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
   const int nb = a.nb;
   const bool paired = a.pair || epilogue == EPI_QKV;
+  const bool grp_ok = !paired && (epilogue == EPI_RESID || epilogue == EPI_STORE);
   if (const char* env = shape_env(prologue, epilogue)) {
     int kb = -1, s = 0, nw = 4;
     if (std::sscanf(env, "%d,%d,%d", &kb, &s, &nw) >= 1 && nw >= 4 && nw <= GEMV_MAX_WAVES) {
       if (kb == 0) return Shape{false, 64, nb, nw};
       if (kb > 0 && kb <= 4 && s >= 1 && s <= 64 && !(paired && s % 2) && s * nb <= 64 * kb)
         return Shape{true, s, kb, GEMV_TILE_WAVES};
+      if (kb < 0 && kb >= -4 && grp_ok && s >= 1 && s <= 64 && s * nb <= 256 * -kb)
+        return Shape{true, s, -kb, GEMV_TILE_WAVES, true};
     }
   }
   const int cap = 4 * n_cu;
@@ -897,7 +916,11 @@ Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
       if (items_for(a, S) > cap) continue;
       if (best.S == 0 || (S % 4 == 0 && best.S % 4 != 0)) best.S = S;
     }
-    if (best.S) return best;
+    if (best.S) {
+      const int sg = std::min(64, 256 / nb);
+      if (kb >= 2 && grp_ok && sg >= 1 && items_for(a, sg) <= n_cu) return Shape{true, sg, 1, GEMV_TILE_WAVES, true};
+      return best;
+    }
   }
   // nothing fits: the largest items, waves looping over them
   const int S = std::min(64, (256 / nb) & (paired ? ~1 : ~0));
@@ -905,17 +928,19 @@ Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
 }
 
 size_t lds_bytes(const GemvArgs& a, const Shape& sh, int prologue) {
-  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, prologue == PRO_ATTN_EVEN, sh.NW).words) * 4;
+  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, prologue == PRO_ATTN_EVEN, sh.grp ? 1 : sh.NW).words) * 4;
 }
 
-template <int PRO, int EPI, bool TILE, int WT>
+template <int PRO, int EPI, bool TILE, int WT, bool GRP = false>
 int grid_for(int n_items, const Shape& sh, int n_cu, size_t lds) {
   int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_gemv<PRO, EPI, TILE, WT>),
-                                                   64 * sh.NW, lds) != hipSuccess || occ < 1)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &occ, reinterpret_cast<const void*>(k_gemv<PRO, EPI, TILE, WT, GRP>), 64 * sh.NW, lds) != hipSuccess ||
+      occ < 1)
     occ = 1;
   // one resident round of work groups: more would queue behind the first
-  return std::min((n_items + sh.NW - 1) / sh.NW, n_cu * occ);
+  const int per_group = GRP ? 1 : sh.NW;
+  return std::min((n_items + per_group - 1) / per_group, n_cu * occ);
 }
 
 // Items of the launch; in region mode also each region's first item.
@@ -929,12 +954,13 @@ int n_items_of(GemvArgs& a, const Shape& sh) {
   return n;
 }
 
-template <int PRO, int EPI, bool TILE, int WT>
+template <int PRO, int EPI, bool TILE, int WT, bool GRP = false>
 hipError_t launch_one(const GemvArgs& a, int n_items, const Shape& sh, int n_cu, size_t lds, hipStream_t s) {
   if (TILE && sh.NW != GEMV_TILE_WAVES) return hipErrorInvalidValue;  // the kernel's launch bound
-  const int grid = grid_for<PRO, EPI, TILE, WT>(n_items, sh, n_cu, lds);
+  if (GRP && (sh.S * a.nb > 256 * sh.KB || sh.S > 64)) return hipErrorInvalidValue;
+  const int grid = grid_for<PRO, EPI, TILE, WT, GRP>(n_items, sh, n_cu, lds);
   if (grid <= 0) return hipSuccess;
-  launch_kernel(k_gemv<PRO, EPI, TILE, WT>, dim3(grid), dim3(64 * sh.NW), lds, s, a, n_items, sh.S, sh.KB);
+  launch_kernel(k_gemv<PRO, EPI, TILE, WT, GRP>, dim3(grid), dim3(64 * sh.NW), lds, s, a, n_items, sh.S, sh.KB);
   return hipGetLastError();
 }
 
@@ -951,6 +977,11 @@ hipError_t launch_pe(const GemvArgs& a0, const Shape& sh, int n_cu, hipStream_t 
   const int n_items = n_items_of(a, sh);
   const size_t lds = lds_bytes(a, sh, PRO);
   const int wt = weight_kind(a);
+  if constexpr (EPI == EPI_RESID || EPI == EPI_STORE) {
+    if (sh.grp && wt == WT_Q4) return launch_one<PRO, EPI, true, WT_Q4, true>(a, n_items, sh, n_cu, lds, s);
+    if (sh.grp && wt == WT_Q6) return launch_one<PRO, EPI, true, WT_Q6, true>(a, n_items, sh, n_cu, lds, s);
+  }
+  if (sh.grp) return hipErrorInvalidValue;
 #define MCPM_WT(TT, WW) \
   if (sh.tile == TT && wt == WW) return launch_one<PRO, EPI, TT, WW>(a, n_items, sh, n_cu, lds, s);
   MCPM_WT(true, WT_Q4) MCPM_WT(true, WT_Q6) MCPM_WT(false, WT_Q4) MCPM_WT(false, WT_Q6)

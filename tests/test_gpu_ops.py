@@ -146,6 +146,36 @@ def test_gemv_q8k_bit_exact(ctx, orc, gtype, rows, cols):
     assert_bits(ctx.download(od2, np.float32, rows), want)
 
 
+# Work-group items forced through the shape override ("-KB,S": S rows, KB
+# steps per wave): a ragged last item (37 rows), one row per group with each
+# group looping over many items, two steps per wave, and 32 blocks per row.
+GRP_SHAPES = [(37, 2304, "-1,11"), (2304, 5888, "-1,1"), (2304, 5888, "-2,22"), (130, 8192, "-1,8"),
+              (1000, 2304, "-2,56")]
+
+
+@pytest.mark.parametrize("rows,cols,shape", GRP_SHAPES)
+@pytest.mark.parametrize("gtype", [mcpm.TYPE_Q4_K, mcpm.TYPE_Q6_K])
+def test_gemv_group_items_bit_exact(ctx, orc, monkeypatch, gtype, rows, cols, shape):
+    monkeypatch.setenv("MCPM_GEMV_SHAPE_OTHER", shape)
+    rng = np.random.default_rng(rows * 11 + cols)
+    nb = cols // 256
+    blk = (rand_q4k if gtype == mcpm.TYPE_Q4_K else rand_q6k)(rng, rows * nb, extreme=True)
+    x = rand_act(rng, cols)
+    xq = q8k_from(orc, x)
+    announce(f"gemv group items type={gtype} {rows}x{cols} shape={shape}")
+    t = ctx.tensor(blk, gtype, cols, rows)
+    want = np.zeros(rows, np.float32)
+    (orc.or_gemv_q4_K_q8_K if gtype == mcpm.TYPE_Q4_K else orc.or_gemv_q6_K_q8_K)(P(blk), P(xq), P(want), rows, cols)
+    od = ctx.zeros(rows * 4)
+    fn = ctx.lib.mcpm_gemv_q4_K_q8_K if gtype == mcpm.TYPE_Q4_K else ctx.lib.mcpm_gemv_q6_K_q8_K
+    mcpm.check(fn(ctx.h, t.h, up(ctx, xq).ptr, od.ptr, rows, cols))
+    assert_bits(ctx.download(od, np.float32, rows), want)
+    od2 = ctx.zeros(rows * 4)
+    fn2 = ctx.lib.mcpm_gemv_q4_K if gtype == mcpm.TYPE_Q4_K else ctx.lib.mcpm_gemv_q6_K
+    mcpm.check(fn2(ctx.h, t.h, up(ctx, x).ptr, od2.ptr, rows, cols))
+    assert_bits(ctx.download(od2, np.float32, rows), want)
+
+
 @pytest.mark.parametrize("v_type", [mcpm.TYPE_Q4_K, mcpm.TYPE_Q6_K])
 def test_qkv(ctx, orc, v_type):
     rng = np.random.default_rng(5 + v_type)
