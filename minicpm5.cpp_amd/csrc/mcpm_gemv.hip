@@ -88,6 +88,7 @@ __host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool attn,
 // (one Q8_K bsum group).  Blocks past nb re-read block nb-1 (in bounds,
 // results unused).
 constexpr int NR = (MAX_NB + 15) / 16;
+constexpr int CHAIN_BATCH = 12;  // TILE chain: blocks whose LDS entries are read together
 
 // PRO_ATTN_EVEN: thread t < 256 combines values t*nb .. t*nb+nb-1 (one head:
 // head_dim % nb == 0, nb <= 16) over the chunks, ATTN_RB chunks' o_c per load
@@ -761,20 +762,21 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
             const int sr = pass * 16 + (lane >> 2);
             const int src = min(sr, S - 1);
             float a0 = 0.0f, a1 = 0.0f, am = 0.0f;
-            // four blocks' entries read at once, then their fma steps in order
+            // CHAIN_BATCH blocks' entries read at once (one LDS round trip for
+            // up to 12 blocks), then their fma steps in order
 #pragma unroll 1
-            for (int bq = 0; bq < nb; bq += 4) {
-              int i0[4], i1[4];
-              f32x4 dv[4];  // (d_x*d_w, d_x*dmin_w, minsum, -)
+            for (int bq = 0; bq < nb; bq += CHAIN_BATCH) {
+              int i0[CHAIN_BATCH], i1[CHAIN_BATCH];
+              f32x4 dv[CHAIN_BATCH];  // (d_x*d_w, d_x*dmin_w, minsum, -)
 #pragma unroll
-              for (int k = 0; k < 4; ++k) {
+              for (int k = 0; k < CHAIN_BATCH; ++k) {
                 const uint32_t* e = chain + (min(bq + k, nb - 1) * S + src) * 12;
                 i0[k] = static_cast<int>(e[c]);
                 i1[k] = static_cast<int>(e[c + 4]);
                 dv[k] = *reinterpret_cast<const f32x4*>(e + 8);
               }
 #pragma unroll
-              for (int k = 0; k < 4; ++k) {
+              for (int k = 0; k < CHAIN_BATCH; ++k) {
                 if (bq + k < nb) {
                   a0 = __builtin_fmaf(dv[k].x, static_cast<float>(i0[k]), a0);
                   a1 = __builtin_fmaf(dv[k].x, static_cast<float>(i1[k]), a1);
@@ -782,10 +784,11 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
                 }
               }
             }
-            // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) on lane c == 0
+            // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) on lane c == 0, the partner
+            // lanes 4r+2 and 4r+1 read by DPP row shifts
             float v = a0 + a1;
-            v = v + __shfl_down(v, 2);
-            v = v + __shfl_down(v, 1);
+            v = v + dpp_f<0x102>(v);  // row_shl:2
+            v = v + dpp_f<0x101>(v);  // row_shl:1
             if (t.q4) v = v + am;
             if (c == 0 && sr < S) vrow[sr] = v;
           }
