@@ -91,6 +91,33 @@ def prefill_measure(eng, cfg, n_prompt=1024, reps=3):
                          "flop_per_pass": 2 * macs}}
 
 
+def sampled_measure(eng, cfg, n_prompt=1024, n_gen=512, temperature=0.8, top_p=0.95):
+    """The long-context configuration's decode: after an n_prompt-token prompt
+    (batched prefill), n_gen tokens drawn by the device sampler (temperature,
+    top-p), the KV cache growing to n_prompt + n_gen.  The decode rate is
+    (n_gen - 1) over the difference between the n_gen-token and the 1-token
+    runs (both include the same prefill); the greedy loop at the same
+    positions is timed the same way, for the sampler's share."""
+    eng.init_kv_cache(n_prompt + n_gen + 4)
+    prompt = np.random.default_rng(SEED + 2).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+
+    def run(fn, n):
+        t0 = time.perf_counter()
+        fn(n)
+        eng.sync()
+        return time.perf_counter() - t0
+
+    sampled = lambda n: eng.generate_sampled(prompt, n, temperature, top_p, SEED)
+    greedy = lambda n: eng.generate_greedy(prompt, n)
+    run(sampled, 8)  # warm-up: graphs, sampler scratch
+    ts = run(sampled, n_gen) - run(sampled, 1)
+    tg = run(greedy, n_gen) - run(greedy, 1)
+    return {"prompt_tokens": n_prompt, "tokens": n_gen, "temperature": temperature, "top_p": top_p,
+            "context_at_end": n_prompt + n_gen - 1, "tokens_per_s": round((n_gen - 1) / ts, 1),
+            "ms_per_token": round(1e3 * ts / (n_gen - 1), 4),
+            "greedy_tokens_per_s_same_positions": round((n_gen - 1) / tg, 1)}
+
+
 def cpu_baseline(image, cfg_vocab, budget_s=15.0):
     """The reference's own CPU ops (oracle/_ref, AVX2 + OpenMP) when built,
     else the oracle's C restatement, timed on a bounded decode sample."""
@@ -129,6 +156,8 @@ def main():
     ap.add_argument("--mix", type=int, default=0, help="0: Q6_K v/down in every layer; 1: llama.cpp layers")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of a graph replay")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 1024-token prefill measurement")
+    ap.add_argument("--no-sampled", action="store_true",
+                    help="skip the sampled decode after a 1024-token prompt (device sampler)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run device-to-device copies of this many MB (the reference kernel of known "
                          "size for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -192,6 +221,13 @@ def main():
             f"{prefill['prefill_tokens_per_s']:.0f} tok/s ({prefill['roofline']['achieved']:.1f} TFLOP/s), "
             f"first token after {prefill['time_to_first_token_ms']:.1f} ms")
 
+    sampled = None
+    if not args.no_sampled:
+        sampled = sampled_measure(eng, cfg)
+        log(f"sampled decode after a {sampled['prompt_tokens']}-token prompt: {sampled['tokens_per_s']:.1f} tok/s "
+            f"(T {sampled['temperature']}, top-p {sampled['top_p']}; greedy at the same positions "
+            f"{sampled['greedy_tokens_per_s_same_positions']:.1f} tok/s)")
+
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -230,6 +266,7 @@ def main():
                      "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 3)},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "sampled_decode": sampled,
     }
     print(json.dumps(res), flush=True)
     eng.free()

@@ -143,6 +143,13 @@ int mcpm_execute_attention(mcpm_ctx *ctx, float *attn_out, const float *q, const
 int mcpm_get_embedding(mcpm_ctx *ctx, float *out, const mcpm_tensor *embd, int token);
 /* First index of the maximum of x[0..n) into *out (device int). */
 int mcpm_argmax(mcpm_ctx *ctx, const float *x, int n, int *out);
+/* Sampler::sample (src/sampler.cpp:8-73) on device logits x[0..n) for the
+ * uniform draw r in [0,1), token into *out (device int): temperature, softmax,
+ * the top-p cut over the (p desc, id asc) order, the walk; its running sums
+ * are taken in double over blocks of 256 positions (the reference's run
+ * sequentially in float; see mcpm_sampler.hip), so its choice can differ
+ * from mcpm_sample_logits only for draws within rounding of a boundary. */
+int mcpm_sample_device(mcpm_ctx *ctx, const float *x, int n, float temperature, float top_p, float r, int *out);
 
 /* ------------------------------------------------------------ engine ----- */
 
@@ -190,9 +197,16 @@ int mcpm_engine_decode_steps(mcpm_engine *e, int n_steps);
 int mcpm_engine_tokens(mcpm_engine *e, int *out, int n);
 
 /* Same loop with the reference's temperature / top-p sampler
- * (src/sampler.cpp:8-73) drawing from std::mt19937(seed). */
+ * (src/sampler.cpp:8-73) on the device (mcpm_sample_device's arithmetic),
+ * drawing std::uniform_real_distribution<float> from std::mt19937(seed), one
+ * draw per generated token. */
 int mcpm_engine_generate_sampled(mcpm_engine *e, const int *prompt, int n_prompt, int n_gen, float temperature,
                                  float top_p, uint32_t seed, int *out_tokens);
+/* Continues the last generate call by n_steps sampled tokens (draws from a
+ * new std::mt19937(seed)); the token list must have room (mcpm_engine_tokens
+ * reads it).  No counterpart in the reference: its chat loop
+ * (src/chat_session.cpp:154-186) samples token by token. */
+int mcpm_engine_decode_sampled(mcpm_engine *e, int n_steps, float temperature, float top_p, uint32_t seed);
 
 /* Sampler::sample (src/sampler.cpp:8-73) on host logits for a given uniform
  * draw r in [0,1): returns the token id, or a negative error code. */

@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cmath>
+#include <random>
 #include <vector>
 
 #include "gguf.h"
@@ -90,6 +91,11 @@ struct mcpm_engine {
   // batched prompt processing
   bool use_prefill = true;
   PrefillBufs pf;
+  // sampled decode: the token graph ends at the logits and the device sampler
+  // picks the next token
+  bool sample_mode = false;
+  void* d_sample = nullptr;
+  size_t sample_cap = 0;
 };
 
 namespace {
@@ -134,7 +140,7 @@ void free_engine(mcpm_engine* e) {
                   static_cast<void*>(e->h), static_cast<void*>(e->logits), static_cast<void*>(e->argmax_part),
                   static_cast<void*>(e->st), static_cast<void*>(e->out_tokens), static_cast<void*>(e->kc),
                   static_cast<void*>(e->vc), static_cast<void*>(e->rope), static_cast<void*>(e->attn_part),
-                  })
+                  e->d_sample})
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
   free_prefill(e->pf);
@@ -390,7 +396,7 @@ int enqueue_token(mcpm_engine* e) {
     a.argmax_part = e->argmax_part;
     MCPM_HIP(timed(e, MCPM_KC_LM_HEAD, [&] { return launch_gemv(a, PRO_NORM_EVEN, EPI_LOGITS, n_cu, s); }));
   }
-  MCPM_HIP(launch_argmax_final(e->argmax_part, e->lm_grid, nullptr, e->st, e->out_tokens, s));
+  if (!e->sample_mode) MCPM_HIP(launch_argmax_final(e->argmax_part, e->lm_grid, nullptr, e->st, e->out_tokens, s));
   return MCPM_OK;
 }
 
@@ -682,6 +688,100 @@ int mcpm_engine_decode_steps(mcpm_engine* e, int n_steps) {
     const int rc = run_token(e);
     if (rc) return rc;
   }
+  e->gen_count += n_steps;
+  e->next_pos += n_steps;
+  return MCPM_OK;
+}
+
+// The token graph without (sampled) or with (greedy) the argmax at its end.
+static int set_sample_mode(mcpm_engine* e, bool on) {
+  if (e->sample_mode == on) return MCPM_OK;
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  e->sample_mode = on;
+  drop_graph(e);
+  return MCPM_OK;
+}
+
+static int ensure_sampler(mcpm_engine* e) {
+  const size_t need = sampler_bytes(e->cfg.vocab);
+  if (need <= e->sample_cap) return MCPM_OK;
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  if (e->d_sample) (void)hipFree(e->d_sample);
+  e->d_sample = nullptr;
+  e->sample_cap = 0;
+  int rc = alloc_dev(&e->d_sample, need);
+  if (rc) return rc;
+  e->sample_cap = need;
+  return MCPM_OK;
+}
+
+// The next token from the logits of the step just queued: it becomes the
+// next input token and the next entry of the generated list.
+static int sample_step(mcpm_engine* e, float temperature, float top_p, float r) {
+  MCPM_HIP(launch_sample(e->d_sample, e->sample_cap, e->logits, e->cfg.vocab, temperature, top_p, r, nullptr, e->st,
+                         e->out_tokens, e->ctx->stream));
+  return MCPM_OK;
+}
+
+static bool bad_sampling(float temperature, float top_p) { return !(temperature == temperature) || !(top_p == top_p); }
+
+int mcpm_engine_generate_sampled(mcpm_engine* e, const int* prompt, int n_prompt, int n_gen, float temperature,
+                                 float top_p, uint32_t seed, int* out_tokens) {
+  if (!e || !prompt || !out_tokens || n_prompt <= 0 || n_gen <= 0 || bad_sampling(temperature, top_p))
+    return fail(MCPM_ERR_ARG, "mcpm_engine_generate_sampled: bad argument");
+  if (!e->kc) return fail(MCPM_ERR_CONTEXT, "KV cache not initialised");
+  if (n_prompt + n_gen - 1 > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab) return fail(MCPM_ERR_ARG, "prompt token out of range");
+  int rc = ensure_out_tokens(e, n_gen);
+  if (!rc) rc = ensure_staging(e, n_prompt);
+  if (!rc) rc = ensure_sampler(e);
+  if (!rc) rc = set_sample_mode(e, true);
+  if (rc) return rc;
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  // the draws of std::uniform_real_distribution<float> over std::mt19937(seed),
+  // one per generated token (src/sampler.cpp:5-6, seeded by the caller)
+  std::mt19937 rng(seed);
+  std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+  const int first = (e->use_prefill && n_prompt > 1) ? n_prompt - 1 : 0;
+  if (first) rc = mcpm_engine_prefill(e, prompt, first, 0);
+  for (int p = first; p < n_prompt && !rc; ++p) {
+    rc = queue_state(e, p, prompt[p], p, 0);
+    if (!rc) rc = run_token(e);
+  }
+  if (!rc) rc = sample_step(e, temperature, top_p, dist(rng));
+  for (int i = 1; i < n_gen && !rc; ++i) {
+    rc = run_token(e);
+    if (!rc) rc = sample_step(e, temperature, top_p, dist(rng));
+  }
+  const int rc2 = set_sample_mode(e, false);
+  if (rc) return rc;
+  if (rc2) return rc2;
+  e->gen_count = n_gen;
+  e->next_pos = n_prompt + n_gen - 1;
+  MCPM_HIP(hipMemcpyAsync(out_tokens, e->out_tokens, n_gen * sizeof(int), hipMemcpyDeviceToHost, e->ctx->stream));
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  return MCPM_OK;
+}
+
+int mcpm_engine_decode_sampled(mcpm_engine* e, int n_steps, float temperature, float top_p, uint32_t seed) {
+  if (!e || n_steps < 0 || bad_sampling(temperature, top_p))
+    return fail(MCPM_ERR_ARG, "mcpm_engine_decode_sampled: bad argument");
+  if (e->gen_count == 0) return fail(MCPM_ERR_ARG, "mcpm_engine_decode_sampled: no generate call to continue");
+  if (e->next_pos + n_steps > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
+  if (e->gen_count + n_steps > e->out_cap) return fail(MCPM_ERR_ARG, "mcpm_engine_decode_sampled: token list full");
+  int rc = ensure_sampler(e);
+  if (!rc) rc = set_sample_mode(e, true);
+  if (rc) return rc;
+  std::mt19937 rng(seed);
+  std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+  for (int i = 0; i < n_steps && !rc; ++i) {
+    rc = run_token(e);
+    if (!rc) rc = sample_step(e, temperature, top_p, dist(rng));
+  }
+  const int rc2 = set_sample_mode(e, false);
+  if (rc) return rc;
+  if (rc2) return rc2;
   e->gen_count += n_steps;
   e->next_pos += n_steps;
   return MCPM_OK;

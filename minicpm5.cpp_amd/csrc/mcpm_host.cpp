@@ -237,6 +237,7 @@ void mcpm_destroy(mcpm_ctx* c) {
   if (c->h_rope) (void)hipHostFree(c->h_rope);
   if (c->d_attn_part) (void)hipFree(c->d_attn_part);
   if (c->d_argmax_part) (void)hipFree(c->d_argmax_part);
+  if (c->d_sample) (void)hipFree(c->d_sample);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -546,6 +547,22 @@ int mcpm_argmax(mcpm_ctx* c, const float* x, int n, int* out) {
   if (rc) return rc;
   MCPM_HIP(launch_argmax_partial(x, n, c->d_argmax_part, nparts, c->stream));
   MCPM_HIP(launch_argmax_final(c->d_argmax_part, nparts, out, nullptr, nullptr, c->stream));
+  return MCPM_OK;
+}
+
+int mcpm_sample_device(mcpm_ctx* c, const float* logits, int n, float temperature, float top_p, float r, int* out) {
+  if (!c || !logits || !out || n <= 0 || !(r >= 0.0f && r < 1.0f))
+    return fail(MCPM_ERR_ARG, "mcpm_sample_device: bad argument");
+  const size_t need = sampler_bytes(n);
+  if (need > c->sample_cap) {
+    if (c->d_sample) (void)hipFree(c->d_sample);
+    c->d_sample = nullptr;
+    c->sample_cap = 0;
+    MCPM_HIP(hipMalloc(&c->d_sample, need));
+    c->sample_cap = need;
+  }
+  MCPM_HIP(launch_sample(c->d_sample, c->sample_cap, logits, n, temperature, top_p, r, out, nullptr, nullptr,
+                         c->stream));
   return MCPM_OK;
 }
 

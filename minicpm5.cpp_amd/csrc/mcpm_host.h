@@ -20,6 +20,8 @@ struct mcpm_ctx {
   size_t attn_part_cap = 0;
   float2* d_argmax_part = nullptr;
   int argmax_cap = 0;
+  void* d_sample = nullptr;  // device sampler scratch
+  size_t sample_cap = 0;
 };
 
 struct mcpm_tensor {

@@ -223,6 +223,14 @@ struct StepState {
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s);
 
+// The temperature / top-p sampler on the device (mcpm_sampler.hip): scratch
+// bytes for n logits, and its passes for one uniform draw r.  The token goes
+// to *out_token (device) when given, and when st is given it becomes the next
+// input token, is appended to out_tokens and pos advances (as the argmax does).
+size_t sampler_bytes(int n);
+hipError_t launch_sample(void* scratch, size_t scratch_bytes, const float* logits, int n, float temperature,
+                         float top_p, float r, int* out_token, StepState* st, int* out_tokens, hipStream_t s);
+
 // When `start` is set, the GEMV and attention launch helpers record these
 // events at their kernel's start and end (hipExtLaunchKernel), so the elapsed
 // time is the kernel's own duration.  Set around one launch by the engine's

@@ -1,4 +1,5 @@
-// sampler.cpp -- temperature / top-p sampling of the decode loop.
+// sampler.cpp -- the host temperature / top-p sampler (mcpm_sample_logits);
+// the engine's sampled decode runs the device sampler (mcpm_sampler.hip).
 //
 // Sampler::sample (src/sampler.cpp:8-73): optional temperature scaling,
 // softmax with the max subtracted, probabilities sorted in decreasing order,
@@ -55,43 +56,6 @@ int sample_token(const float* logits, int n, float temperature, float top_p, flo
 }
 
 }  // namespace mcpm
-
-extern "C" {
-
-int mcpm_engine_generate_sampled(mcpm_engine* e, const int* prompt, int n_prompt, int n_gen, float temperature,
-                                 float top_p, uint32_t seed, int* out_tokens) {
-  if (!e || !prompt || !out_tokens || n_prompt <= 0 || n_gen <= 0)
-    return mcpm::fail(MCPM_ERR_ARG, "mcpm_engine_generate_sampled: bad argument");
-  mcpm_model_config c;
-  int rc = mcpm_engine_config(e, &c);
-  if (rc) return rc;
-  std::mt19937 rng(seed);
-  std::uniform_real_distribution<float> dist(0.0f, 1.0f);
-  std::vector<float> logits(static_cast<size_t>(c.vocab));
-  int next = -1;
-  // all but the last prompt token in batched passes (when enabled)
-  const int first = (mcpm_engine_uses_prefill(e) && n_prompt > 1) ? n_prompt - 1 : 0;
-  if (first) {
-    rc = mcpm_engine_prefill(e, prompt, first, 0);
-    if (rc) return rc;
-  }
-  for (int p = first; p < n_prompt; ++p) {
-    const bool last = (p == n_prompt - 1);
-    rc = mcpm_engine_forward(e, prompt[p], p, 1 << 30, last ? logits.data() : nullptr, nullptr);
-    if (rc) return rc;
-  }
-  next = mcpm::sample_token(logits.data(), c.vocab, temperature, top_p, dist(rng));
-  out_tokens[0] = next;
-  for (int i = 1; i < n_gen; ++i) {
-    rc = mcpm_engine_forward(e, next, n_prompt + i - 1, 1 << 30, logits.data(), nullptr);
-    if (rc) return rc;
-    next = mcpm::sample_token(logits.data(), c.vocab, temperature, top_p, dist(rng));
-    out_tokens[i] = next;
-  }
-  return MCPM_OK;
-}
-
-}  // extern "C"
 
 extern "C" int mcpm_sample_logits(const float* logits, int n, float temperature, float top_p, float r) {
   if (!logits || n <= 0) return mcpm::fail(MCPM_ERR_ARG, "mcpm_sample_logits: bad argument");

@@ -102,6 +102,7 @@ _SIGS = {
     "mcpm_execute_attention": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "mcpm_get_embedding": (_I, [_P, _P, _P, _I]),
     "mcpm_argmax": (_I, [_P, _P, _I, _P]),
+    "mcpm_sample_device": (_I, [_P, _P, _I, _F, _F, _F, _P]),
     "mcpm_engine_load_gguf": (_I, [_P, C.c_char_p, C.POINTER(_P)]),
     "mcpm_engine_load_gguf_memory": (_I, [_P, _P, _SZ, C.POINTER(_P)]),
     "mcpm_engine_free": (None, [_P]),
@@ -113,6 +114,7 @@ _SIGS = {
     "mcpm_engine_decode_steps": (_I, [_P, _I]),
     "mcpm_engine_tokens": (_I, [_P, _P, _I]),
     "mcpm_engine_generate_sampled": (_I, [_P, _P, _I, _I, _F, _F, C.c_uint32, _P]),
+    "mcpm_engine_decode_sampled": (_I, [_P, _I, _F, _F, C.c_uint32]),
     "mcpm_sample_logits": (_I, [_P, _I, _F, _F, _F]),
     "mcpm_engine_set_graph": (_I, [_P, _I]),
     "mcpm_engine_set_kernel_timing": (_I, [_P, _I]),
@@ -331,6 +333,9 @@ class Engine:
 
     def decode_steps(self, n: int):
         check(self.lib.mcpm_engine_decode_steps(self.h, n))
+
+    def decode_sampled(self, n: int, temperature: float, top_p: float, seed: int):
+        check(self.lib.mcpm_engine_decode_sampled(self.h, n, temperature, top_p, seed))
 
     def tokens(self, n: int) -> np.ndarray:
         out = np.empty(n, np.int32)

@@ -765,3 +765,76 @@ int or_sample(const float *logits, int n, float temperature, float top_p, float 
     free(pr);
     return out;
 }
+
+/* The device sampler's arithmetic (mcpm_sample_device and the engine's
+ * sampled decode).  Sampler::sample (src/sampler.cpp:8-73) step for step --
+ * temperature, softmax with the max subtracted, the (p desc, id asc) order
+ * when 0 < top_p < 1, the top-p cut, the walk over the running sum -- with
+ * every running sum taken in double over blocks of OR_SB positions: in order
+ * within a block, the blocks in order, a position's running sum being the
+ * sum of the blocks before it plus its in-block running sum.  The walk
+ * compares r*C with the running sum of p (C = the running sum at the cut),
+ * which is the reference's comparison of r with the running sum of p/cum
+ * without the per-term division.  Deviation from the reference: rounding
+ * only (its sums run sequentially in float, which a GPU cannot split).
+ * Positions past the cut never enter a sum that decides anything. */
+#define OR_SB 256
+
+int or_sample_blocked(const float *logits, int n, float temperature, float top_p, float r) {
+    const float inv_temp = (temperature > 0.0f) ? (1.0f / temperature) : 1.0f;
+    const int apply_temp = (temperature != 1.0f && temperature > 0.0f);
+    float maxl = -1e9f;
+    for (int i = 0; i < n; ++i) {
+        const float v = apply_temp ? logits[i] * inv_temp : logits[i];
+        if (v > maxl) maxl = v;
+    }
+    or_pi *pr = (or_pi *)malloc(sizeof(or_pi) * (size_t)n);
+    double total = 0.0, blk = 0.0;
+    for (int i = 0; i < n; ++i) {
+        const float v = apply_temp ? logits[i] * inv_temp : logits[i];
+        pr[i].p = or_expf(v - maxl);
+        pr[i].id = i;
+        blk = blk + (double)pr[i].p;
+        if (i % OR_SB == OR_SB - 1 || i == n - 1) {
+            total = total + blk;
+            blk = 0.0;
+        }
+    }
+    const float sum = (float)total;
+    for (int i = 0; i < n; ++i) pr[i].p = pr[i].p / sum;
+    const int topp = (top_p > 0.0f && top_p < 1.0f);
+    if (topp) qsort(pr, (size_t)n, sizeof(or_pi), cmp_pi);
+    /* the cut: first k whose running sum, rounded to float, reaches top_p */
+    int cnt = n;
+    double off = 0.0, pre = 0.0, C = 0.0;
+    for (int k = 0; k < n; ++k) {
+        pre = pre + (double)pr[k].p;
+        C = off + pre;
+        if (topp && (float)C >= top_p) {
+            cnt = k + 1;
+            break;
+        }
+        if (k % OR_SB == OR_SB - 1) {
+            off = off + pre;
+            pre = 0.0;
+        }
+    }
+    /* the walk: first k < cnt whose running sum reaches r*C */
+    const double t = (double)r * C;
+    int out = pr[cnt - 1].id;
+    off = 0.0;
+    pre = 0.0;
+    for (int k = 0; k < cnt; ++k) {
+        pre = pre + (double)pr[k].p;
+        if (t <= off + pre) {
+            out = pr[k].id;
+            break;
+        }
+        if (k % OR_SB == OR_SB - 1) {
+            off = off + pre;
+            pre = 0.0;
+        }
+    }
+    free(pr);
+    return out;
+}

@@ -136,6 +136,8 @@ void or_mt_seed(or_mt19937 *g, uint32_t seed);
 uint32_t or_mt_next(or_mt19937 *g);
 float or_mt_uniform01(or_mt19937 *g);
 int or_sample(const float *logits, int n, float temperature, float top_p, float r);
+/* The same steps with running sums in blocked double (the device sampler). */
+int or_sample_blocked(const float *logits, int n, float temperature, float top_p, float r);
 
 #ifdef __cplusplus
 }

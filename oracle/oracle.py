@@ -77,6 +77,7 @@ _ORACLE_SIGS = {
     "or_mt_next": (C.c_uint32, [_P]),
     "or_mt_uniform01": (_F, [_P]),
     "or_sample": (_I, [_P, _I, _F, _F, _F]),
+    "or_sample_blocked": (_I, [_P, _I, _F, _F, _F]),
 }
 
 _REF_SIGS = {

@@ -109,7 +109,7 @@ def test_sampled_matches_oracle_sampler(small_engine, small_image):
         om.forward(int(t), p, lg)
     out = []
     for i in range(24):
-        nxt = orc.or_sample(lg.ctypes.data, 4000, 0.8, 0.95, orc.or_mt_uniform01(gen.ctypes.data))
+        nxt = orc.or_sample_blocked(lg.ctypes.data, 4000, 0.8, 0.95, orc.or_mt_uniform01(gen.ctypes.data))
         out.append(nxt)
         if i < 23:
             om.forward(nxt, len(prompt) + i, lg)

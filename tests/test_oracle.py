@@ -448,6 +448,98 @@ def test_sampler_vs_numpy_spec(orc):
         assert got == want
 
 
+def _exact_blocked_spec(orc, lg, T, top_p, r):
+    """The device sampler's decision in exact rational arithmetic, valid when
+    every running sum is exact in double (then blocking and order of the
+    double sums cannot matter): float32 temperature, max and quotients, the
+    oracle's exp, exact sums, float32 rounding where the spec rounds."""
+    from fractions import Fraction
+    f32 = np.float32
+    v = (lg * (f32(1) / f32(T))).astype(np.float32) if (T > 0 and T != 1.0) else lg
+    m = max(f32(-1e9), v.max())
+    e = np.array([orc.or_expf(float(x)) for x in (v - m).astype(np.float32)], np.float32)
+    E = sum((Fraction(float(x)) for x in e), Fraction(0))
+    s = f32(float(E))
+    p = (e / s).astype(np.float32)
+    topp = 0 < top_p < 1
+    order = np.lexsort((np.arange(p.size), -p)) if topp else np.arange(p.size)
+    run, P = Fraction(0), []
+    for k in order:
+        run += Fraction(float(p[k]))
+        P.append(run)
+    assert all(float(x) == x for x in P), "case is not exact in double"
+    cnt = p.size
+    if topp:
+        hit = [k for k, x in enumerate(P) if f32(float(x)) >= f32(top_p)]
+        cnt = hit[0] + 1 if hit else p.size
+    t = Fraction(float(r) * float(P[cnt - 1]))
+    for k in range(cnt):
+        if t <= P[k]:
+            return int(order[k])
+    return int(order[cnt - 1])
+
+
+def test_blocked_sampler_exact_cases(orc):
+    """or_sample_blocked against exact arithmetic on cases whose double sums
+    are exact (p >= 2^-15, a few thousand terms: <= 50 significant bits), over
+    several blocks of 256, with and without a top-p cut, draws near 0 and 1."""
+    rng = np.random.default_rng(21)
+    for trial in range(16):
+        n = [300, 1000, 2500, 256, 257, 40][trial % 6]
+        lg = (rng.standard_normal(n) * 0.3).astype(np.float32)
+        if trial % 5 == 0:
+            lg[rng.integers(0, n, 8)] = lg[0]  # ties, ordered by id
+        T, top_p = [(0.8, 0.95), (1.0, 0.5), (1.0, 1.0), (1.3, 0.05), (0.7, 0.0), (1.0, 0.999)][trial % 6]
+        for r in [0.0, float(rng.random()), float(np.nextafter(np.float32(1), np.float32(0)))]:
+            got = orc.or_sample_blocked(P(lg), n, T, top_p, r)
+            assert got == _exact_blocked_spec(orc, lg, T, top_p, r), (trial, r)
+
+
+def _real_sampler_choice(orc, lg, T, top_p, r):
+    """The sampler's decision with the float32 probabilities summed exactly
+    (integers in units of 2^-149) and compared exactly: the real-number
+    statement of sampler.cpp:8-73 that both float orders approximate."""
+    from fractions import Fraction
+    from itertools import accumulate
+    f32 = np.float32
+    v = (lg * (f32(1) / f32(T))).astype(np.float32) if (T > 0 and T != 1.0) else lg
+    m = max(f32(-1e9), v.max())
+    e = np.array([orc.or_expf(float(x)) for x in (v - m).astype(np.float32)], np.float32)
+    s = f32(float(sum((Fraction(float(x)) for x in e), Fraction(0))))
+    p = (e / s).astype(np.float32)
+    topp = 0 < top_p < 1
+    order = np.lexsort((np.arange(p.size), -p)) if topp else np.arange(p.size)
+    units = [int(Fraction(float(x)) * 2**149) for x in p[order]]
+    P = list(accumulate(units))
+    cnt = p.size
+    if topp:
+        tp = Fraction(float(f32(top_p))) * 2**149
+        cnt = next((k + 1 for k, x in enumerate(P) if x >= tp), p.size)
+    rf = Fraction(float(r))
+    k = next((k for k in range(cnt) if P[k] >= rf * P[cnt - 1]), cnt - 1)
+    return int(order[k])
+
+
+def test_blocked_sampler_agrees_with_reference_order(orc):
+    """On general inputs (sums not exact): or_sample_blocked makes the choice
+    of exact arithmetic (its double sums are ~1e-16 off) and the reference's
+    fp32 running sums (or_sample) mostly do too -- over 5000 terms their
+    drift moves the choice by a few positions now and then."""
+    rng = np.random.default_rng(22)
+    blocked = ref = total = 0
+    for trial in range(24):
+        lg = (rng.standard_normal(5000) * [0.5, 3.0, 8.0][trial % 3]).astype(np.float32)
+        T, top_p = [(0.8, 0.95), (1.0, 1.0), (1.2, 0.7)][trial % 3]
+        for _ in range(4):
+            r = float(np.float32(rng.random()))
+            want = _real_sampler_choice(orc, lg, T, top_p, r)
+            blocked += orc.or_sample_blocked(P(lg), lg.size, T, top_p, r) == want
+            ref += orc.or_sample(P(lg), lg.size, T, top_p, r) == want
+            total += 1
+    assert blocked >= total - 1, (blocked, total)
+    assert ref >= 0.9 * total, (ref, total)
+
+
 def test_mt19937_known_answers(orc):
     """std::mt19937 default seed 5489: first output 3499211612 and, as the C++
     standard requires ([rand.predef]), the 10000th output 4123659995."""
