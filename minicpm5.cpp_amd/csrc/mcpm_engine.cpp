@@ -82,7 +82,7 @@ struct mcpm_engine {
   bool attn_fused = false;  // the O-projection's prologue combines the attention partials
   // graph
   bool use_graph = true;
-  hipGraphExec_t graph = nullptr;
+  hipGraphExec_t graph[2] = {nullptr, nullptr};  // greedy (argmax at the end), sampled
   // timing
   int timing_class = -1;
   std::vector<TimedPair> events;
@@ -107,8 +107,10 @@ int alloc_dev(void** p, size_t bytes) {
 }
 
 void drop_graph(mcpm_engine* e) {
-  if (e->graph) (void)hipGraphExecDestroy(e->graph);
-  e->graph = nullptr;
+  for (hipGraphExec_t& g : e->graph) {
+    if (g) (void)hipGraphExecDestroy(g);
+    g = nullptr;
+  }
 }
 
 void free_prefill(PrefillBufs& b) {
@@ -404,7 +406,8 @@ int run_token(mcpm_engine* e) {
   // Events recorded inside a captured graph cannot be read back with
   // hipEventElapsedTime, so a timed kernel class runs the same launches eagerly.
   if (!e->use_graph || e->timing_class >= 0) return enqueue_token(e);
-  if (!e->graph) {
+  hipGraphExec_t& graph = e->graph[e->sample_mode ? 1 : 0];
+  if (!graph) {
     hipStream_t s = e->ctx->stream;
     MCPM_HIP(hipStreamSynchronize(s));
     MCPM_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -416,14 +419,14 @@ int run_token(mcpm_engine* e) {
       return rc;
     }
     if (ce != hipSuccess) return hip_fail(ce, "hipStreamEndCapture");
-    const hipError_t ie = hipGraphInstantiate(&e->graph, g, nullptr, nullptr, 0);
+    const hipError_t ie = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (ie != hipSuccess) {
-      e->graph = nullptr;
+      graph = nullptr;
       return hip_fail(ie, "hipGraphInstantiate");
     }
   }
-  MCPM_HIP(hipGraphLaunch(e->graph, e->ctx->stream));
+  MCPM_HIP(hipGraphLaunch(graph, e->ctx->stream));
   return MCPM_OK;
 }
 
@@ -693,12 +696,10 @@ int mcpm_engine_decode_steps(mcpm_engine* e, int n_steps) {
   return MCPM_OK;
 }
 
-// The token graph without (sampled) or with (greedy) the argmax at its end.
+// The token graph without (sampled) or with (greedy) the argmax at its end;
+// each is captured once and kept.
 static int set_sample_mode(mcpm_engine* e, bool on) {
-  if (e->sample_mode == on) return MCPM_OK;
-  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
   e->sample_mode = on;
-  drop_graph(e);
   return MCPM_OK;
 }
 
