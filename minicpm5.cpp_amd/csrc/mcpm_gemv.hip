@@ -575,6 +575,18 @@ __device__ __forceinline__ float hsum8(const float (&acc)[8]) {
   return ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
 }
 
+// Work groups are dispatched round-robin over the 8 XCDs (work group b on
+// XCD b % 8), each with its own L2.  A GRP item's rows are 16-byte runs of
+// every chunk plane that do not fill whole 128-byte lines, so a line is
+// shared with the neighbouring item: giving each XCD a contiguous range of
+// items (this bijection of [0, G)) lets the neighbour's half come from the
+// same L2 instead of HBM.
+__device__ __forceinline__ int xcd_contiguous(int b, int G) {
+  const int x = b & 7, k = b >> 3;
+  const int q = G >> 3, r = G & 7;  // XCD x runs q + (x < r) work groups
+  return x * q + min(x, r) + k;
+}
+
 // ---------------------------------------------------------------- kernel ---
 // TILE: S slots per item, KB steps per item, 4 waves.  ROW: S = 64, KB = nb,
 // 4..8 waves.  TILE's bound of 4 waves lets a wave hold up to 512 registers
@@ -599,7 +611,8 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
   // This wave's steps: item first + (t / KB) * stride, step t % KB.  Steps
   // past the last re-read the last one (cached, results unused), so every
   // load is issued unconditionally and no wait depends on a branch.
-  const int first = GRP ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) * NW + wave;
+  const int first = GRP ? xcd_contiguous(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x))
+                        : static_cast<int>(blockIdx.x) * NW + wave;
   const int n_mine = first < n_items ? (n_items - 1 - first) / stride + 1 : 0;
   const int n_steps = n_mine * KB;
   const float invS = 1.0f / static_cast<float>(S);
