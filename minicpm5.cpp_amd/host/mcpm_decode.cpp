@@ -3,10 +3,13 @@
 // every prompt token at positions 0.., then the argmax of each step's logits
 // fed back.  --device-loop runs the same decode with the argmax on the GPU
 // (no logits copy per token); --prefill sends all prompt tokens but the last
-// through the batched prefill before the per-token loop.
+// through the batched prefill before the per-token loop; --sample T,P,SEED
+// samples each token on the GPU (temperature T, top-p P, mt19937 seeded with
+// SEED) in the device loop.
 //
 //   mcpm_decode (--gguf FILE | --synth SEED [--layers N] [--vocab N])
-//               [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--prefill] [--verbose]
+//               [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--prefill]
+//               [--sample T,P,SEED] [--verbose]
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -20,14 +23,17 @@
 static void usage() {
     std::fprintf(stderr,
                  "usage: mcpm_decode (--gguf FILE | --synth SEED [--layers N] [--vocab N])\n"
-                 "                   [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--prefill] [--verbose]\n");
+                 "                   [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--prefill]\n"
+                 "                   [--sample T,P,SEED] [--verbose]\n");
 }
 
 int main(int argc, char** argv) {
     std::string gguf;
     long long synth_seed = -1;
     int layers = 40, vocab = 130560, n_prompt = 32, n_tokens = 64;
-    bool device_loop = false, verbose = false, use_prefill = false;
+    bool device_loop = false, verbose = false, use_prefill = false, sample = false;
+    float temperature = 1.0f, top_p = 1.0f;
+    unsigned sample_seed = 0;
     std::vector<int> prompt_ids;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
@@ -58,6 +64,13 @@ int main(int argc, char** argv) {
         else if (a == "--tokens") n_tokens = std::atoi(next());
         else if (a == "--device-loop") device_loop = true;
         else if (a == "--prefill") use_prefill = true;
+        else if (a == "--sample") {
+            if (std::sscanf(next(), "%f,%f,%u", &temperature, &top_p, &sample_seed) != 3) {
+                usage();
+                return 2;
+            }
+            sample = device_loop = true;
+        }
         else if (a == "--verbose") verbose = true;
         else {
             usage();
@@ -112,7 +125,8 @@ int main(int argc, char** argv) {
     const auto t0 = std::chrono::steady_clock::now();
     double decode_s = 0.0;
     if (device_loop) {
-        out = engine.generate_greedy(prompt, n_tokens);
+        out = sample ? engine.generate_sampled(prompt, n_tokens, temperature, top_p, sample_seed)
+                     : engine.generate_greedy(prompt, n_tokens);
         decode_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     } else {
         auto argmax = [](const std::vector<float>& v) {

@@ -27,6 +27,10 @@ public:
     // Feeds prompt at positions 0.., then returns n_gen greedy tokens (all
     // prompt tokens but the last go through prefill()).
     std::vector<int> generate_greedy(const std::vector<int>& prompt, int n_gen);
+    // The same loop with Sampler::sample (src/sampler.cpp:8-73) on the device
+    // after each token: temperature, top-p, draws from std::mt19937(seed).
+    std::vector<int> generate_sampled(const std::vector<int>& prompt, int n_gen, float temperature, float top_p,
+                                      uint32_t seed);
     // Fills the KV cache for tokens at positions pos0.. in batched passes
     // (MFMA GEMMs), exactly as forward() per token would, without logits.  A
     // chat driver keeps the cache across turns and prefills only the new

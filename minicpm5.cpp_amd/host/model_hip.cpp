@@ -80,6 +80,16 @@ void MiniCPM5Engine::prefill(const std::vector<int>& tokens, int pos0) {
     check(mcpm_engine_prefill(engine_, tokens.data(), static_cast<int>(tokens.size()), pos0), "mcpm_engine_prefill");
 }
 
+std::vector<int> MiniCPM5Engine::generate_sampled(const std::vector<int>& prompt, int n_gen, float temperature,
+                                                 float top_p, uint32_t seed) {
+    if (!engine_) throw std::runtime_error("generate_sampled: no model loaded");
+    std::vector<int> out(static_cast<size_t>(n_gen > 0 ? n_gen : 0));
+    check(mcpm_engine_generate_sampled(engine_, prompt.data(), static_cast<int>(prompt.size()), n_gen, temperature,
+                                       top_p, seed, out.data()),
+          "mcpm_engine_generate_sampled");
+    return out;
+}
+
 std::vector<int> MiniCPM5Engine::generate_greedy(const std::vector<int>& prompt, int n_gen) {
     if (!engine_) throw std::runtime_error("generate_greedy: no model loaded");
     std::vector<int> out(static_cast<size_t>(n_gen > 0 ? n_gen : 0));

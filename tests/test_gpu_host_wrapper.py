@@ -139,3 +139,34 @@ def test_engine_mirror_greedy_matches_oracle(mode):
     want = om.generate_greedy(prompt, n_gen)
     om.close()
     assert got == list(want)
+
+
+@pytest.mark.gpu
+def test_engine_mirror_sampled_matches_oracle():
+    """mcpm_decode --sample: MiniCPM5Engine::generate_sampled against the
+    oracle model with the device sampler's arithmetic and the same draws."""
+    import oracle as O
+    orc = O.oracle()
+    cfg = mcpm.make_config(2, 2304, 32, 8, 64, 5760, 4096)
+    seed, prompt, n_gen, T, top_p, sseed = 7, [5, 1000, 77, 4095, 12], 10, 0.9, 0.9, 31
+    announce("mcpm_decode --sample")
+    cmd = [DECODE, "--synth", str(seed), "--layers", "2", "--vocab", "4096",
+           "--prompt-ids", ",".join(map(str, prompt)), "--tokens", str(n_gen), "--sample", f"{T},{top_p},{sseed}"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    line = next(l for l in r.stdout.splitlines() if l.startswith("tokens:"))
+    got = [int(t) for t in line.split()[1:]]
+    om = O.OracleModel(mcpm.synth_gguf(cfg, seed=seed, mix=0))
+    om.init_kv(len(prompt) + n_gen + 2)
+    lg = np.empty(4096, np.float32)
+    for p, t in enumerate(prompt):
+        om.forward(int(t), p, lg)
+    gen = np.zeros(625, np.uint32)
+    orc.or_mt_seed(P(gen), sseed)
+    want = []
+    for i in range(n_gen):
+        if want:
+            om.forward(want[-1], len(prompt) + i - 1, lg)
+        want.append(orc.or_sample_blocked(P(lg), 4096, T, top_p, orc.or_mt_uniform01(P(gen))))
+    om.close()
+    assert got == want
