@@ -140,9 +140,9 @@ hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc
 // and over the chunks, in order:
 //   m = max m_c; f_c = exp(m_c - m); Z = fma(z_c, f_c, Z); O_i = fma(o_c[i], f_c, O_i)
 //   out_i = O_i / Z
-// A split takes ceil(nch/16) consecutive chunks (at most ATTN_CPW), keeping
-// o_c in registers, so a kv head has at most 16 splits (up to 16*ATTN_CPW
-// chunks).  Every split writes its chunks' partials; the combine over the
+// A split takes ceil(nch/64) consecutive chunks (at most ATTN_CPW), keeping
+// o_c in registers, so a kv head has at most 64 splits (up to 64*ATTN_CPW
+// chunks): one chunk per work group up to 4096 positions.  Every split writes its chunks' partials; the combine over the
 // chunks runs in the consumer (the O-projection's prologue, or
 // k_attn_combine), after the kernel boundary, so no split waits for another.
 // Partials (AttnPart): o_c at o[(h*max_chunks + c)*head_dim + i], (m_c, z_c)
@@ -150,7 +150,7 @@ hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc
 // once, one chunk ahead, and the rows are staged through LDS.
 constexpr int ATTN_MAX_GROUP = 8;
 constexpr int ATTN_CPW = 8;
-constexpr int ATTN_MAX_SPLITS = 16;
+constexpr int ATTN_MAX_SPLITS = 64;
 
 __host__ __device__ inline int attn_chunks_per_split(int nch) {
   const int c = (nch + ATTN_MAX_SPLITS - 1) / ATTN_MAX_SPLITS;
@@ -160,8 +160,8 @@ __host__ __device__ inline int attn_splits(int nch) {
   const int cps = attn_chunks_per_split(nch);
   return (nch + cps - 1) / cps;
 }
-// The split count is not monotonic in the chunk count (16 chunks take 16
-// splits, 18 take 9): a launch covers the most any count in [lo, hi] needs.
+// The split count is not monotonic in the chunk count (64 chunks take 64
+// splits, 66 take 33): a launch covers the most any count in [lo, hi] needs.
 inline int attn_max_splits(int lo, int hi) {
   int m = 1;
   for (int n = std::max(lo, 1); n <= hi; ++n) m = std::max(m, attn_splits(n));

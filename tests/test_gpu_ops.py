@@ -250,9 +250,10 @@ def test_rope(ctx, orc, pos):
 
 
 # (position, KV capacity): the launch covers the splits of every chunk count
-# up to the capacity's, which is not monotonic (16 chunks take 16 splits, 18
-# take 9), so positions well below a capacity of 17-32 chunks are included
-ATTN_CASES = [(c, c + 3) for c in (0, 1, 63, 64, 65, 511, 2048, 4096)] + [(700, 1152), (1000, 1536), (960, 2000)]
+# up to the capacity's, which is not monotonic (64 chunks take 64 splits, 66
+# take 33), so positions well below a capacity of 65-128 chunks are included
+ATTN_CASES = [(c, c + 3) for c in (0, 1, 63, 64, 65, 511, 2048, 4096)] + [(700, 1152), (1000, 1536), (960, 2000),
+                                                                         (3000, 4600), (4200, 8192)]
 
 
 @pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: f"pos{c[0]}-cap{c[1]}")
