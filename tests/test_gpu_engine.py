@@ -183,3 +183,24 @@ def test_reference_geometry_tokens(ctx, name):
     want = O.OracleModel(img).generate_greedy(g["prompt"], n)
     np.testing.assert_array_equal(got, want)
     e.free()
+
+
+def test_long_context_greedy_matches_oracle(ctx):
+    """A 1100-token prompt (18 attention chunks per head) and 8 greedy tokens
+    on a model whose O projection combines the attention partials in its
+    prologue (q dim 1024: 4 blocks): every chunk batch of the combine runs,
+    against the oracle."""
+    cfg = mcpm.make_config(2, 1024, 16, 4, 64, 2048, 1000)
+    img = mcpm.synth_gguf(cfg, seed=404, mix=0)
+    prompt = [int(t) for t in np.random.default_rng(17).integers(0, 1000, 1100)]
+    announce("long context greedy vs oracle (1100-token prompt)")
+    eng = mcpm.Engine(ctx, image=img)
+    try:
+        eng.init_kv_cache(1120)
+        got = list(eng.generate_greedy(prompt, 8))
+    finally:
+        eng.free()
+    om = O.OracleModel(img)
+    want = list(om.generate_greedy(prompt, 8))
+    om.close()
+    assert got == want
