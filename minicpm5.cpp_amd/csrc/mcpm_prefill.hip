@@ -139,8 +139,8 @@ __device__ __forceinline__ h2 splat_h(int v) {
 // column l%16.  With K index k = 4*s + i over sub-blocks s and bytes i,
 // lane l's K range is sub-blocks 2g and 2g+1 (g = l/16): element 64g + 4m + i
 // (low) and 64g + 32 + 4m + i (high) of the block for lane group m.
-template <int WT, int NT>
-__global__ void __launch_bounds__(256) k_gemm_q8k(const GemmArgs a) {
+template <int WT, int NT, int OCC>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) k_gemm_q8k(const GemmArgs a) {
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   const int n_rt = (a.rows + 15) >> 4;
   const int n_tg = (a.n_tok + 16 * NT - 1) / (16 * NT);
@@ -401,21 +401,31 @@ hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const Qu
                            bool add, hipStream_t s) {
   if (w.type != MCPM_TYPE_Q4_K && w.type != MCPM_TYPE_Q6_K) return hipErrorInvalidValue;
   GemmArgs a{w, rows, nb, n_tok, q.xh, q.xd, q.xbs, out, ld_out, add ? 1 : 0};
-  // token tiles per wave (MCPM_PREFILL_NT=2|4 overrides, a tuning aid)
+  // token tiles per wave and waves per SIMD (MCPM_PREFILL_NT=1|2|4 and
+  // MCPM_PREFILL_OCC=1|2 override, tuning aids)
   static const int nt_env = [] {
     const char* v = std::getenv("MCPM_PREFILL_NT");
     return v ? std::atoi(v) : 0;
   }();
-  const int NT = nt_env == 2 || nt_env == 4 ? nt_env : 2;
+  static const int occ_env = [] {
+    const char* v = std::getenv("MCPM_PREFILL_OCC");
+    return v ? std::atoi(v) : 0;
+  }();
+  const bool q4 = w.type == MCPM_TYPE_Q4_K;
+  // Defaults: two waves per SIMD (registers held to 256 so a second wave hides
+  // the first's load latency); 32 tokens per wave for Q4_K, 16 for Q6_K, whose
+  // four MFMA operand sets need the room.
+  const int NT = nt_env == 1 || nt_env == 2 || nt_env == 4 ? nt_env : (q4 ? 2 : 1);
+  const int OCC = occ_env == 1 ? 1 : 2;
   const int n_tiles = ((rows + 15) / 16) * ((n_tok + 16 * NT - 1) / (16 * NT));
   const dim3 grid((n_tiles + 3) / 4);
-  if (NT == 4) {
-    if (w.type == MCPM_TYPE_Q4_K) launch_kernel(k_gemm_q8k<0, 4>, grid, dim3(256), 0, s, a);
-    else launch_kernel(k_gemm_q8k<1, 4>, grid, dim3(256), 0, s, a);
-  } else {
-    if (w.type == MCPM_TYPE_Q4_K) launch_kernel(k_gemm_q8k<0, 2>, grid, dim3(256), 0, s, a);
-    else launch_kernel(k_gemm_q8k<1, 2>, grid, dim3(256), 0, s, a);
+#define MCPM_GEMM(N, O) \
+  if (NT == N && OCC == O) { \
+    if (q4) launch_kernel(k_gemm_q8k<0, N, O>, grid, dim3(256), 0, s, a); \
+    else launch_kernel(k_gemm_q8k<1, N, O>, grid, dim3(256), 0, s, a); \
   }
+  MCPM_GEMM(1, 1) MCPM_GEMM(1, 2) MCPM_GEMM(2, 1) MCPM_GEMM(2, 2) MCPM_GEMM(4, 1) MCPM_GEMM(4, 2)
+#undef MCPM_GEMM
   return hipGetLastError();
 }
 
