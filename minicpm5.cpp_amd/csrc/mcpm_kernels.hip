@@ -14,6 +14,8 @@
 //    explicit.
 #include <algorithm>
 
+#include <cstdlib>
+
 #include "mcpm_device.h"
 
 namespace mcpm {
@@ -201,6 +203,54 @@ __device__ __forceinline__ void attn_load_chunk(AttnRegs<NV>& R, const float* __
   }
 }
 
+// One token on one chunk staged in LDS (K rows in sK with stride HDM + 4, V
+// rows in sV, the token's group of queries in sQ): scores and softmax terms
+// (wave <-> head, lane <-> position) into sE and mz[hh] = (m_c, z_c), a
+// barrier, then the weighted V sums, thread (head, dim) oi = tid + 256u into
+// o[u].  Positions at or past T take no part.
+template <int HDM, int OPT>
+__device__ __forceinline__ void attn_token_chunk(const float* sK, const float* sV, const float* sQ, float* sE,
+                                                 float2* mz, int c, int T, int group, int hd, int gh, float scale,
+                                                 float (&o)[OPT]) {
+  constexpr int KS = HDM + 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int hh = wave; hh < group; hh += 4) {
+    const float* qh = &sQ[hh * HDM];
+    const float* kt = &sK[lane * KS];
+    float dot = 0.0f;
+#pragma unroll 4
+    for (int i = 0; i < hd; i += 4) {
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(kt + i);
+      const f32x4 q4 = *reinterpret_cast<const f32x4*>(qh + i);
+      dot = __builtin_fmaf(q4.x, k4.x, dot);
+      dot = __builtin_fmaf(q4.y, k4.y, dot);
+      dot = __builtin_fmaf(q4.z, k4.z, dot);
+      dot = __builtin_fmaf(q4.w, k4.w, dot);
+    }
+    const bool present = c * ATTN_CHUNK + lane < T;
+    const float sv = present ? dot * scale : -1e9f;
+    const float mc = fmaxf(wave_max_fast(sv), -1e9f);
+    const float e = present ? exp_f32(sv - mc) : 0.0f;
+    const float z = wave_tree_sum_fast(e);
+    sE[hh * ATTN_CHUNK + lane] = e;
+    if (lane == 0) mz[hh] = make_float2(mc, z);
+  }
+  __syncthreads();
+  const int nt = min(ATTN_CHUNK, T - c * ATTN_CHUNK);
+#pragma unroll
+  for (int u = 0; u < OPT; ++u) {
+    const int oi = tid + 256 * u;
+    float acc = 0.0f;
+    if (oi < gh) {
+      const int hh = oi / hd, i = oi - hh * hd;
+      const float* eh = &sE[hh * ATTN_CHUNK];
+#pragma unroll 8
+      for (int j = 0; j < nt; ++j) acc = __builtin_fmaf(eh[j], sV[j * HDM + i], acc);
+    }
+    o[u] = acc;
+  }
+}
+
 template <int HDM>
 __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, const int* __restrict__ state,
@@ -216,7 +266,7 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
   __shared__ float sQ[ATTN_MAX_GROUP * HDM];
   __shared__ float sE[ATTN_MAX_GROUP * ATTN_CHUNK];
   __shared__ float2 sMZ[ATTN_CPW * ATTN_MAX_GROUP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int kvh = blockIdx.x, split = blockIdx.y;
   // decode: the position from the step state; prefill (pos0 >= 0): token
   // blockIdx.z at position pos0 + z, with its own q and partials
@@ -272,43 +322,10 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
       }
       if (cc + 1 < n) attn_load_chunk<NV>(R, kc, vc, c + 1, T, kvd, head_off, r4, nf4);
       __syncthreads();
-      // scores and the chunk's softmax terms: wave <-> head, lane <-> position
-      for (int hh = wave; hh < group; hh += 4) {
-        const float* qh = &sQ[hh * HDM];
-        const float* kt = &sK[lane * KS];
-        float dot = 0.0f;
-#pragma unroll 4
-        for (int i = 0; i < hd; i += 4) {
-          const f32x4 k4 = *reinterpret_cast<const f32x4*>(kt + i);
-          const f32x4 q4 = *reinterpret_cast<const f32x4*>(qh + i);
-          dot = __builtin_fmaf(q4.x, k4.x, dot);
-          dot = __builtin_fmaf(q4.y, k4.y, dot);
-          dot = __builtin_fmaf(q4.z, k4.z, dot);
-          dot = __builtin_fmaf(q4.w, k4.w, dot);
-        }
-        const bool present = c * ATTN_CHUNK + lane < T;
-        const float sv = present ? dot * scale : -1e9f;
-        const float mc = fmaxf(wave_max_fast(sv), -1e9f);
-        const float e = present ? exp_f32(sv - mc) : 0.0f;
-        const float z = wave_tree_sum_fast(e);
-        sE[hh * ATTN_CHUNK + lane] = e;
-        if (lane == 0) sMZ[cc * ATTN_MAX_GROUP + hh] = make_float2(mc, z);
-      }
-      __syncthreads();
-      // weighted V: thread <-> (head, dim)
-      const int nt = min(ATTN_CHUNK, T - c * ATTN_CHUNK);
+      float o[OPT];
+      attn_token_chunk<HDM, OPT>(sK, sV, sQ, sE, sMZ + cc * ATTN_MAX_GROUP, c, T, group, hd, gh, scale, o);
 #pragma unroll
-      for (int u = 0; u < OPT; ++u) {
-        const int oi = tid + 256 * u;
-        float o = 0.0f;
-        if (oi < gh) {
-          const int hh = oi / hd, i = oi - hh * hd;
-          const float* eh = &sE[hh * ATTN_CHUNK];
-#pragma unroll 8
-          for (int j = 0; j < nt; ++j) o = __builtin_fmaf(eh[j], sV[j * HDM + i], o);
-        }
-        oc[u][cc] = o;
-      }
+      for (int u = 0; u < OPT; ++u) oc[u][cc] = o[u];
     }
   }
 
@@ -327,6 +344,82 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
   if (tid < ATTN_CPW * ATTN_MAX_GROUP) {
     const int cc = tid / ATTN_MAX_GROUP, hh = tid % ATTN_MAX_GROUP;
     if (cc < n && hh < group) part_mz[static_cast<size_t>(kvh * group + hh) * max_chunks + c0 + cc] = sMZ[cc * ATTN_MAX_GROUP + hh];
+  }
+}
+
+// Prefill: chunk blockIdx.y of kv head blockIdx.x for the tile of tt
+// consecutive tokens from blockIdx.z * tt (token z at position pos0 + z,
+// its own q and partials).  The chunk's K and V rows are staged once; every
+// token of the tile whose context reaches the chunk then runs
+// attn_token_chunk on it -- the arithmetic of k_attention's launch for that
+// token -- and writes its partial for the chunk.  Rows the tile stages past
+// a token's context take no part in that token's sums.
+template <int HDM>
+__global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict__ q, const float* __restrict__ kc,
+                                                        const float* __restrict__ vc, int n_heads, int n_kv_heads,
+                                                        int hd, int max_chunks, float* __restrict__ part_o,
+                                                        float2* __restrict__ part_mz, int pos0, int n_tok, int tt,
+                                                        size_t tok_q, size_t tok_o, size_t tok_mz) {
+  constexpr int NV = HDM / 16;
+  constexpr int OPT = ATTN_MAX_GROUP * HDM / 256;
+  constexpr int NQ = ATTN_MAX_GROUP * HDM / 256;
+  constexpr int KS = HDM + 4;
+  __shared__ float sK[ATTN_CHUNK * KS];
+  __shared__ float sV[ATTN_CHUNK * HDM];
+  __shared__ float sQ[ATTN_MAX_GROUP * HDM];
+  __shared__ float sE[ATTN_MAX_GROUP * ATTN_CHUNK];
+  __shared__ float2 sMZ[ATTN_MAX_GROUP];
+  const int tid = threadIdx.x;
+  const int kvh = blockIdx.x, c = blockIdx.y;
+  const int z0 = static_cast<int>(blockIdx.z) * tt;
+  const int zlo = max(z0, c * ATTN_CHUNK - pos0);  // first token with pos0 + z + 1 > c * ATTN_CHUNK
+  const int zhi = min(z0 + tt, n_tok);
+  if (zlo >= zhi) return;
+  const int group = n_heads / n_kv_heads;
+  const int kvd = n_kv_heads * hd;
+  const int r4 = hd / 4, nf4 = ATTN_CHUNK * r4;
+  const int gh = group * hd;
+  const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+  const size_t head_off = static_cast<size_t>(kvh) * hd;
+
+  AttnRegs<NV> R;
+  attn_load_chunk<NV>(R, kc, vc, c, pos0 + zhi, kvd, head_off, r4, nf4);
+  auto load_q = [&](int z, float (&qv)[NQ]) {
+    const float* qg = q + static_cast<size_t>(z) * tok_q + static_cast<size_t>(kvh) * gh;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) qv[u] = qg[min(tid + 256 * u, gh - 1)];
+  };
+  float qv[NQ];
+  load_q(zlo, qv);
+#pragma unroll
+  for (int u = 0; u < NV; ++u) {
+    const int f = min(tid + 256 * u, nf4 - 1);
+    const int j = f / r4, c4 = f - j * r4;
+    *reinterpret_cast<f32x4*>(&sK[j * KS + c4 * 4]) = R.k[u];
+    *reinterpret_cast<f32x4*>(&sV[j * HDM + c4 * 4]) = R.v[u];
+  }
+  for (int z = zlo; z < zhi; ++z) {
+    __syncthreads();  // the previous token's readers of sQ, sE and sMZ are done
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int i = tid + 256 * u;
+      if (i < gh) sQ[(i / hd) * HDM + i % hd] = qv[u];
+    }
+    if (z + 1 < zhi) load_q(z + 1, qv);
+    __syncthreads();
+    float o[OPT];
+    attn_token_chunk<HDM, OPT>(sK, sV, sQ, sE, sMZ, c, pos0 + z + 1, group, hd, gh, scale, o);
+    float* po = part_o + static_cast<size_t>(z) * tok_o;
+#pragma unroll
+    for (int u = 0; u < OPT; ++u) {
+      const int oi = tid + 256 * u;
+      if (oi < gh) {
+        const int hh = oi / hd, i = oi - hh * hd;
+        po[(static_cast<size_t>(kvh * group + hh) * max_chunks + c) * hd + i] = o[u];
+      }
+    }
+    if (tid < group)
+      part_mz[static_cast<size_t>(z) * tok_mz + static_cast<size_t>(kvh * group + tid) * max_chunks + c] = sMZ[tid];
   }
 }
 
@@ -374,16 +467,23 @@ hipError_t launch_attention_batch(const float* q, const float* kc, const float* 
   if (head_dim <= 0 || head_dim > 128 || head_dim % 4 || n_heads % n_kv_heads ||
       n_heads / n_kv_heads > ATTN_MAX_GROUP || pos0 < 0)
     return hipErrorInvalidValue;
-  // enough splits for every token's chunk count; a token's surplus splits
-  // return at once
-  const dim3 grid(n_kv_heads, attn_max_splits(pos0 / ATTN_CHUNK + 1, (pos0 + n_tok - 1) / ATTN_CHUNK + 1), n_tok);
+  if (n_tok <= 0) return hipSuccess;
+  // one work group per (kv head, chunk, token tile); tiles whose tokens do
+  // not reach a chunk return at once
+  // tokens per tile (MCPM_PREFILL_ATTN_TT overrides, a tuning aid)
+  static const int tt_env = [] {
+    const char* v = std::getenv("MCPM_PREFILL_ATTN_TT");
+    return v ? std::atoi(v) : 0;
+  }();
+  const int tt = tt_env >= 1 && tt_env <= 256 ? tt_env : 16;
+  const dim3 grid(n_kv_heads, (pos0 + n_tok - 1) / ATTN_CHUNK + 1, (n_tok + tt - 1) / tt);
   const size_t tok_q = static_cast<size_t>(n_heads) * head_dim;
   if (head_dim <= 64)
-    hipLaunchKernelGGL(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, nullptr, n_heads, n_kv_heads, head_dim,
-                       max_chunks, part.o, part.mz, pos0, tok_q, tok_o, tok_mz);
+    hipLaunchKernelGGL(k_attention_tile<64>, grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
+                       max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
   else
-    hipLaunchKernelGGL(k_attention<128>, grid, dim3(256), 0, s, q, kc, vc, nullptr, n_heads, n_kv_heads, head_dim,
-                       max_chunks, part.o, part.mz, pos0, tok_q, tok_o, tok_mz);
+    hipLaunchKernelGGL(k_attention_tile<128>, grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
+                       max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
   return hipGetLastError();
 }
 
