@@ -133,7 +133,10 @@ __device__ __forceinline__ h2 splat_h(int v) {
   return h2{h, h};
 }
 
-// A wave computes 16 rows x 16*NT tokens over all blocks.  MFMA operand
+// A work group takes 64 rows (one 16-row tile per wave) x 16*NT tokens over
+// all blocks.  The tokens' activations of a block (codes, d, bsums) are
+// staged in LDS once for the four waves, double-buffered: block b+1's loads
+// are in flight while block b's MFMAs run.  MFMA operand
 // layout (v_mfma_f32_16x16x32_f16): lane l feeds A row l%16 and B column
 // l%16 with K = 8*(l/16) .. +7; D lane l register i is row 4*(l/16)+i,
 // column l%16.  With K index k = 4*s + i over sub-blocks s and bytes i,
@@ -141,15 +144,52 @@ __device__ __forceinline__ h2 splat_h(int v) {
 // (low) and 64g + 32 + 4m + i (high) of the block for lane group m.
 template <int WT, int NT, int OCC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) k_gemm_q8k(const GemmArgs a) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  constexpr int TOK = 16 * NT;        // tokens of the work group's tile
+  constexpr int BROW = QK_K + 8;      // halves per token row of sB (padded: rows 132 dwords apart)
+  constexpr int PPT = TOK * 32 / 256; // 16-byte pieces of a block's codes per thread
+  __shared__ __attribute__((aligned(16))) _Float16 sB[2][TOK * BROW];
+  __shared__ float sXd[2][TOK];
+  __shared__ __attribute__((aligned(16))) _Float16 sBs[2][TOK * 16];
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int n_rt = (a.rows + 15) >> 4;
-  const int n_tg = (a.n_tok + 16 * NT - 1) / (16 * NT);
-  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tile >= n_rt * n_tg) return;
-  const int r0 = (tile % n_rt) * 16, t0 = (tile / n_rt) * (16 * NT);
+  const int n_rg = (n_rt + 3) >> 2;
+  const int rg = static_cast<int>(blockIdx.x) % n_rg, tg = static_cast<int>(blockIdx.x) / n_rg;
+  const int r0 = (4 * rg + wave) * 16, t0 = tg * TOK;
+  const bool live = r0 < a.rows;  // uniform in the wave: a wave past the rows only stages
   const size_t rows = static_cast<size_t>(a.rows);
   const int ra = min(r0 + c16, a.rows - 1);  // A operand row of this lane
   const int K = a.nb * QK_K;
+
+  // staging of block b: piece p = tid + 256k is 16 bytes (p % 32) of token
+  // p / 32's codes; thread t < TOK also takes token t's d, t < 2*TOK half of
+  // token t/2's bsums.  Tokens past the end re-read the last one (unused).
+  u32x4 pf[PPT], pbs;
+  float pxd = 0.0f;
+  auto fetch = [&](int b) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int p = tid + 256 * k;
+      const size_t tk = static_cast<size_t>(min(t0 + p / 32, a.n_tok - 1));
+      pf[k] = *reinterpret_cast<const u32x4*>(a.xh + tk * K + b * QK_K + (p % 32) * 8);
+    }
+    if (tid < TOK) pxd = a.xd[static_cast<size_t>(min(t0 + tid, a.n_tok - 1)) * a.nb + b];
+    if (tid < 2 * TOK)
+      pbs = *reinterpret_cast<const u32x4*>(a.xbs + (static_cast<size_t>(min(t0 + tid / 2, a.n_tok - 1)) * a.nb + b) * 16 +
+                                            (tid & 1) * 8);
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int p = tid + 256 * k;
+      *reinterpret_cast<u32x4*>(&sB[buf][(p / 32) * BROW + (p % 32) * 8]) = pf[k];
+    }
+    if (tid < TOK) sXd[buf][tid] = pxd;
+    if (tid < 2 * TOK) *reinterpret_cast<u32x4*>(&sBs[buf][(tid / 2) * 16 + (tid & 1) * 8]) = pbs;
+  };
+  fetch(0);
+  stash(0);
+  __syncthreads();
 
   float acc[NT][8][4], accm[NT][4];
 #pragma unroll
@@ -161,15 +201,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       for (int m = 0; m < 8; ++m) acc[n][m][i] = 0.0f;
     }
   }
-  int tok[NT];
-#pragma unroll
-  for (int n = 0; n < NT; ++n) tok[n] = min(t0 + 16 * n + c16, a.n_tok - 1);
-
   const h2 off1024{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
   const h2 off1026{static_cast<_Float16>(1026.0f), static_cast<_Float16>(1026.0f)};
   const f32x4 zero4{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int b = 0; b < a.nb; ++b) {
+    const int buf = b & 1;
+    if (b + 1 < a.nb) fetch(b + 1);  // in flight during this block's MFMAs
+    if (live) {
     // d (and dmin) of the four D rows of this lane
     float dw[4], dmw[4];
 #pragma unroll
@@ -258,8 +297,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
 
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-      const size_t tk = static_cast<size_t>(tok[n]);
-      const u32x4* xp = reinterpret_cast<const u32x4*>(a.xh + tk * K + b * QK_K + 64 * g);
+      const int lt = 16 * n + c16;  // the lane's token column in the tile
+      const u32x4* xp = reinterpret_cast<const u32x4*>(&sB[buf][lt * BROW + 64 * g]);
       uint32_t xw[32];
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
@@ -269,10 +308,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         xw[4 * v + 2] = x4.z;
         xw[4 * v + 3] = x4.w;
       }
-      const float xdv = a.xd[tk * a.nb + b];
+      const float xdv = sXd[buf][lt];
       uint32_t bsw[8];  // Q6_K: bsums of the token's block as fp16 pairs (lanes 0..15 use them)
       if constexpr (WT == 1) {
-        const u32x4* bp = reinterpret_cast<const u32x4*>(a.xbs + (tk * a.nb + b) * 16);
+        const u32x4* bp = reinterpret_cast<const u32x4*>(&sBs[buf][lt * 16]);
         const u32x4 b0 = bp[0], b1 = bp[1];
         bsw[0] = b0.x;
         bsw[1] = b0.y;
@@ -302,12 +341,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         for (int i = 0; i < 4; ++i) acc[n][m][i] = __builtin_fmaf(ds[i], D[i], acc[n][m][i]);
       }
       if constexpr (WT == 0) {
-        const h8 BM = *reinterpret_cast<const h8*>(a.xbs + (tk * a.nb + b) * 16 + 8 * (g & 1));
+        const h8 BM = *reinterpret_cast<const h8*>(&sBs[buf][lt * 16 + 8 * (g & 1)]);
         const f32x4 DM = __builtin_amdgcn_mfma_f32_16x16x32_f16(AM, BM, zero4, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) accm[n][i] = __builtin_fmaf(-(xdv * dmw[i]), DM[i], accm[n][i]);
       }
     }
+    }  // live
+    // block b+1 into the other buffer, whose last readers passed the previous barrier
+    if (b + 1 < a.nb) stash(buf ^ 1);
+    __syncthreads();
   }
 
 #pragma unroll
@@ -417,8 +460,9 @@ hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const Qu
   // four MFMA operand sets need the room.
   const int NT = nt_env == 1 || nt_env == 2 || nt_env == 4 ? nt_env : (q4 ? 2 : 1);
   const int OCC = occ_env == 1 ? 1 : 2;
-  const int n_tiles = ((rows + 15) / 16) * ((n_tok + 16 * NT - 1) / (16 * NT));
-  const dim3 grid((n_tiles + 3) / 4);
+  // one work group per 64 rows (four 16-row tiles) x 16*NT tokens
+  const int n_groups = ((rows + 63) / 64) * ((n_tok + 16 * NT - 1) / (16 * NT));
+  const dim3 grid(n_groups);
 #define MCPM_GEMM(N, O) \
   if (NT == N && OCC == O) { \
     if (q4) launch_kernel(k_gemm_q8k<0, N, O>, grid, dim3(256), 0, s, a); \
