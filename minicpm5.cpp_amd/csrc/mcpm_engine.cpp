@@ -209,7 +209,7 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
   auto* e = new mcpm_engine();
   e->ctx = ctx;
   e->cfg = c;
-  e->attn_fused = (qd / QK_K) % 4 == 0 && qd / QK_K <= 16 && c.head_dim % (qd / QK_K) == 0;
+  e->attn_fused = qd / QK_K <= 8 && c.head_dim % 8 == 0;
   int rc = MCPM_OK;
   int64_t wb = 0;
   auto T = [&](const std::string& n) { return f.find(n); };

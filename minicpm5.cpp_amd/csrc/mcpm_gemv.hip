@@ -90,16 +90,19 @@ __host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool attn,
 constexpr int NR = (MAX_NB + 15) / 16;
 constexpr int CHAIN_BATCH = 12;  // TILE chain: blocks whose LDS entries are read together
 
-// PRO_ATTN_EVEN: thread t < 256 combines values t*nb .. t*nb+nb-1 (one head:
-// head_dim % nb == 0, nb <= 16) over the chunks, ATTN_RB chunks' o_c per load
-// batch, the (m_c, z_c) of the first ATTN_MZ chunks loaded with the first.
-constexpr int ATTN_RB = 4, ATTN_MZ = 8, ATTN_MAX_NB = 16;
+// PRO_ATTN_EVEN: thread t < 32*nb combines the ATTN_VALS values t*8 .. t*8+7
+// (one head: head_dim % 8 == 0, nb <= 8) over the chunks.  The o_c of the
+// first ATTN_RB chunks and the (m_c, z_c) of the first ATTN_MZ are loaded with
+// the activations, before the weights; the next ATTN_BATCH chunks' loads (and
+// their maxima's) are issued together once the weights are queued, so a
+// context of up to ATTN_RB + ATTN_BATCH chunks costs one round trip after them.
+constexpr int ATTN_VALS = 8, ATTN_RB = 8, ATTN_MZ = 16, ATTN_BATCH = 16, ATTN_MAX_NB = 8;
 
 struct ProRegs {
   f32x4 x[NR][4];  // fp32 activations of the lane's 16 values
   f32x4 g[NR][4];  // RMSNorm weights, same layout
   float xp[MAX_NB];  // RMSNorm: x[t], x[t+256], ... of thread t < 256 (its partial's terms)
-  f32x4 ao[ATTN_RB][4];  // PRO_ATTN_EVEN: o_c of thread t's nb values, chunks 0..ATTN_RB-1
+  f32x4 ao[ATTN_RB][2];  // PRO_ATTN_EVEN: o_c of thread t's 8 values, chunks 0..ATTN_RB-1
   float2 amz[ATTN_MZ];   // (m_c, z_c) of its head, chunks 0..ATTN_MZ-1
   u32x4 q[NR];     // Q8_K codes of the lane's 16 values
   int bs[NR];      // Q8_K bsums[j]
@@ -134,13 +137,13 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
     }
   }
   if constexpr (PRO == PRO_ATTN_EVEN) {
-    if (wave >= 4) return;  // threads 0..255 form the activations
     const int t = static_cast<int>(threadIdx.x);
-    const int hd = a.head_dim, maxc = a.attn_max_chunks, nv4 = nb >> 2;
-    const int i0 = t * nb, h = i0 / hd, d0 = i0 - h * hd;
+    if (t * ATTN_VALS >= nb * QK_K) return;  // threads 0..32*nb-1 form the activations
+    const int hd = a.head_dim, maxc = a.attn_max_chunks;
+    const int i0 = t * ATTN_VALS, h = i0 / hd, d0 = i0 - h * hd;
     const int last = a.state[1] / ATTN_CHUNK;  // chunks 0..last
     const float2* mz = a.attn_mz + static_cast<size_t>(h) * maxc;
-    // only the chunks present and the thread's own vectors (uniform branches)
+    // only the chunks present (uniform branches)
 #pragma unroll
     for (int c = 0; c < ATTN_MZ; ++c)
       if (c <= last) X.amz[c] = mz[c];
@@ -148,9 +151,8 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
     for (int c = 0; c < ATTN_RB; ++c) {
       if (c <= last) {
         const f32x4* o = reinterpret_cast<const f32x4*>(a.x + (static_cast<size_t>(h) * maxc + c) * hd + d0);
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (v < nv4) X.ao[c][v] = o[v];
+        X.ao[c][0] = o[0];
+        X.ao[c][1] = o[1];
       }
     }
   }
@@ -185,68 +187,87 @@ __device__ __forceinline__ void store_xblock(uint32_t* L, const LdsPlan& P, int 
 // PRO_ATTN_EVEN: the attention output x[i] of threads' values (head h, dim
 // d) from the chunk partials, in chunk order (k_attn_combine's arithmetic):
 // m = max m_c; f_c = exp(m_c - m); Z = fma(z_c, f_c, Z); O = fma(o_c[d], f_c, O);
-// x = O / Z, into sx (fp32, nb*256), then a work-group barrier.
-__device__ __forceinline__ void attn_combine(const GemvArgs& a, const ProRegs& X, float* sx) {
-  const int nb = a.nb, hd = a.head_dim, maxc = a.attn_max_chunks, nv4 = nb >> 2;
-  if (threadIdx.x >= QK_K) {  // waves 4 and up take no values
-    __syncthreads();
-    return;
-  }
+// x = O / Z, into sx (fp32, nb*256).
+__device__ __forceinline__ void attn_combine_values(const GemvArgs& a, const ProRegs& X, float* sx) {
+  const int hd = a.head_dim, maxc = a.attn_max_chunks;
   const int t = static_cast<int>(threadIdx.x);
-  const int i0 = t * nb, h = i0 / hd, d0 = i0 - h * hd;
+  const int i0 = t * ATTN_VALS, h = i0 / hd, d0 = i0 - h * hd;
   const int nch = a.state[1] / ATTN_CHUNK + 1;
   const float2* mzp = a.attn_mz + static_cast<size_t>(h) * maxc;
+  const float* op = a.x + static_cast<size_t>(h) * maxc * hd + d0;
+  // When the context has them: chunks ATTN_RB .. ATTN_RB+ATTN_BATCH-1 and the
+  // maxima of chunks ATTN_MZ .. ATTN_MZ+ATTN_BATCH-1, all issued together at
+  // indices clamped to the last chunk (a repeated maximum changes nothing;
+  // repeated o_c are not used), the maxima first.
+  const bool more_mz = nch > ATTN_MZ, more_o = nch > ATTN_RB;  // uniform
+  float mb[ATTN_BATCH];
+  if (more_mz) {
+#pragma unroll
+    for (int k = 0; k < ATTN_BATCH; ++k) mb[k] = mzp[min(ATTN_MZ + k, nch - 1)].x;
+  }
+  f32x4 ob[ATTN_BATCH][2];
+  float2 zb[ATTN_BATCH];
+  auto load_batch = [&](int c0) {
+#pragma unroll
+    for (int k = 0; k < ATTN_BATCH; ++k) {
+      const int c = min(c0 + k, nch - 1);
+      zb[k] = mzp[c];
+      const f32x4* o = reinterpret_cast<const f32x4*>(op + static_cast<size_t>(c) * hd);
+      ob[k][0] = o[0];
+      ob[k][1] = o[1];
+    }
+  };
+  if (more_o) load_batch(ATTN_RB);
   float m = X.amz[0].x;
 #pragma unroll
   for (int c = 1; c < ATTN_MZ; ++c)
     if (c < nch) m = fmaxf(m, X.amz[c].x);
-  for (int c = ATTN_MZ; c < nch; ++c) m = fmaxf(m, mzp[c].x);
-  float Z = 0.0f;
-  f32x4 O[4];
+  if (more_mz) {
 #pragma unroll
-  for (int v = 0; v < 4; ++v) O[v] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  auto step = [&](float2 mz, const f32x4 (&o)[4]) {
+    for (int k = 0; k < ATTN_BATCH; ++k) m = fmaxf(m, mb[k]);
+  }
+  for (int c0 = ATTN_MZ + ATTN_BATCH; c0 < nch; c0 += ATTN_BATCH) {
+#pragma unroll
+    for (int k = 0; k < ATTN_BATCH; ++k) mb[k] = mzp[min(c0 + k, nch - 1)].x;
+#pragma unroll
+    for (int k = 0; k < ATTN_BATCH; ++k) m = fmaxf(m, mb[k]);
+  }
+  float Z = 0.0f;
+  f32x4 O[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+  auto step = [&](float2 mz, const f32x4 (&o)[2]) {
     const float f = exp_f32(mz.x - m);
     Z = __builtin_fmaf(mz.y, f, Z);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      if (v < nv4) {
-        O[v].x = __builtin_fmaf(o[v].x, f, O[v].x);
-        O[v].y = __builtin_fmaf(o[v].y, f, O[v].y);
-        O[v].z = __builtin_fmaf(o[v].z, f, O[v].z);
-        O[v].w = __builtin_fmaf(o[v].w, f, O[v].w);
-      }
+    for (int v = 0; v < 2; ++v) {
+      O[v].x = __builtin_fmaf(o[v].x, f, O[v].x);
+      O[v].y = __builtin_fmaf(o[v].y, f, O[v].y);
+      O[v].z = __builtin_fmaf(o[v].z, f, O[v].z);
+      O[v].w = __builtin_fmaf(o[v].w, f, O[v].w);
     }
   };
+  // the steps in chunk order
 #pragma unroll
   for (int c = 0; c < ATTN_RB; ++c)
     if (c < nch) step(X.amz[c], X.ao[c]);
-  // further chunks, ATTN_RB at a time: loads first, then the steps in order
-  for (int c0 = ATTN_RB; c0 < nch; c0 += ATTN_RB) {
-    f32x4 ob[ATTN_RB][4];
-    float2 mb[ATTN_RB];
+  for (int c0 = ATTN_RB; c0 < nch; c0 += ATTN_BATCH) {
+    if (c0 > ATTN_RB) load_batch(c0);
 #pragma unroll
-    for (int k = 0; k < ATTN_RB; ++k) {
-      if (c0 + k < nch) {
-        const int c = c0 + k;
-        mb[k] = mzp[c];
-        const f32x4* o = reinterpret_cast<const f32x4*>(a.x + (static_cast<size_t>(h) * maxc + c) * hd + d0);
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (v < nv4) ob[k][v] = o[v];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < ATTN_RB; ++k)
-      if (c0 + k < nch) step(mb[k], ob[k]);
+    for (int k = 0; k < ATTN_BATCH; ++k)
+      if (c0 + k < nch) step(zb[k], ob[k]);
   }
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    if (v < nv4) {
-      const f32x4 r = O[v];
-      *reinterpret_cast<f32x4*>(sx + i0 + 4 * v) = f32x4{r.x / Z, r.y / Z, r.z / Z, r.w / Z};
-    }
+  for (int v = 0; v < 2; ++v) {
+    const f32x4 r = O[v];
+    *reinterpret_cast<f32x4*>(sx + i0 + 4 * v) = f32x4{r.x / Z, r.y / Z, r.z / Z, r.w / Z};
   }
+}
+
+// attn_combine_values on the threads that hold values, then a work-group
+// barrier.
+__device__ __forceinline__ void attn_combine(const GemvArgs& a, const ProRegs& X, float* sx) {
+  // threads past the values take no part but the barrier, which every thread
+  // reaches exactly once (a wave may hold both kinds when nb == 1)
+  if (static_cast<int>(threadIdx.x) * ATTN_VALS < a.nb * QK_K) attn_combine_values(a, X, sx);
   __syncthreads();
 }
 
@@ -1030,7 +1051,7 @@ int gemv_grid(const GemvArgs& a0, int n_cu) {
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s) {
   if (a.nb <= 0 || a.nb > MAX_NB) return hipErrorInvalidValue;
-  if (prologue == PRO_ATTN_EVEN && (a.nb > ATTN_MAX_NB || a.nb % 4 || a.head_dim <= 0 || a.head_dim % a.nb))
+  if (prologue == PRO_ATTN_EVEN && (a.nb > ATTN_MAX_NB || a.head_dim <= 0 || a.head_dim % ATTN_VALS))
     return hipErrorInvalidValue;
   if (a.pair && a.reg[0].w.type != a.reg[1].w.type) return hipErrorInvalidValue;
   GemvArgs b = a;
