@@ -251,6 +251,86 @@ __device__ __forceinline__ void attn_token_chunk(const float* sK, const float* s
   }
 }
 
+// NT consecutive tokens (token k with context Tk[k], k < NT; every Tk[k] >
+// c*ATTN_CHUNK) on one chunk: each token's sums are attn_token_chunk's, in
+// the same order, and the tokens' chains run side by side, so each K and V
+// value read from LDS serves NT tokens.  Token k's queries at sQ + k*QSZ, its
+// softmax terms at sE + k*ESZ, its (m_c, z_c) at mz[k*ATTN_MAX_GROUP + hh], its
+// outputs in o[k].
+template <int HDM, int OPT, int NT>
+__device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* sV, const float* sQ, float* sE,
+                                                  float2* mz, int c, const int (&Tk)[NT], int group, int hd, int gh,
+                                                  float scale, float (&o)[NT][OPT]) {
+  constexpr int KS = HDM + 4;
+  constexpr int QSZ = ATTN_MAX_GROUP * HDM, ESZ = ATTN_MAX_GROUP * ATTN_CHUNK;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int hh = wave; hh < group; hh += 4) {
+    const float* kt = &sK[lane * KS];
+    float dot[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) dot[k] = 0.0f;
+#pragma unroll 4
+    for (int i = 0; i < hd; i += 4) {
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(kt + i);
+#pragma unroll
+      for (int k = 0; k < NT; ++k) {
+        const f32x4 q4 = *reinterpret_cast<const f32x4*>(sQ + k * QSZ + hh * HDM + i);
+        dot[k] = __builtin_fmaf(q4.x, k4.x, dot[k]);
+        dot[k] = __builtin_fmaf(q4.y, k4.y, dot[k]);
+        dot[k] = __builtin_fmaf(q4.z, k4.z, dot[k]);
+        dot[k] = __builtin_fmaf(q4.w, k4.w, dot[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      const bool present = c * ATTN_CHUNK + lane < Tk[k];
+      const float sv = present ? dot[k] * scale : -1e9f;
+      const float mc = fmaxf(wave_max_fast(sv), -1e9f);
+      const float e = present ? exp_f32(sv - mc) : 0.0f;
+      const float z = wave_tree_sum_fast(e);
+      sE[k * ESZ + hh * ATTN_CHUNK + lane] = e;
+      if (lane == 0) mz[k * ATTN_MAX_GROUP + hh] = make_float2(mc, z);
+    }
+  }
+  __syncthreads();
+  // positions 0..nt_k-1 for token k: the first nt_lo for every token, then
+  // the later ones for the tokens that have them
+  int nt[NT];
+#pragma unroll
+  for (int k = 0; k < NT; ++k) nt[k] = min(ATTN_CHUNK, Tk[k] - c * ATTN_CHUNK);
+  int nt_lo = nt[0], nt_hi = nt[0];
+#pragma unroll
+  for (int k = 1; k < NT; ++k) {
+    nt_lo = min(nt_lo, nt[k]);
+    nt_hi = max(nt_hi, nt[k]);
+  }
+#pragma unroll
+  for (int u = 0; u < OPT; ++u) {
+    const int oi = tid + 256 * u;
+    float acc[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) acc[k] = 0.0f;
+    if (oi < gh) {
+      const int hh = oi / hd, i = oi - hh * hd;
+      const float* eh = &sE[hh * ATTN_CHUNK];
+#pragma unroll 4
+      for (int j = 0; j < nt_lo; ++j) {
+        const float v = sV[j * HDM + i];
+#pragma unroll
+        for (int k = 0; k < NT; ++k) acc[k] = __builtin_fmaf(eh[k * ESZ + j], v, acc[k]);
+      }
+      for (int j = nt_lo; j < nt_hi; ++j) {
+        const float v = sV[j * HDM + i];
+#pragma unroll
+        for (int k = 0; k < NT; ++k)
+          if (j < nt[k]) acc[k] = __builtin_fmaf(eh[k * ESZ + j], v, acc[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NT; ++k) o[k][u] = acc[k];
+  }
+}
+
 template <int HDM>
 __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, const int* __restrict__ state,
@@ -349,11 +429,13 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
 
 // Prefill: chunk blockIdx.y of kv head blockIdx.x for the tile of tt
 // consecutive tokens from blockIdx.z * tt (token z at position pos0 + z,
-// its own q and partials).  The chunk's K and V rows are staged once; every
-// token of the tile whose context reaches the chunk then runs
-// attn_token_chunk on it -- the arithmetic of k_attention's launch for that
-// token -- and writes its partial for the chunk.  Rows the tile stages past
-// a token's context take no part in that token's sums.
+// its own q and partials).  The chunk's K and V rows are staged once; the
+// tile's tokens whose context reaches the chunk then run on it ATTN_TOK at a
+// time (attn_tokens_chunk: for each token the arithmetic of k_attention's
+// launch for that token) and write their partials for the chunk.  Rows the
+// tile stages past a token's context take no part in that token's sums.
+constexpr int ATTN_TOK = 4;
+
 template <int HDM>
 __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict__ q, const float* __restrict__ kc,
                                                         const float* __restrict__ vc, int n_heads, int n_kv_heads,
@@ -364,11 +446,13 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
   constexpr int OPT = ATTN_MAX_GROUP * HDM / 256;
   constexpr int NQ = ATTN_MAX_GROUP * HDM / 256;
   constexpr int KS = HDM + 4;
+  constexpr int NT = ATTN_TOK;
+  constexpr int QSZ = ATTN_MAX_GROUP * HDM, ESZ = ATTN_MAX_GROUP * ATTN_CHUNK;
   __shared__ float sK[ATTN_CHUNK * KS];
   __shared__ float sV[ATTN_CHUNK * HDM];
-  __shared__ float sQ[ATTN_MAX_GROUP * HDM];
-  __shared__ float sE[ATTN_MAX_GROUP * ATTN_CHUNK];
-  __shared__ float2 sMZ[ATTN_MAX_GROUP];
+  __shared__ float sQ[NT * QSZ];
+  __shared__ float sE[NT * ESZ];
+  __shared__ float2 sMZ[NT * ATTN_MAX_GROUP];
   const int tid = threadIdx.x;
   const int kvh = blockIdx.x, c = blockIdx.y;
   const int z0 = static_cast<int>(blockIdx.z) * tt;
@@ -384,12 +468,16 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
 
   AttnRegs<NV> R;
   attn_load_chunk<NV>(R, kc, vc, c, pos0 + zhi, kvd, head_off, r4, nf4);
-  auto load_q = [&](int z, float (&qv)[NQ]) {
-    const float* qg = q + static_cast<size_t>(z) * tok_q + static_cast<size_t>(kvh) * gh;
+  // the queries of tokens z .. z+NT-1 (tokens past the tile re-read its last)
+  auto load_q = [&](int z, float (&qv)[NT][NQ]) {
 #pragma unroll
-    for (int u = 0; u < NQ; ++u) qv[u] = qg[min(tid + 256 * u, gh - 1)];
+    for (int k = 0; k < NT; ++k) {
+      const float* qg = q + static_cast<size_t>(min(z + k, zhi - 1)) * tok_q + static_cast<size_t>(kvh) * gh;
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) qv[k][u] = qg[min(tid + 256 * u, gh - 1)];
+    }
   };
-  float qv[NQ];
+  float qv[NT][NQ];
   load_q(zlo, qv);
 #pragma unroll
   for (int u = 0; u < NV; ++u) {
@@ -398,28 +486,40 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
     *reinterpret_cast<f32x4*>(&sK[j * KS + c4 * 4]) = R.k[u];
     *reinterpret_cast<f32x4*>(&sV[j * HDM + c4 * 4]) = R.v[u];
   }
-  for (int z = zlo; z < zhi; ++z) {
-    __syncthreads();  // the previous token's readers of sQ, sE and sMZ are done
+  for (int z = zlo; z < zhi; z += NT) {
+    __syncthreads();  // the previous tokens' readers of sQ, sE and sMZ are done
 #pragma unroll
-    for (int u = 0; u < NQ; ++u) {
-      const int i = tid + 256 * u;
-      if (i < gh) sQ[(i / hd) * HDM + i % hd] = qv[u];
-    }
-    if (z + 1 < zhi) load_q(z + 1, qv);
-    __syncthreads();
-    float o[OPT];
-    attn_token_chunk<HDM, OPT>(sK, sV, sQ, sE, sMZ, c, pos0 + z + 1, group, hd, gh, scale, o);
-    float* po = part_o + static_cast<size_t>(z) * tok_o;
+    for (int k = 0; k < NT; ++k) {
 #pragma unroll
-    for (int u = 0; u < OPT; ++u) {
-      const int oi = tid + 256 * u;
-      if (oi < gh) {
-        const int hh = oi / hd, i = oi - hh * hd;
-        po[(static_cast<size_t>(kvh * group + hh) * max_chunks + c) * hd + i] = o[u];
+      for (int u = 0; u < NQ; ++u) {
+        const int i = tid + 256 * u;
+        if (i < gh) sQ[k * QSZ + (i / hd) * HDM + i % hd] = qv[k][u];
       }
     }
-    if (tid < group)
-      part_mz[static_cast<size_t>(z) * tok_mz + static_cast<size_t>(kvh * group + tid) * max_chunks + c] = sMZ[tid];
+    if (z + NT < zhi) load_q(z + NT, qv);
+    __syncthreads();
+    int Tk[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) Tk[k] = pos0 + min(z + k, zhi - 1) + 1;
+    float o[NT][OPT];
+    attn_tokens_chunk<HDM, OPT, NT>(sK, sV, sQ, sE, sMZ, c, Tk, group, hd, gh, scale, o);
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      if (z + k < zhi) {
+        float* po = part_o + static_cast<size_t>(z + k) * tok_o;
+#pragma unroll
+        for (int u = 0; u < OPT; ++u) {
+          const int oi = tid + 256 * u;
+          if (oi < gh) {
+            const int hh = oi / hd, i = oi - hh * hd;
+            po[(static_cast<size_t>(kvh * group + hh) * max_chunks + c) * hd + i] = o[k][u];
+          }
+        }
+        if (tid < group)
+          part_mz[static_cast<size_t>(z + k) * tok_mz + static_cast<size_t>(kvh * group + tid) * max_chunks + c] =
+              sMZ[k * ATTN_MAX_GROUP + tid];
+      }
+    }
   }
 }
 
