@@ -28,6 +28,7 @@
 //  * Q4_K's min sum (sum over sub-blocks of mn * pair-sum of bsums) is one
 //    more MFMA: A = mn[k/2] for k < 16, B = bsums[k].
 // Attention per token is the decode kernel at that token's position.
+#include <cstdio>
 #include <cstdlib>
 
 #include "mcpm_device.h"
@@ -224,7 +225,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       }
     }
     // A operands of the eight lane groups (and Q4_K's min operand)
-    h8 A[8], AH[8], AM, AC[8], AS[8];
+    h8 A[8], AH[8], AM;
+    uint32_t acw[8];  // Q6_K: the offset operand's one nonzero dword per lane group
+    h2 sc[4];         // Q6_K: scales 4g .. 4g+3 of this lane's row, as fp16 pairs
     if constexpr (WT == 0) {
       const u32x4 hdr = *reinterpret_cast<const u32x4*>(a.w.p1 + (static_cast<size_t>(b) * rows + ra) * 16);
       const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
@@ -254,7 +257,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       // scales 4g .. 4g+3 (signed bytes) = dword g of the 16 scales
       const uint32_t scw = g == 0 ? scr.x : g == 1 ? scr.y : g == 2 ? scr.z : scr.w;
       // the offset operand: K entries 0, 1 (lanes 0..15, halves 0, 1) are
-      // sc[2m], sc[2m+1] of this lane's row
+      // -sc[2m], -sc[2m+1] of this lane's row, the rest zero
       const uint32_t scall[4] = {scr.x, scr.y, scr.z, scr.w};
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
@@ -262,9 +265,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         const int lo = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1), 8);
         const int hi = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1) + 8, 8);
         const h2 pair{static_cast<_Float16>(static_cast<float>(-lo)), static_cast<_Float16>(static_cast<float>(-hi))};
-        AC[m] = g == 0 ? __builtin_bit_cast(h8, u32x4{h2bits(pair), 0u, 0u, 0u}) : h8{};
+        acw[m] = g == 0 ? h2bits(pair) : 0u;
       }
-      h2 sc[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) sc[k] = splat_h(__builtin_amdgcn_sbfe(static_cast<int>(scw), 8 * k, 8));
       const uint8_t* ql = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
@@ -291,23 +293,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)];
         A[m] = a_operand((lw[m] >> nib) & 0x0f0f0f0fu, (lw[8 + m] >> nib) & 0x0f0f0f0fu, sa, sb, off1024);
         AH[m] = a_operand((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, off1026);
-        AS[m] = __builtin_bit_cast(h8, u32x4{h2bits(sa), h2bits(sa), h2bits(sb), h2bits(sb)});
       }
     }
 
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
       const int lt = 16 * n + c16;  // the lane's token column in the tile
-      const u32x4* xp = reinterpret_cast<const u32x4*>(&sB[buf][lt * BROW + 64 * g]);
-      uint32_t xw[32];
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const u32x4 x4 = xp[v];
-        xw[4 * v] = x4.x;
-        xw[4 * v + 1] = x4.y;
-        xw[4 * v + 2] = x4.z;
-        xw[4 * v + 3] = x4.w;
-      }
+      const uint32_t* xp = reinterpret_cast<const uint32_t*>(&sB[buf][lt * BROW + 64 * g]);
       const float xdv = sXd[buf][lt];
       uint32_t bsw[8];  // Q6_K: bsums of the token's block as fp16 pairs (lanes 0..15 use them)
       if constexpr (WT == 1) {
@@ -327,13 +319,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       for (int i = 0; i < 4; ++i) ds[i] = xdv * dw[i];
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
-        const h8 B = __builtin_bit_cast(h8, u32x4{xw[2 * m], xw[2 * m + 1], xw[16 + 2 * m], xw[17 + 2 * m]});
+        // dwords 2m, 2m+1 (low K-half) and 16+2m, 17+2m (high) of the lane's 32
+        const uint2 xl = *reinterpret_cast<const uint2*>(xp + 2 * m);
+        const uint2 xh = *reinterpret_cast<const uint2*>(xp + 16 + 2 * m);
+        const h8 B = __builtin_bit_cast(h8, u32x4{xl.x, xl.y, xh.x, xh.y});
         f32x4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[m], B, zero4, 0, 0, 0);
         if constexpr (WT == 1) {
           const f32x4 DH = __builtin_amdgcn_mfma_f32_16x16x32_f16(AH[m], B, zero4, 0, 0, 0);
-          const h8 BC = g == 0 ? __builtin_bit_cast(h8, u32x4{bsw[m], 0u, 0u, 0u}) : h8{};
-          const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC[m], BC, zero4, 0, 0, 0);  // -C
-          const f32x4 EC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AS[m], B, NC, 0, 0, 0);      // E - C
+          const h8 AC = __builtin_bit_cast(h8, u32x4{acw[m], 0u, 0u, 0u});
+          const h8 BC = __builtin_bit_cast(h8, u32x4{g == 0 ? bsw[m] : 0u, 0u, 0u, 0u});
+          const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)];
+          const h8 AS = __builtin_bit_cast(h8, u32x4{h2bits(sa), h2bits(sa), h2bits(sb), h2bits(sb)});
+          const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC, BC, zero4, 0, 0, 0);  // -C
+          const f32x4 EC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AS, B, NC, 0, 0, 0);      // E - C
 #pragma unroll
           for (int i = 0; i < 4; ++i) D[i] = __builtin_fmaf(32.0f, EC[i], __builtin_fmaf(16.0f, DH[i], D[i]));
         }
@@ -445,21 +443,26 @@ hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const Qu
   if (w.type != MCPM_TYPE_Q4_K && w.type != MCPM_TYPE_Q6_K) return hipErrorInvalidValue;
   GemmArgs a{w, rows, nb, n_tok, q.xh, q.xd, q.xbs, out, ld_out, add ? 1 : 0};
   // token tiles per wave and waves per SIMD (MCPM_PREFILL_NT=1|2|4 and
-  // MCPM_PREFILL_OCC=1|2 override, tuning aids)
-  static const int nt_env = [] {
-    const char* v = std::getenv("MCPM_PREFILL_NT");
-    return v ? std::atoi(v) : 0;
-  }();
-  static const int occ_env = [] {
-    const char* v = std::getenv("MCPM_PREFILL_OCC");
-    return v ? std::atoi(v) : 0;
-  }();
+  // MCPM_PREFILL_OCC=1|2 override, tuning aids; "a,b" sets Q4_K a, Q6_K b)
+  struct Pair {
+    int q4 = 0, q6 = 0;
+  };
+  auto env_pair = [](const char* name) {
+    Pair p;
+    if (const char* v = std::getenv(name)) {
+      const int n = std::sscanf(v, "%d,%d", &p.q4, &p.q6);
+      if (n == 1) p.q6 = p.q4;
+    }
+    return p;
+  };
+  static const Pair nt_env = env_pair("MCPM_PREFILL_NT"), occ_env = env_pair("MCPM_PREFILL_OCC");
   const bool q4 = w.type == MCPM_TYPE_Q4_K;
+  const int nt_e = q4 ? nt_env.q4 : nt_env.q6, occ_e = q4 ? occ_env.q4 : occ_env.q6;
   // Defaults: two waves per SIMD (registers held to 256 so a second wave hides
   // the first's load latency); 32 tokens per wave for Q4_K, 16 for Q6_K, whose
   // four MFMA operand sets need the room.
-  const int NT = nt_env == 1 || nt_env == 2 || nt_env == 4 ? nt_env : (q4 ? 2 : 1);
-  const int OCC = occ_env == 1 ? 1 : 2;
+  const int NT = nt_e == 1 || nt_e == 2 || nt_e == 4 ? nt_e : (q4 ? 2 : 1);
+  const int OCC = occ_e == 1 ? 1 : 2;
   // one work group per 64 rows (four 16-row tiles) x 16*NT tokens
   const int n_groups = ((rows + 63) / 64) * ((n_tok + 16 * NT - 1) / (16 * NT));
   const dim3 grid(n_groups);
