@@ -11,7 +11,9 @@ forward plus argmax on the device).  --warmup steps run untimed, then exactly
 
 Printed: one JSON line with tokens/s, the achieved HBM bandwidth of the
 dominant kernel against the 8 TB/s peak (HIP events around its launches, on
-the engine stream), and the reference's CPU path timed on this host's cores.
+the engine stream), and the reference's CPU path timed on this host's cores;
+beside them the long-context prefill and sampled decode, and the single-op
+configurations (one GEMV cold and warm, the FFN block, QKV + attention).
 """
 import argparse
 import json
@@ -118,6 +120,83 @@ def sampled_measure(eng, cfg, n_prompt=1024, n_gen=512, temperature=0.8, top_p=0
             "greedy_tokens_per_s_same_positions": round((n_gen - 1) / tg, 1)}
 
 
+def ops_measure(ctx, eng, cfg, bd, cold_mb=640):
+    """The single-op configurations, kernel time from HIP events at each
+    kernel's start and end:
+      C1  one Q4_K GEMV 5760 x 2304 with the ties-even Q8_K quantize prologue
+          (mcpm_gemv_q4_K), warm (one weight copy, resident in the 256 MB
+          Infinity Cache) and cold (a rotation over cold_mb of copies);
+      C2  the FFN block as the engine runs it (RMSNorm + Q8_K + gate/up +
+          SwiGLU, then Q8_K + down + residual: two fused kernels), per layer
+          of the decode measured above, weights streamed from HBM;
+      C3  QKV (with RoPE and the KV append) + attention at contexts 512, 2048
+          and 4096 (the engine's kernels after a prompt of that length)."""
+    out = {}
+    rows, cols = 5760, 2304
+    w = mcpm.synth_normal(SEED + 10, 1, rows * cols, 0.0, 0.02).reshape(rows, cols)
+    native = mcpm.quantize_rows(mcpm.TYPE_Q4_K, w)
+    n_copies = max(1, -(-(cold_mb << 20) // native.nbytes))
+    copies = [ctx.tensor(native, mcpm.TYPE_Q4_K, cols, rows) for _ in range(n_copies)]
+    x = ctx.upload(mcpm.synth_normal(SEED + 10, 2, cols))
+    y = ctx.alloc(rows * 4)
+    c1_bytes = native.nbytes + cols * 4 + rows * 4
+
+    def timed(seq, reps):
+        ctx.set_op_timing(True)
+        for _ in range(reps):
+            for t in seq:
+                mcpm.check(ctx.lib.mcpm_gemv_q4_K(ctx.h, t.h, x.ptr, y.ptr, rows, cols))
+        ms, n = ctx.op_time()
+        ctx.set_op_timing(False)
+        return 1e3 * ms / max(n, 1)
+
+    timed(copies[:1], 20)
+    c1 = {"bytes": c1_bytes}
+    for name, seq, reps in (("warm", copies[:1], 400), ("cold", copies, 4)):
+        us = timed(seq, reps)
+        gbps = c1_bytes / (us * 1e-6) / 1e9
+        c1[name] = {"us": round(us, 3), "GBps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+    c1["cold"]["rotation_MB"] = round(n_copies * native.nbytes / 1e6, 1)
+    out["c1_gemv_q4k_5760x2304"] = c1
+    for t in copies:
+        t.free()
+    x.free()
+    y.free()
+
+    gu, dn = bd["gate_up"], bd["down"]
+    c2_us = gu["avg_us"] + dn["avg_us"]
+    c2_bytes = gu["bytes_per_launch"] + dn["bytes_per_launch"]
+    out["c2_ffn_block"] = {"us": round(c2_us, 3), "bytes": c2_bytes,
+                           "GBps": round(c2_bytes / (c2_us * 1e-6) / 1e9, 1),
+                           "frac": round(c2_bytes / (c2_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                           "kernels_us": {"gate_up": round(gu["avg_us"], 3), "down": round(dn["avg_us"], 3)}}
+
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    qkv_w = eng.kernel_bytes(mcpm.KC_QKV)
+    c3 = {}
+    eng.init_kv_cache(4096 + 64)
+    for ctx_len in (512, 2048, 4096):
+        prompt = np.random.default_rng(SEED + ctx_len).integers(0, cfg.vocab, ctx_len).astype(np.int32)
+        eng.generate_greedy(prompt, 1)
+        eng.sync()
+        us = {}
+        for kc, name in ((mcpm.KC_QKV, "qkv"), (mcpm.KC_ATTN, "attn")):
+            eng.set_kernel_timing(kc)
+            eng.decode_steps(4)
+            eng.sync()
+            ms, n = eng.kernel_time()
+            eng.set_kernel_timing(-1)
+            us[name] = 1e3 * ms / max(n, 1)
+        # KV read at about ctx_len + 4 positions, plus the new row's append
+        b = qkv_w + 2 * (ctx_len + 4) * kvd * 4 + 2 * kvd * 4
+        t = us["qkv"] + us["attn"]
+        c3[str(ctx_len)] = {"us": round(t, 3), "qkv_us": round(us["qkv"], 3), "attn_us": round(us["attn"], 3),
+                            "bytes": b, "GBps": round(b / (t * 1e-6) / 1e9, 1),
+                            "frac": round(b / (t * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+    out["c3_qkv_attention"] = c3
+    return out
+
+
 def cpu_baseline(image, cfg_vocab, budget_s=15.0):
     """The reference's own CPU ops (oracle/_ref, AVX2 + OpenMP) when built,
     else the oracle's C restatement, timed on a bounded decode sample."""
@@ -158,6 +237,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 1024-token prefill measurement")
     ap.add_argument("--no-sampled", action="store_true",
                     help="skip the sampled decode after a 1024-token prompt (device sampler)")
+    ap.add_argument("--no-ops", action="store_true",
+                    help="skip the single-op configurations (one GEMV cold/warm, FFN block, QKV + attention)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run device-to-device copies of this many MB (the reference kernel of known "
                          "size for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -228,6 +309,15 @@ def main():
             f"(T {sampled['temperature']}, top-p {sampled['top_p']}; greedy at the same positions "
             f"{sampled['greedy_tokens_per_s_same_positions']:.1f} tok/s)")
 
+    ops = None
+    if not args.no_ops:
+        ops = ops_measure(ctx, eng, cfg, bd)
+        c1 = ops["c1_gemv_q4k_5760x2304"]
+        log(f"ops: C1 GEMV {c1['warm']['us']:.2f} us warm ({c1['warm']['GBps']:.0f} GB/s), "
+            f"{c1['cold']['us']:.2f} us cold ({c1['cold']['GBps']:.0f} GB/s); "
+            f"C2 FFN block {ops['c2_ffn_block']['us']:.2f} us; C3 QKV+attention "
+            + ", ".join(f"{k}: {v['us']:.2f} us" for k, v in ops["c3_qkv_attention"].items()))
+
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -267,6 +357,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": prefill,
         "sampled_decode": sampled,
+        "ops": ops,
     }
     print(json.dumps(res), flush=True)
     eng.free()

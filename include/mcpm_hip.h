@@ -151,6 +151,17 @@ int mcpm_argmax(mcpm_ctx *ctx, const float *x, int n, int *out);
  * from mcpm_sample_logits only for draws within rounding of a boundary. */
 int mcpm_sample_device(mcpm_ctx *ctx, const float *x, int n, float temperature, float top_p, float r, int *out);
 
+/* Per-op kernel timing, a measurement aid with no counterpart in the
+ * reference (its ops are timed with wall clocks around OpenMP regions).
+ * While enabled, each launch of the single-kernel GEMV entries
+ * (mcpm_gemv_q4_K_q8_K, mcpm_gemv_q6_K_q8_K, mcpm_gemv_qkv_q8_K,
+ * mcpm_gemv_gate_up_q4_K_q8_K, mcpm_gemv_q4_K, mcpm_gemv_q6_K) records events
+ * at its kernel's start and end.  mcpm_op_time waits for the stream, returns
+ * the summed kernel time and the number of timed launches since the last
+ * call (or since timing was enabled), and starts a new count. */
+int mcpm_set_op_timing(mcpm_ctx *ctx, int enable);
+int mcpm_op_time(mcpm_ctx *ctx, double *total_ms, int64_t *launches);
+
 /* ------------------------------------------------------------ engine ----- */
 
 typedef struct {

@@ -190,6 +190,28 @@ int check_q8k_gemv(const mcpm_tensor* w, int type, int rows, int cols, const cha
   return MCPM_OK;
 }
 
+// The single-kernel GEMV entries launch through here: with per-op timing on,
+// the kernel records an event pair at its start and end (hipExtLaunchKernel).
+template <class F>
+hipError_t op_launch(mcpm_ctx* c, F&& launch) {
+  if (!c->op_timing) return launch();
+  if (c->op_used == c->op_events.size()) {
+    std::pair<hipEvent_t, hipEvent_t> p{nullptr, nullptr};
+    hipError_t err = hipEventCreate(&p.first);
+    if (err == hipSuccess) err = hipEventCreate(&p.second);
+    if (err != hipSuccess) {
+      if (p.first) (void)hipEventDestroy(p.first);
+      return err;
+    }
+    c->op_events.push_back(p);
+  }
+  const auto& p = c->op_events[c->op_used++];
+  g_launch_timing = LaunchTiming{p.first, p.second};
+  const hipError_t err = launch();
+  g_launch_timing = LaunchTiming{};
+  return err;
+}
+
 }  // namespace
 
 extern "C" {
@@ -238,6 +260,10 @@ void mcpm_destroy(mcpm_ctx* c) {
   if (c->d_attn_part) (void)hipFree(c->d_attn_part);
   if (c->d_argmax_part) (void)hipFree(c->d_argmax_part);
   if (c->d_sample) (void)hipFree(c->d_sample);
+  for (auto& p : c->op_events) {
+    (void)hipEventDestroy(p.first);
+    (void)hipEventDestroy(p.second);
+  }
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -345,6 +371,29 @@ int mcpm_tensor_dequantize_rows(mcpm_ctx* c, const mcpm_tensor* t, int64_t row0,
 
 // -------------------------------------------------------------- per-op ----
 
+int mcpm_set_op_timing(mcpm_ctx* c, int enable) {
+  if (!c) return fail(MCPM_ERR_ARG, "mcpm_set_op_timing: null context");
+  MCPM_HIP(hipStreamSynchronize(c->stream));
+  c->op_timing = enable != 0;
+  c->op_used = 0;
+  return MCPM_OK;
+}
+
+int mcpm_op_time(mcpm_ctx* c, double* total_ms, int64_t* launches) {
+  if (!c || !total_ms || !launches) return fail(MCPM_ERR_ARG, "mcpm_op_time: null argument");
+  MCPM_HIP(hipStreamSynchronize(c->stream));
+  double sum = 0.0;
+  for (size_t i = 0; i < c->op_used; ++i) {
+    float ms = 0.0f;
+    MCPM_HIP(hipEventElapsedTime(&ms, c->op_events[i].first, c->op_events[i].second));
+    sum += ms;
+  }
+  *total_ms = sum;
+  *launches = static_cast<int64_t>(c->op_used);
+  c->op_used = 0;
+  return MCPM_OK;
+}
+
 int mcpm_quantize_row_q8_K(mcpm_ctx* c, const float* x, int n, void* y) {
   if (!c || !x || !y || n <= 0 || n % QK_K) return fail(MCPM_ERR_ARG, "mcpm_quantize_row_q8_K: bad argument");
   MCPM_HIP(launch_quantize_q8k(x, nullptr, 0.0f, n, PRO_QUANT_EVEN, static_cast<BlockQ8K*>(y), c->stream));
@@ -357,7 +406,7 @@ int mcpm_gemv_q4_K_q8_K(mcpm_ctx* c, const mcpm_tensor* w, const void* xq, float
   if (rc) return rc;
   GemvArgs a = single_region(w, out, rows, cols);
   a.xq = static_cast<const BlockQ8K*>(xq);
-  MCPM_HIP(launch_gemv(a, PRO_Q8K, EPI_STORE, c->n_cu, c->stream));
+  MCPM_HIP(op_launch(c, [&] { return launch_gemv(a, PRO_Q8K, EPI_STORE, c->n_cu, c->stream); }));
   return MCPM_OK;
 }
 
@@ -367,7 +416,7 @@ int mcpm_gemv_q6_K_q8_K(mcpm_ctx* c, const mcpm_tensor* w, const void* xq, float
   if (rc) return rc;
   GemvArgs a = single_region(w, out, rows, cols);
   a.xq = static_cast<const BlockQ8K*>(xq);
-  MCPM_HIP(launch_gemv(a, PRO_Q8K, EPI_STORE, c->n_cu, c->stream));
+  MCPM_HIP(op_launch(c, [&] { return launch_gemv(a, PRO_Q8K, EPI_STORE, c->n_cu, c->stream); }));
   return MCPM_OK;
 }
 
@@ -393,7 +442,7 @@ int mcpm_gemv_qkv_q8_K(mcpm_ctx* c, const mcpm_tensor* wq, const mcpm_tensor* wk
   a.total_rows = q_rows + 2 * kv_rows;
   a.nb = cols / QK_K;
   a.xq = static_cast<const BlockQ8K*>(xq);
-  MCPM_HIP(launch_gemv(a, PRO_Q8K, EPI_STORE, c->n_cu, c->stream));
+  MCPM_HIP(op_launch(c, [&] { return launch_gemv(a, PRO_Q8K, EPI_STORE, c->n_cu, c->stream); }));
   return MCPM_OK;
 }
 
@@ -411,7 +460,7 @@ int mcpm_gemv_gate_up_q4_K_q8_K(mcpm_ctx* c, const mcpm_tensor* wg, const mcpm_t
   a.total_rows = rows;
   a.nb = cols / QK_K;
   a.xq = static_cast<const BlockQ8K*>(xq);
-  MCPM_HIP(launch_gemv(a, PRO_Q8K, EPI_STORE, c->n_cu, c->stream));
+  MCPM_HIP(op_launch(c, [&] { return launch_gemv(a, PRO_Q8K, EPI_STORE, c->n_cu, c->stream); }));
   return MCPM_OK;
 }
 
@@ -422,7 +471,7 @@ static int gemv_f32act_q8k(mcpm_ctx* c, const mcpm_tensor* w, int type, const fl
   if (rc) return rc;
   GemvArgs a = single_region(w, out, rows, cols);
   a.x = x;
-  MCPM_HIP(launch_gemv(a, PRO_QUANT_EVEN, EPI_STORE, c->n_cu, c->stream));
+  MCPM_HIP(op_launch(c, [&] { return launch_gemv(a, PRO_QUANT_EVEN, EPI_STORE, c->n_cu, c->stream); }));
   return MCPM_OK;
 }
 

@@ -1,6 +1,7 @@
 // mcpm_host.h -- host-side objects behind the C ABI handles.
 #pragma once
 
+#include <utility>
 #include <vector>
 
 #include "mcpm_internal.h"
@@ -22,6 +23,10 @@ struct mcpm_ctx {
   int argmax_cap = 0;
   void* d_sample = nullptr;  // device sampler scratch
   size_t sample_cap = 0;
+  // per-op kernel timing (mcpm_set_op_timing): an event pair per timed launch
+  bool op_timing = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> op_events;
+  size_t op_used = 0;
 };
 
 struct mcpm_tensor {

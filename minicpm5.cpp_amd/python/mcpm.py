@@ -117,6 +117,8 @@ _SIGS = {
     "mcpm_engine_decode_sampled": (_I, [_P, _I, _F, _F, C.c_uint32]),
     "mcpm_sample_logits": (_I, [_P, _I, _F, _F, _F]),
     "mcpm_engine_set_graph": (_I, [_P, _I]),
+    "mcpm_set_op_timing": (_I, [_P, _I]),
+    "mcpm_op_time": (_I, [_P, C.POINTER(C.c_double), C.POINTER(_I64)]),
     "mcpm_engine_set_kernel_timing": (_I, [_P, _I]),
     "mcpm_engine_kernel_time": (_I, [_P, C.POINTER(C.c_double), C.POINTER(_I64)]),
     "mcpm_engine_kernel_bytes": (_I64, [_P, _I]),
@@ -293,6 +295,16 @@ class Context:
 
     def tensor(self, native: np.ndarray, ggml_type: int, cols: int, rows: int) -> Tensor:
         return Tensor(self, native, ggml_type, cols, rows)
+
+    def set_op_timing(self, enable: bool):
+        check(self.lib.mcpm_set_op_timing(self.h, 1 if enable else 0))
+
+    def op_time(self):
+        """(summed kernel ms, timed launches) since the last call."""
+        t = C.c_double()
+        n = C.c_int64()
+        check(self.lib.mcpm_op_time(self.h, C.byref(t), C.byref(n)))
+        return t.value, n.value
 
     def close(self):
         if self.h:

@@ -410,3 +410,30 @@ def test_c3_attention_golden(ctx, orc, ctxlen):
     mcpm.check(ctx.lib.mcpm_execute_attention(ctx.h, od.ptr, qr.ptr, kr.ptr, vd.ptr, up(ctx, kc).ptr,
                                               up(ctx, vc).ptr, ctxlen, ms, NH, NKV, HD))
     assert_close(ctx.download(od, np.float32, NH * HD), g[f"attn_{ctxlen}"])
+
+
+def test_op_timing_counts_gemv_kernels(ctx):
+    """mcpm_set_op_timing / mcpm_op_time: each timed GEMV launch adds one
+    event pair, the count restarts after each read, and the results of a
+    timed launch are those of an untimed one."""
+    W = _weights(20260105, 7, 512, 768, mcpm.TYPE_Q4_K)
+    x = mcpm.synth_normal(20260105, 8, 768)
+    announce("op timing")
+    t = ctx.tensor(W, mcpm.TYPE_Q4_K, 768, 512)
+    xd = up(ctx, x)
+    o0, o1 = ctx.zeros(512 * 4), ctx.zeros(512 * 4)
+    try:
+        mcpm.check(ctx.lib.mcpm_gemv_q4_K(ctx.h, t.h, xd.ptr, o0.ptr, 512, 768))
+        ctx.set_op_timing(True)
+        for _ in range(3):
+            mcpm.check(ctx.lib.mcpm_gemv_q4_K(ctx.h, t.h, xd.ptr, o1.ptr, 512, 768))
+        ms, n = ctx.op_time()
+        assert n == 3 and ms > 0.0
+        assert ctx.op_time() == (0.0, 0)
+        ctx.set_op_timing(False)
+        mcpm.check(ctx.lib.mcpm_gemv_q4_K(ctx.h, t.h, xd.ptr, o1.ptr, 512, 768))
+        assert ctx.op_time() == (0.0, 0)
+        assert_bits(ctx.download(o1, np.float32, 512), ctx.download(o0, np.float32, 512))
+    finally:
+        ctx.set_op_timing(False)
+        ctx.sync()
