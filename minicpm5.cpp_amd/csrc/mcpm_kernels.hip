@@ -144,9 +144,10 @@ hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc
 //   out_i = O_i / Z
 // A split takes ceil(nch/64) consecutive chunks (at most ATTN_CPW), keeping
 // o_c in registers, so a kv head has at most 64 splits (up to 64*ATTN_CPW
-// chunks): one chunk per work group up to 4096 positions.  Every split writes its chunks' partials; the combine over the
-// chunks runs in the consumer (the O-projection's prologue, or
-// k_attn_combine), after the kernel boundary, so no split waits for another.
+// chunks): one chunk per work group up to 4096 positions.  Every split
+// writes its chunks' partials; the combine over the chunks runs in the
+// consumer (the O-projection's prologue, or k_attn_combine), after the
+// kernel boundary, so no split waits for another.
 // Partials (AttnPart): o_c at o[(h*max_chunks + c)*head_dim + i], (m_c, z_c)
 // at mz[h*max_chunks + c].  Every load of a chunk's K and V rows is issued at
 // once, one chunk ahead, and the rows are staged through LDS.
