@@ -219,6 +219,16 @@ int mcpm_engine_generate_sampled(mcpm_engine *e, const int *prompt, int n_prompt
  * (src/chat_session.cpp:154-186) samples token by token. */
 int mcpm_engine_decode_sampled(mcpm_engine *e, int n_steps, float temperature, float top_p, uint32_t seed);
 
+/* The generate loops continuing a cached context: tokens[0..n) go at
+ * positions pos0.. and the KV rows below pos0 are kept as they are (a previous
+ * turn's), then n_gen tokens are generated as above.  For a chat driver that
+ * keeps the cache across turns and processes only each turn's new tokens; the
+ * reference re-runs forward() over the whole conversation from position 0
+ * every turn (src/chat_session.cpp:126-160). */
+int mcpm_engine_generate_greedy_at(mcpm_engine *e, const int *tokens, int n, int pos0, int n_gen, int *out_tokens);
+int mcpm_engine_generate_sampled_at(mcpm_engine *e, const int *tokens, int n, int pos0, int n_gen,
+                                    float temperature, float top_p, uint32_t seed, int *out_tokens);
+
 /* Sampler::sample (src/sampler.cpp:8-73) on host logits for a given uniform
  * draw r in [0,1): returns the token id, or a negative error code. */
 int mcpm_sample_logits(const float *logits, int n, float temperature, float top_p, float r);

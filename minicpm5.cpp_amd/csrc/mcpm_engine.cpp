@@ -640,62 +640,6 @@ int mcpm_engine_forward(mcpm_engine* e, int token, int pos, int max_seq_len, flo
   return MCPM_OK;
 }
 
-int mcpm_engine_generate_greedy(mcpm_engine* e, const int* prompt, int n_prompt, int n_gen, int* out_tokens) {
-  if (!e || !prompt || !out_tokens || n_prompt <= 0 || n_gen <= 0)
-    return fail(MCPM_ERR_ARG, "mcpm_engine_generate_greedy: bad argument");
-  if (!e->kc) return fail(MCPM_ERR_CONTEXT, "KV cache not initialised");
-  if (n_prompt + n_gen - 1 > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
-  for (int i = 0; i < n_prompt; ++i)
-    if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab) return fail(MCPM_ERR_ARG, "prompt token out of range");
-  int rc = ensure_out_tokens(e, n_gen);
-  if (!rc) rc = ensure_staging(e, n_prompt);
-  if (rc) return rc;
-  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-  // all but the last prompt token in batched passes, the last one (whose
-  // argmax is the first generated token) through the per-token graph
-  const int first = (e->use_prefill && n_prompt > 1) ? n_prompt - 1 : 0;
-  if (first) rc = mcpm_engine_prefill(e, prompt, first, 0);
-  for (int p = first; p < n_prompt && !rc; ++p) {
-    rc = queue_state(e, p, prompt[p], p, 0);
-    if (!rc) rc = run_token(e);
-  }
-  for (int i = 1; i < n_gen && !rc; ++i) rc = run_token(e);
-  if (rc) return rc;
-  e->gen_count = n_gen;
-  e->next_pos = n_prompt + n_gen - 1;
-  MCPM_HIP(hipMemcpyAsync(out_tokens, e->out_tokens, n_gen * sizeof(int), hipMemcpyDeviceToHost, e->ctx->stream));
-  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-  return MCPM_OK;
-}
-
-int mcpm_engine_decode_steps(mcpm_engine* e, int n_steps) {
-  if (!e || n_steps < 0) return fail(MCPM_ERR_ARG, "mcpm_engine_decode_steps: bad argument");
-  if (e->gen_count == 0) return fail(MCPM_ERR_ARG, "mcpm_engine_decode_steps: no generate call to continue");
-  if (e->next_pos + n_steps > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
-  if (e->gen_count + n_steps > e->out_cap) {
-    // grow the token list, keeping what is there
-    std::vector<int> keep(e->gen_count);
-    MCPM_HIP(hipMemcpyAsync(keep.data(), e->out_tokens, keep.size() * sizeof(int), hipMemcpyDeviceToHost,
-                            e->ctx->stream));
-    MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-    int rc = ensure_out_tokens(e, e->gen_count + n_steps);
-    if (rc) return rc;
-    MCPM_HIP(hipMemcpy(e->out_tokens, keep.data(), keep.size() * sizeof(int), hipMemcpyHostToDevice));
-    // the state's capacity field must follow the new array
-    StepState st;
-    MCPM_HIP(hipMemcpy(&st, e->st, sizeof(st), hipMemcpyDeviceToHost));
-    st.n_out = e->out_cap;
-    MCPM_HIP(hipMemcpy(e->st, &st, sizeof(st), hipMemcpyHostToDevice));
-  }
-  for (int i = 0; i < n_steps; ++i) {
-    const int rc = run_token(e);
-    if (rc) return rc;
-  }
-  e->gen_count += n_steps;
-  e->next_pos += n_steps;
-  return MCPM_OK;
-}
-
 // The token graph without (sampled) or with (greedy) the argmax at its end;
 // each is captured once and kept.
 static int set_sample_mode(mcpm_engine* e, bool on) {
@@ -726,43 +670,98 @@ static int sample_step(mcpm_engine* e, float temperature, float top_p, float r) 
 
 static bool bad_sampling(float temperature, float top_p) { return !(temperature == temperature) || !(top_p == top_p); }
 
-int mcpm_engine_generate_sampled(mcpm_engine* e, const int* prompt, int n_prompt, int n_gen, float temperature,
-                                 float top_p, uint32_t seed, int* out_tokens) {
-  if (!e || !prompt || !out_tokens || n_prompt <= 0 || n_gen <= 0 || bad_sampling(temperature, top_p))
-    return fail(MCPM_ERR_ARG, "mcpm_engine_generate_sampled: bad argument");
+// Tokens at positions pos0 .. pos0+n-1 (the KV rows below pos0 are kept as
+// they are), then n_gen tokens: all given tokens but the last in batched
+// passes, the last one (whose argmax or draw is the first generated token)
+// through the per-token graph.  sampled: Sampler::sample on the device after
+// each token with the draws of std::uniform_real_distribution<float> over
+// std::mt19937(seed), one per generated token (src/sampler.cpp:5-6, seeded by
+// the caller); else the greedy argmax.
+static int generate_at(mcpm_engine* e, const int* toks, int n, int pos0, int n_gen, bool sampled, float temperature,
+                       float top_p, uint32_t seed, int* out_tokens, const char* fn) {
+  if (!e || !toks || !out_tokens || n <= 0 || n_gen <= 0 || pos0 < 0 ||
+      (sampled && bad_sampling(temperature, top_p)))
+    return fail(MCPM_ERR_ARG, std::string(fn) + ": bad argument");
   if (!e->kc) return fail(MCPM_ERR_CONTEXT, "KV cache not initialised");
-  if (n_prompt + n_gen - 1 > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
-  for (int i = 0; i < n_prompt; ++i)
-    if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab) return fail(MCPM_ERR_ARG, "prompt token out of range");
+  if (static_cast<int64_t>(pos0) + n + n_gen - 1 > e->max_seq)
+    return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
+  for (int i = 0; i < n; ++i)
+    if (toks[i] < 0 || toks[i] >= e->cfg.vocab) return fail(MCPM_ERR_ARG, "prompt token out of range");
   int rc = ensure_out_tokens(e, n_gen);
-  if (!rc) rc = ensure_staging(e, n_prompt);
-  if (!rc) rc = ensure_sampler(e);
-  if (!rc) rc = set_sample_mode(e, true);
+  if (!rc) rc = ensure_staging(e, n);
+  if (!rc && sampled) rc = ensure_sampler(e);
+  if (!rc) rc = set_sample_mode(e, sampled);
   if (rc) return rc;
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-  // the draws of std::uniform_real_distribution<float> over std::mt19937(seed),
-  // one per generated token (src/sampler.cpp:5-6, seeded by the caller)
   std::mt19937 rng(seed);
   std::uniform_real_distribution<float> dist(0.0f, 1.0f);
-  const int first = (e->use_prefill && n_prompt > 1) ? n_prompt - 1 : 0;
-  if (first) rc = mcpm_engine_prefill(e, prompt, first, 0);
-  for (int p = first; p < n_prompt && !rc; ++p) {
-    rc = queue_state(e, p, prompt[p], p, 0);
+  const int first = (e->use_prefill && n > 1) ? n - 1 : 0;
+  if (first) rc = mcpm_engine_prefill(e, toks, first, pos0);
+  for (int i = first; i < n && !rc; ++i) {
+    rc = queue_state(e, i, toks[i], pos0 + i, 0);
     if (!rc) rc = run_token(e);
   }
-  if (!rc) rc = sample_step(e, temperature, top_p, dist(rng));
+  if (!rc && sampled) rc = sample_step(e, temperature, top_p, dist(rng));
   for (int i = 1; i < n_gen && !rc; ++i) {
     rc = run_token(e);
-    if (!rc) rc = sample_step(e, temperature, top_p, dist(rng));
+    if (!rc && sampled) rc = sample_step(e, temperature, top_p, dist(rng));
   }
   const int rc2 = set_sample_mode(e, false);
   if (rc) return rc;
   if (rc2) return rc2;
   e->gen_count = n_gen;
-  e->next_pos = n_prompt + n_gen - 1;
+  e->next_pos = pos0 + n + n_gen - 1;
   MCPM_HIP(hipMemcpyAsync(out_tokens, e->out_tokens, n_gen * sizeof(int), hipMemcpyDeviceToHost, e->ctx->stream));
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
   return MCPM_OK;
+}
+
+int mcpm_engine_generate_greedy(mcpm_engine* e, const int* prompt, int n_prompt, int n_gen, int* out_tokens) {
+  return generate_at(e, prompt, n_prompt, 0, n_gen, false, 0.0f, 0.0f, 0u, out_tokens, "mcpm_engine_generate_greedy");
+}
+
+int mcpm_engine_generate_greedy_at(mcpm_engine* e, const int* tokens, int n, int pos0, int n_gen, int* out_tokens) {
+  return generate_at(e, tokens, n, pos0, n_gen, false, 0.0f, 0.0f, 0u, out_tokens, "mcpm_engine_generate_greedy_at");
+}
+
+int mcpm_engine_decode_steps(mcpm_engine* e, int n_steps) {
+  if (!e || n_steps < 0) return fail(MCPM_ERR_ARG, "mcpm_engine_decode_steps: bad argument");
+  if (e->gen_count == 0) return fail(MCPM_ERR_ARG, "mcpm_engine_decode_steps: no generate call to continue");
+  if (e->next_pos + n_steps > e->max_seq) return fail(MCPM_ERR_CONTEXT, "Maximum context exceeded (pos >= max_seq_len).");
+  if (e->gen_count + n_steps > e->out_cap) {
+    // grow the token list, keeping what is there
+    std::vector<int> keep(e->gen_count);
+    MCPM_HIP(hipMemcpyAsync(keep.data(), e->out_tokens, keep.size() * sizeof(int), hipMemcpyDeviceToHost,
+                            e->ctx->stream));
+    MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+    int rc = ensure_out_tokens(e, e->gen_count + n_steps);
+    if (rc) return rc;
+    MCPM_HIP(hipMemcpy(e->out_tokens, keep.data(), keep.size() * sizeof(int), hipMemcpyHostToDevice));
+    // the state's capacity field must follow the new array
+    StepState st;
+    MCPM_HIP(hipMemcpy(&st, e->st, sizeof(st), hipMemcpyDeviceToHost));
+    st.n_out = e->out_cap;
+    MCPM_HIP(hipMemcpy(e->st, &st, sizeof(st), hipMemcpyHostToDevice));
+  }
+  for (int i = 0; i < n_steps; ++i) {
+    const int rc = run_token(e);
+    if (rc) return rc;
+  }
+  e->gen_count += n_steps;
+  e->next_pos += n_steps;
+  return MCPM_OK;
+}
+
+int mcpm_engine_generate_sampled(mcpm_engine* e, const int* prompt, int n_prompt, int n_gen, float temperature,
+                                 float top_p, uint32_t seed, int* out_tokens) {
+  return generate_at(e, prompt, n_prompt, 0, n_gen, true, temperature, top_p, seed, out_tokens,
+                     "mcpm_engine_generate_sampled");
+}
+
+int mcpm_engine_generate_sampled_at(mcpm_engine* e, const int* tokens, int n, int pos0, int n_gen, float temperature,
+                                    float top_p, uint32_t seed, int* out_tokens) {
+  return generate_at(e, tokens, n, pos0, n_gen, true, temperature, top_p, seed, out_tokens,
+                     "mcpm_engine_generate_sampled_at");
 }
 
 int mcpm_engine_decode_sampled(mcpm_engine* e, int n_steps, float temperature, float top_p, uint32_t seed) {

@@ -5,11 +5,16 @@
 // (no logits copy per token); --prefill sends all prompt tokens but the last
 // through the batched prefill before the per-token loop; --sample T,P,SEED
 // samples each token on the GPU (temperature T, top-p P, mt19937 seeded with
-// SEED) in the device loop.
+// SEED) in the device loop.  --turns N1,N2,... runs a multi-turn exchange
+// through KVSession (host/kv_session.h): turn 0 sends the prompt, turn i
+// appends the previous response and Ni new random ids, and each turn
+// generates --tokens tokens, keeping the KV rows of the conversation so far;
+// --no-reuse forgets them before every turn (the reference's behaviour, the
+// same tokens).
 //
 //   mcpm_decode (--gguf FILE | --synth SEED [--layers N] [--vocab N])
 //               [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--prefill]
-//               [--sample T,P,SEED] [--verbose]
+//               [--sample T,P,SEED] [--turns N1,N2,... [--no-reuse]] [--verbose]
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -18,20 +23,22 @@
 #include <string>
 #include <vector>
 
+#include "kv_session.h"
 #include "model.h"
 
 static void usage() {
     std::fprintf(stderr,
                  "usage: mcpm_decode (--gguf FILE | --synth SEED [--layers N] [--vocab N])\n"
                  "                   [--prompt N | --prompt-ids ID,ID,...] [--tokens N] [--device-loop] [--prefill]\n"
-                 "                   [--sample T,P,SEED] [--verbose]\n");
+                 "                   [--sample T,P,SEED] [--turns N1,N2,... [--no-reuse]] [--verbose]\n");
 }
 
 int main(int argc, char** argv) {
     std::string gguf;
     long long synth_seed = -1;
     int layers = 40, vocab = 130560, n_prompt = 32, n_tokens = 64;
-    bool device_loop = false, verbose = false, use_prefill = false, sample = false;
+    bool device_loop = false, verbose = false, use_prefill = false, sample = false, reuse = true;
+    std::vector<int> turns;
     float temperature = 1.0f, top_p = 1.0f;
     unsigned sample_seed = 0;
     std::vector<int> prompt_ids;
@@ -71,6 +78,19 @@ int main(int argc, char** argv) {
             }
             sample = device_loop = true;
         }
+        else if (a == "--turns") {
+            for (const char* p = next(); *p;) {
+                char* end = nullptr;
+                const long v = std::strtol(p, &end, 10);
+                if (end == p || v < 1) {
+                    usage();
+                    return 2;
+                }
+                turns.push_back(static_cast<int>(v));
+                p = (*end == ',') ? end + 1 : end;
+            }
+        }
+        else if (a == "--no-reuse") reuse = false;
         else if (a == "--verbose") verbose = true;
         else {
             usage();
@@ -104,7 +124,8 @@ int main(int argc, char** argv) {
     }
     if (!ok) return 1;
     const mcpm_model_config& cfg = engine.config();
-    const int max_seq = n_prompt + n_tokens;
+    int max_seq = n_prompt + n_tokens;
+    for (int t : turns) max_seq += t + n_tokens;
     engine.init_kv_cache(max_seq);
 
     std::vector<int> prompt = prompt_ids;
@@ -119,6 +140,33 @@ int main(int argc, char** argv) {
             std::fprintf(stderr, "prompt id %d outside [0, %d)\n", t, cfg.vocab);
             return 2;
         }
+    }
+
+    if (!turns.empty()) {
+        // turn 0: the prompt; turn i: the previous response and turns[i-1] new ids
+        KVSession session(engine, max_seq);
+        SessionSampling sp;
+        sp.greedy = !sample;
+        sp.temperature = temperature;
+        sp.top_p = top_p;
+        sp.seed = sample_seed;
+        std::mt19937 gen(4321);
+        std::uniform_int_distribution<int> pick(0, cfg.vocab - 1);
+        std::vector<int> conversation = prompt;
+        for (size_t t = 0; t <= turns.size(); ++t) {
+            if (t > 0)
+                for (int k = 0; k < turns[t - 1]; ++k) conversation.push_back(pick(gen));
+            if (!reuse) session.clear();
+            const auto ts = std::chrono::steady_clock::now();
+            const std::vector<int> resp = session.generate_response(conversation, n_tokens, {}, sp);
+            const double ms = std::chrono::duration<double>(std::chrono::steady_clock::now() - ts).count() * 1e3;
+            std::printf("turn %zu: conversation %zu, reused %d, processed %d, %.1f ms, tokens:", t,
+                        conversation.size(), session.reused_tokens(), session.processed_tokens(), ms);
+            for (int tok : resp) std::printf(" %d", tok);
+            std::printf("\n");
+            conversation.insert(conversation.end(), resp.begin(), resp.end());
+        }
+        return 0;
     }
 
     std::vector<int> out;

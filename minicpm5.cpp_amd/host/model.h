@@ -31,6 +31,11 @@ public:
     // after each token: temperature, top-p, draws from std::mt19937(seed).
     std::vector<int> generate_sampled(const std::vector<int>& prompt, int n_gen, float temperature, float top_p,
                                       uint32_t seed);
+    // The same two loops continuing a cached context: tokens go at positions
+    // pos0.., the KV rows below pos0 are kept (a previous turn's).
+    std::vector<int> generate_greedy_at(const std::vector<int>& tokens, int pos0, int n_gen);
+    std::vector<int> generate_sampled_at(const std::vector<int>& tokens, int pos0, int n_gen, float temperature,
+                                         float top_p, uint32_t seed);
     // Fills the KV cache for tokens at positions pos0.. in batched passes
     // (MFMA GEMMs), exactly as forward() per token would, without logits.  A
     // chat driver keeps the cache across turns and prefills only the new

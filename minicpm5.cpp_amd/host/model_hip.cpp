@@ -97,3 +97,22 @@ std::vector<int> MiniCPM5Engine::generate_greedy(const std::vector<int>& prompt,
           "mcpm_engine_generate_greedy");
     return out;
 }
+
+std::vector<int> MiniCPM5Engine::generate_greedy_at(const std::vector<int>& tokens, int pos0, int n_gen) {
+    if (!engine_) throw std::runtime_error("generate_greedy_at: no model loaded");
+    std::vector<int> out(static_cast<size_t>(n_gen > 0 ? n_gen : 0));
+    check(mcpm_engine_generate_greedy_at(engine_, tokens.data(), static_cast<int>(tokens.size()), pos0, n_gen,
+                                         out.data()),
+          "mcpm_engine_generate_greedy_at");
+    return out;
+}
+
+std::vector<int> MiniCPM5Engine::generate_sampled_at(const std::vector<int>& tokens, int pos0, int n_gen,
+                                                     float temperature, float top_p, uint32_t seed) {
+    if (!engine_) throw std::runtime_error("generate_sampled_at: no model loaded");
+    std::vector<int> out(static_cast<size_t>(n_gen > 0 ? n_gen : 0));
+    check(mcpm_engine_generate_sampled_at(engine_, tokens.data(), static_cast<int>(tokens.size()), pos0, n_gen,
+                                          temperature, top_p, seed, out.data()),
+          "mcpm_engine_generate_sampled_at");
+    return out;
+}

@@ -115,6 +115,8 @@ _SIGS = {
     "mcpm_engine_tokens": (_I, [_P, _P, _I]),
     "mcpm_engine_generate_sampled": (_I, [_P, _P, _I, _I, _F, _F, C.c_uint32, _P]),
     "mcpm_engine_decode_sampled": (_I, [_P, _I, _F, _F, C.c_uint32]),
+    "mcpm_engine_generate_greedy_at": (_I, [_P, _P, _I, _I, _I, _P]),
+    "mcpm_engine_generate_sampled_at": (_I, [_P, _P, _I, _I, _I, _F, _F, C.c_uint32, _P]),
     "mcpm_sample_logits": (_I, [_P, _I, _F, _F, _F]),
     "mcpm_engine_set_graph": (_I, [_P, _I]),
     "mcpm_set_op_timing": (_I, [_P, _I]),
@@ -356,6 +358,21 @@ class Engine:
 
     def sync(self):
         self.ctx.sync()
+
+    def generate_greedy_at(self, tokens, pos0: int, n_gen: int) -> np.ndarray:
+        """tokens at positions pos0.. after the cached rows below pos0, then n_gen greedy tokens."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(n_gen, np.int32)
+        check(self.lib.mcpm_engine_generate_greedy_at(self.h, ptr(tokens), tokens.size, pos0, n_gen, ptr(out)))
+        return out
+
+    def generate_sampled_at(self, tokens, pos0: int, n_gen: int, temperature: float, top_p: float,
+                            seed: int) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(n_gen, np.int32)
+        check(self.lib.mcpm_engine_generate_sampled_at(self.h, ptr(tokens), tokens.size, pos0, n_gen, temperature,
+                                                       top_p, seed, ptr(out)))
+        return out
 
     def generate_sampled(self, prompt, n_gen: int, temperature: float, top_p: float, seed: int) -> np.ndarray:
         prompt = np.ascontiguousarray(prompt, np.int32)

@@ -185,18 +185,20 @@ def test_reference_geometry_tokens(ctx, name):
     e.free()
 
 
-def test_long_context_greedy_matches_oracle(ctx):
-    """A 1100-token prompt (18 attention chunks per head) and 8 greedy tokens
-    on a model whose O projection combines the attention partials in its
-    prologue (q dim 1024: 4 blocks): every chunk batch of the combine runs,
-    against the oracle."""
+@pytest.mark.parametrize("n_prompt", [1100, 2200])
+def test_long_context_greedy_matches_oracle(ctx, n_prompt):
+    """Prompts of 1100 and 2200 tokens (18 and 35 attention chunks per head)
+    and 8 greedy tokens on a model whose O projection combines the attention
+    partials in its prologue (q dim 1024: 4 blocks), against the oracle: the
+    combine's preloaded chunks, its first batch, and (2200) its later batches
+    of partials and maxima."""
     cfg = mcpm.make_config(2, 1024, 16, 4, 64, 2048, 1000)
     img = mcpm.synth_gguf(cfg, seed=404, mix=0)
-    prompt = [int(t) for t in np.random.default_rng(17).integers(0, 1000, 1100)]
-    announce("long context greedy vs oracle (1100-token prompt)")
+    prompt = [int(t) for t in np.random.default_rng(17).integers(0, 1000, n_prompt)]
+    announce(f"long context greedy vs oracle ({n_prompt}-token prompt)")
     eng = mcpm.Engine(ctx, image=img)
     try:
-        eng.init_kv_cache(1120)
+        eng.init_kv_cache(n_prompt + 20)
         got = list(eng.generate_greedy(prompt, 8))
     finally:
         eng.free()
@@ -204,3 +206,44 @@ def test_long_context_greedy_matches_oracle(ctx):
     want = list(om.generate_greedy(prompt, 8))
     om.close()
     assert got == want
+
+
+@pytest.mark.parametrize("prefill", [True, False])
+def test_generate_at_reuses_cached_rows(ctx, prefill):
+    """mcpm_engine_generate_{greedy,sampled}_at: a second turn that keeps the
+    first turn's KV rows (conversation + response but its last token) and
+    runs only its new tokens, or keeps a shorter prefix, generates the tokens
+    of the whole conversation run from position 0 and leaves bit-identical
+    KV rows."""
+    cfg = mcpm.make_config(2, 512, 8, 2, 64, 1400, 2000)
+    img = mcpm.synth_gguf(cfg, seed=606, mix=0)
+    rng = np.random.default_rng(9)
+    turn1 = [int(t) for t in rng.integers(0, 2000, 70)]
+    user2 = [int(t) for t in rng.integers(0, 2000, 90)]
+    announce(f"generate_at reuse (prefill={prefill})")
+    eng = mcpm.Engine(ctx, image=img)
+    try:
+        eng.set_prefill(prefill)
+        cap = 400
+        eng.init_kv_cache(cap)
+        resp1 = list(eng.generate_greedy(turn1, 12))
+        conv2 = turn1 + resp1 + user2
+        n2 = len(conv2)
+        keep = len(turn1) + len(resp1) - 1
+        got = list(eng.generate_greedy_at(conv2[keep:], keep, 10))
+        kv_got = [eng.read_kv(l, 0, n2 + 9) for l in range(cfg.n_layers)]
+        # a shorter kept prefix (an edited turn): positions 30.. rerun
+        got_short = list(eng.generate_greedy_at(conv2[30:], 30, 10))
+        sampled = list(eng.generate_sampled_at(conv2[keep:], keep, 10, 0.9, 0.9, 77))
+        eng.init_kv_cache(cap)
+        want = list(eng.generate_greedy(conv2, 10))
+        kv_want = [eng.read_kv(l, 0, n2 + 9) for l in range(cfg.n_layers)]
+        want_sampled = list(eng.generate_sampled(conv2, 10, 0.9, 0.9, 77))
+        with pytest.raises(mcpm.McpmError):
+            eng.generate_greedy_at(conv2, cap - len(conv2) + 1, 2)  # past the cache
+    finally:
+        eng.free()
+    assert got == want and got_short == want and sampled == want_sampled
+    for (kg, vg), (kw, vw) in zip(kv_got, kv_want):
+        assert_bits(kg, kw)
+        assert_bits(vg, vw)

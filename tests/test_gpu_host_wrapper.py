@@ -170,3 +170,44 @@ def test_engine_mirror_sampled_matches_oracle():
         want.append(orc.or_sample_blocked(P(lg), 4096, T, top_p, orc.or_mt_uniform01(P(gen))))
     om.close()
     assert got == want
+
+
+@pytest.mark.gpu
+def test_session_turns_reuse_cache_and_match_oracle():
+    """mcpm_decode --turns: KVSession keeps the KV rows of the conversation
+    between turns and runs only each turn's new tokens; every turn's tokens
+    equal those of the same conversation run from position 0 (--no-reuse,
+    the reference's way) and the oracle's greedy continuation."""
+    import oracle as O
+    cfg = mcpm.make_config(2, 2304, 32, 8, 64, 5760, 4096)
+    seed, prompt, n_gen = 7, [5, 1000, 77, 4095, 12], 6
+    announce("mcpm_decode --turns")
+    base = [DECODE, "--synth", str(seed), "--layers", "2", "--vocab", "4096",
+            "--prompt-ids", ",".join(map(str, prompt)), "--tokens", str(n_gen), "--turns", "3,40"]
+    runs = {}
+    for reuse in (True, False):
+        r = subprocess.run(base + ([] if reuse else ["--no-reuse"]), capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0, r.stderr
+        runs[reuse] = [l for l in r.stdout.splitlines() if l.startswith("turn ")]
+    assert len(runs[True]) == 3
+
+    def parse(line):
+        head, toks = line.split("tokens:")
+        f = dict(kv.strip().split(" ", 1) for kv in head.split(":", 1)[1].split(",")[:3])
+        return int(f["conversation"]), int(f["reused"]), int(f["processed"]), [int(t) for t in toks.split()]
+
+    turns = [parse(l) for l in runs[True]]
+    fresh = [parse(l) for l in runs[False]]
+    prev = None  # (conversation length, response) of the previous turn
+    for (n, reused, processed, toks), (n2, reused2, _, toks2) in zip(turns, fresh):
+        assert toks == toks2 and n == n2 and reused2 == 0
+        # the previous turn's conversation and response but its last token
+        # (never fed back) are cached
+        assert reused == (0 if prev is None else prev[0] + len(prev[1]) - 1)
+        assert processed == n - reused
+        prev = (n, toks)
+    # turn 0 against the oracle; the later turns' new ids come from the
+    # program's generator, and the run from position 0 checks them
+    om = O.OracleModel(mcpm.synth_gguf(cfg, seed=seed, mix=0))
+    assert list(om.generate_greedy(prompt, n_gen)) == turns[0][3]
+    om.close()
