@@ -206,21 +206,63 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   const h2 off1026{static_cast<_Float16>(1026.0f), static_cast<_Float16>(1026.0f)};
   const f32x4 zero4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // The weight bytes a block's A operands and row scales are built from,
+  // loaded one block ahead like the activations (loaded in their own block,
+  // they would hold every block's MFMAs for a full memory round trip).
+  // Q4_K: hdr = the A row's d/dmin/scales, q[0..1] = its chunk planes 2g and
+  // 2g+1; Q6_K: hdr = its scales, q[0..3] = ql planes 4h.., q[4..5] = qh
+  // planes 2h..; dr[i] = d (and Q4_K's dmin) of D row 4g+i.
+  struct WRaw {
+    u32x4 hdr;
+    u32x4 q[WT == 0 ? 2 : 6];
+    uint32_t dr[4];
+  };
+  auto load_w = [&](WRaw& w, int b) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const size_t r = static_cast<size_t>(min(r0 + 4 * g + i, a.rows - 1));
+      if constexpr (WT == 0)
+        w.dr[i] = *reinterpret_cast<const uint32_t*>(a.w.p1 + (static_cast<size_t>(b) * rows + r) * 16);
+      else
+        w.dr[i] = *reinterpret_cast<const uint16_t*>(a.w.p3 + (static_cast<size_t>(b) * rows + r) * 2);
+    }
+    if constexpr (WT == 0) {
+      w.hdr = *reinterpret_cast<const u32x4*>(a.w.p1 + (static_cast<size_t>(b) * rows + ra) * 16);
+      const uint8_t* q = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
+      w.q[0] = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g) * rows * 16);
+      w.q[1] = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g + 1) * rows * 16);
+    } else {
+      const int h = g >> 1;
+      w.hdr = *reinterpret_cast<const u32x4*>(a.w.p2 + (static_cast<size_t>(b) * rows + ra) * 16);
+      const uint8_t* ql = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
+      const uint8_t* qh = a.w.p1 + (static_cast<size_t>(b) * 4 * rows + ra) * 16;
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) w.q[cc] = *reinterpret_cast<const u32x4*>(ql + static_cast<size_t>(4 * h + cc) * rows * 16);
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+        w.q[4 + cc] = *reinterpret_cast<const u32x4*>(qh + static_cast<size_t>(2 * h + cc) * rows * 16);
+    }
+  };
+  WRaw wc;
+  load_w(wc, 0);
+  WRaw wn = wc;
+
   for (int b = 0; b < a.nb; ++b) {
     const int buf = b & 1;
-    if (b + 1 < a.nb) fetch(b + 1);  // in flight during this block's MFMAs
+    if (b + 1 < a.nb) {  // in flight during this block's MFMAs
+      fetch(b + 1);
+      load_w(wn, b + 1);
+    }
     if (live) {
     // d (and dmin) of the four D rows of this lane
     float dw[4], dmw[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const size_t r = static_cast<size_t>(min(r0 + 4 * g + i, a.rows - 1));
       if constexpr (WT == 0) {
-        const uint32_t hd = *reinterpret_cast<const uint32_t*>(a.w.p1 + (static_cast<size_t>(b) * rows + r) * 16);
-        dw[i] = fp16_to_fp32(static_cast<uint16_t>(hd & 0xffffu));
-        dmw[i] = fp16_to_fp32(static_cast<uint16_t>(hd >> 16));
+        dw[i] = fp16_to_fp32(static_cast<uint16_t>(wc.dr[i] & 0xffffu));
+        dmw[i] = fp16_to_fp32(static_cast<uint16_t>(wc.dr[i] >> 16));
       } else {
-        dw[i] = fp16_to_fp32(*reinterpret_cast<const uint16_t*>(a.w.p3 + (static_cast<size_t>(b) * rows + r) * 2));
+        dw[i] = fp16_to_fp32(static_cast<uint16_t>(wc.dr[i]));
         dmw[i] = 0.0f;
       }
     }
@@ -229,8 +271,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
     uint32_t acw[8];  // Q6_K: the offset operand's one nonzero dword per lane group
     h2 sc[4];         // Q6_K: scales 4g .. 4g+3 of this lane's row, as fp16 pairs
     if constexpr (WT == 0) {
-      const u32x4 hdr = *reinterpret_cast<const u32x4*>(a.w.p1 + (static_cast<size_t>(b) * rows + ra) * 16);
-      const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+      const uint32_t s0 = wc.hdr.y, s1 = wc.hdr.z, s2 = wc.hdr.w;
       const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
       const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
       const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
@@ -239,9 +280,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       const int sh = 16 * (g & 1);
       const h2 sa = splat_h(static_cast<int>((sw >> sh) & 0xffu));        // sc[2g]
       const h2 sb = splat_h(static_cast<int>((sw >> (sh + 8)) & 0xffu));  // sc[2g+1]
-      const uint8_t* q = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
-      const u32x4 q0 = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g) * rows * 16);
-      const u32x4 q1 = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g + 1) * rows * 16);
+      const u32x4 q0 = wc.q[0], q1 = wc.q[1];
       const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
       for (int m = 0; m < 8; ++m)
@@ -252,8 +291,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
                      h2bits(byte_pair_h(mw, 0x04020402u, off1024)), h2bits(byte_pair_h(mw, 0x04030403u, off1024))};
       AM = g < 2 ? __builtin_bit_cast(h8, mr) : h8{};
     } else {
-      const int h = g >> 1, nib = 4 * (g & 1);
-      const u32x4 scr = *reinterpret_cast<const u32x4*>(a.w.p2 + (static_cast<size_t>(b) * rows + ra) * 16);
+      const int nib = 4 * (g & 1);
+      const u32x4 scr = wc.hdr;
       // scales 4g .. 4g+3 (signed bytes) = dword g of the 16 scales
       const uint32_t scw = g == 0 ? scr.x : g == 1 ? scr.y : g == 2 ? scr.z : scr.w;
       // the offset operand: K entries 0, 1 (lanes 0..15, halves 0, 1) are
@@ -269,12 +308,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k) sc[k] = splat_h(__builtin_amdgcn_sbfe(static_cast<int>(scw), 8 * k, 8));
-      const uint8_t* ql = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
-      const uint8_t* qh = a.w.p1 + (static_cast<size_t>(b) * 4 * rows + ra) * 16;
       uint32_t lw[16], hw[8];
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(ql + static_cast<size_t>(4 * h + cc) * rows * 16);
+        const u32x4 v = wc.q[cc];
         lw[4 * cc] = v.x;
         lw[4 * cc + 1] = v.y;
         lw[4 * cc + 2] = v.z;
@@ -282,7 +319,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       }
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(qh + static_cast<size_t>(2 * h + cc) * rows * 16);
+        const u32x4 v = wc.q[4 + cc];
         hw[4 * cc] = v.x;
         hw[4 * cc + 1] = v.y;
         hw[4 * cc + 2] = v.z;
@@ -349,6 +386,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
     // block b+1 into the other buffer, whose last readers passed the previous barrier
     if (b + 1 < a.nb) stash(buf ^ 1);
     __syncthreads();
+    wc = wn;
   }
 
 #pragma unroll
