@@ -93,10 +93,11 @@ constexpr int CHAIN_BATCH = 12;  // TILE chain: blocks whose LDS entries are rea
 // PRO_ATTN_EVEN: thread t < 32*nb combines the ATTN_VALS values t*8 .. t*8+7
 // (one head: head_dim % 8 == 0, nb <= 8) over the chunks.  The o_c of the
 // first ATTN_RB chunks and the (m_c, z_c) of the first ATTN_MZ are loaded with
-// the activations, before the weights; the next ATTN_BATCH chunks' loads (and
-// their maxima's) are issued together once the weights are queued, so a
-// context of up to ATTN_RB + ATTN_BATCH chunks costs one round trip after them.
-constexpr int ATTN_VALS = 8, ATTN_RB = 8, ATTN_MZ = 16, ATTN_BATCH = 16, ATTN_MAX_NB = 8;
+// the activations, before the weights; further chunks' partials (and their
+// maxima) follow in batches of ATTN_BATCH, a batch's loads issued together.
+// Larger batches or preloads cost more than they save: their registers push
+// the kernel past 256 VGPRs into AGPR copies, which slows short contexts.
+constexpr int ATTN_VALS = 8, ATTN_RB = 4, ATTN_MZ = 8, ATTN_BATCH = 8, ATTN_MAX_NB = 8;
 
 struct ProRegs {
   f32x4 x[NR][4];  // fp32 activations of the lane's 16 values
