@@ -40,7 +40,7 @@ struct TimedPair {
 struct PrefillBufs {
   int cap = 0, max_chunks = 0;
   int* tokens = nullptr;
-  float *x = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *g = nullptr, *u = nullptr, *part = nullptr;
+  float *x = nullptr, *qkv = nullptr, *q = nullptr, *g = nullptr, *u = nullptr, *part = nullptr;
   _Float16 *xh = nullptr, *xbs = nullptr;
   float* xd = nullptr;
 };
@@ -115,7 +115,7 @@ void drop_graph(mcpm_engine* e) {
 
 void free_prefill(PrefillBufs& b) {
   for (void* p : {static_cast<void*>(b.tokens), static_cast<void*>(b.x), static_cast<void*>(b.qkv),
-                  static_cast<void*>(b.q), static_cast<void*>(b.att), static_cast<void*>(b.g),
+                  static_cast<void*>(b.q), static_cast<void*>(b.g),
                   static_cast<void*>(b.u), static_cast<void*>(b.part), static_cast<void*>(b.xh),
                   static_cast<void*>(b.xbs), static_cast<void*>(b.xd)})
     if (p) (void)hipFree(p);
@@ -453,7 +453,6 @@ int ensure_prefill(mcpm_engine* e, int cap) {
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.x), n * c.dim * 4);
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.qkv), n * (qd + 2 * kvd) * 4);
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.q), n * qd * 4);
-  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.att), n * qd * 4);
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.g), n * c.ffn * 4);
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.u), n * c.ffn * 4);
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.part), n * c.n_heads * e->max_chunks * (c.head_dim + 2) * 4);
@@ -496,8 +495,7 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
     if (l == c.n_layers - 1) break;  // nothing after the last K/V rows reaches the cache
     MCPM_HIP(launch_attention_batch(b.q, kc, vc, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part, tok_o,
                                     tok_mz, pos0, n, s));
-    MCPM_HIP(launch_attn_combine_batch(part, tok_o, tok_mz, pos0, n, c.n_heads, c.head_dim, e->max_chunks, b.att, s));
-    MCPM_HIP(launch_quant_batch(b.att, nullptr, qd, nullptr, 0.0f, qd, qd, PRO_QUANT_EVEN, n, qb, s));
+    MCPM_HIP(launch_quant_batch_attn(part, tok_o, tok_mz, pos0, n, c.n_heads, c.head_dim, e->max_chunks, qb, s));
     MCPM_HIP(launch_gemm_q8k(view_of(L.wo), c.dim, qd / QK_K, n, qb, b.x, c.dim, true, s));
     MCPM_HIP(launch_quant_batch(b.x, nullptr, c.dim, L.ffn_norm, c.eps, c.dim, c.dim, PRO_NORM_AWAY, n, qb, s));
     MCPM_HIP(launch_gemm_q8k(view_of(L.wg), c.ffn, nbd, n, qb, b.g, c.ffn, false, s));

@@ -283,8 +283,10 @@ hipError_t launch_rope_kv_batch(const float* qkv, int n_tok, int qd, int kvd, in
 hipError_t launch_attention_batch(const float* q, const float* kc, const float* vc, int n_heads, int n_kv_heads,
                                   int head_dim, int max_chunks, const AttnPart& part, size_t tok_o, size_t tok_mz,
                                   int pos0, int n_tok, hipStream_t s);
-hipError_t launch_attn_combine_batch(const AttnPart& part, size_t tok_stride_o, size_t tok_stride_mz, int pos0,
-                                     int n_tok, int n_heads, int head_dim, int max_chunks, float* out, hipStream_t s);
+// The attention output of each token from its chunk partials, quantized
+// ties-even into q (the O projection's input), in one pass.
+hipError_t launch_quant_batch_attn(const AttnPart& part, size_t tok_stride_o, size_t tok_stride_mz, int pos0,
+                                   int n_tok, int n_heads, int head_dim, int max_chunks, QuantBatch q, hipStream_t s);
 hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s);
 hipError_t launch_dequant_rows(const WView& w, int row0, int n_rows, int cols, float* out, hipStream_t s);
 hipError_t launch_gemv_f32(const float* w, const float* x, float* out, int rows, int cols, hipStream_t s);

@@ -434,27 +434,56 @@ __global__ void k_rope_kv_batch(const float* __restrict__ qkv, int qd, int kvd, 
   }
 }
 
-// ------------------------------------------------------- attention combine --
-// k_attn_combine for token t (position pos0 + t) with per-token partials.
-__global__ void k_attn_combine_batch(const float* __restrict__ part_o, const float2* __restrict__ part_mz,
-                                     size_t tok_stride_o, size_t tok_stride_mz, int pos0, int n_out, int hd,
-                                     int max_chunks, float* __restrict__ out) {
-  const int t = blockIdx.y;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n_out) return;
+// ------------------------------------------------- attention combine + Q8_K --
+// Per token t (one work group, position pos0 + t): the attention output from
+// the per-token chunk partials -- k_attn_combine's arithmetic for each value:
+// m = max m_c, then over the chunks in order f_c = exp(m_c - m),
+// Z = fma(z_c, f_c, Z), O = fma(o_c, f_c, O), value O / Z -- then the O
+// projection's ties-even Q8_K quantization of it (k_quant_batch's), with no
+// fp32 copy of the output in between.  A lane takes 4 consecutive values of
+// one head (head_dim % 4 == 0), which share m and Z.
+__global__ void __launch_bounds__(256) k_quant_batch_attn(const float* __restrict__ part_o,
+                                                          const float2* __restrict__ part_mz, size_t tok_stride_o,
+                                                          size_t tok_stride_mz, int pos0, int dim, int hd,
+                                                          int max_chunks, _Float16* __restrict__ xh,
+                                                          float* __restrict__ xd, _Float16* __restrict__ xbs) {
+  const int t = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nch = (pos0 + t) / ATTN_CHUNK + 1;
-  const int h = i / hd, d = i - h * hd;
-  const float2* mz = part_mz + t * tok_stride_mz + static_cast<size_t>(h) * max_chunks;
-  const float* o = part_o + t * tok_stride_o + static_cast<size_t>(h) * max_chunks * hd + d;
-  float m = mz[0].x;
-  for (int c = 1; c < nch; ++c) m = fmaxf(m, mz[c].x);
-  float Z = 0.0f, O = 0.0f;
-  for (int c = 0; c < nch; ++c) {
-    const float f = exp_f32(mz[c].x - m);
-    Z = __builtin_fmaf(mz[c].y, f, Z);
-    O = __builtin_fmaf(o[static_cast<size_t>(c) * hd], f, O);
+  const int nb = dim / QK_K;
+  for (int b = wave; b < nb; b += 4) {
+    const int i0 = b * QK_K + 4 * lane;
+    const int h = i0 / hd, d0 = i0 - h * hd;
+    const float2* mz = part_mz + t * tok_stride_mz + static_cast<size_t>(h) * max_chunks;
+    const float* o = part_o + t * tok_stride_o + static_cast<size_t>(h) * max_chunks * hd + d0;
+    float m = mz[0].x;
+    for (int c = 1; c < nch; ++c) m = fmaxf(m, mz[c].x);
+    float Z = 0.0f;
+    float O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < nch; ++c) {
+      const float2 zc = mz[c];
+      const f32x4 oc = *reinterpret_cast<const f32x4*>(o + static_cast<size_t>(c) * hd);
+      const float f = exp_f32(zc.x - m);
+      Z = __builtin_fmaf(zc.y, f, Z);
+      O[0] = __builtin_fmaf(oc.x, f, O[0]);
+      O[1] = __builtin_fmaf(oc.y, f, O[1]);
+      O[2] = __builtin_fmaf(oc.z, f, O[2]);
+      O[3] = __builtin_fmaf(oc.w, f, O[3]);
+    }
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = O[k] / Z;
+    uint32_t packed;
+    float dq;
+    int gsum;
+    quant_block_wave(v, false, packed, dq, gsum);
+    _Float16* out = xh + static_cast<size_t>(t) * dim + i0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      out[k] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((packed >> (8 * k)) & 0xffu)));
+    if ((lane & 3) == 0) xbs[(static_cast<size_t>(t) * nb + b) * 16 + (lane >> 2)] = static_cast<_Float16>(gsum);
+    if (lane == 0) xd[static_cast<size_t>(t) * nb + b] = dq;
   }
-  out[static_cast<size_t>(t) * n_out + i] = O / Z;
 }
 
 // -------------------------------------------------------------- launchers --
@@ -522,11 +551,12 @@ hipError_t launch_rope_kv_batch(const float* qkv, int n_tok, int qd, int kvd, in
   return hipGetLastError();
 }
 
-hipError_t launch_attn_combine_batch(const AttnPart& part, size_t tok_stride_o, size_t tok_stride_mz, int pos0,
-                                     int n_tok, int n_heads, int head_dim, int max_chunks, float* out, hipStream_t s) {
-  const int n = n_heads * head_dim;
-  hipLaunchKernelGGL(k_attn_combine_batch, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, part.o, part.mz,
-                     tok_stride_o, tok_stride_mz, pos0, n, head_dim, max_chunks, out);
+hipError_t launch_quant_batch_attn(const AttnPart& part, size_t tok_stride_o, size_t tok_stride_mz, int pos0,
+                                  int n_tok, int n_heads, int head_dim, int max_chunks, QuantBatch q, hipStream_t s) {
+  const int dim = n_heads * head_dim;
+  if (dim % QK_K || head_dim % 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_quant_batch_attn, dim3(n_tok), dim3(256), 0, s, part.o, part.mz, tok_stride_o, tok_stride_mz,
+                     pos0, dim, head_dim, max_chunks, q.xh, q.xd, q.xbs);
   return hipGetLastError();
 }
 
