@@ -209,6 +209,7 @@ hipError_t op_launch(mcpm_ctx* c, F&& launch) {
   g_launch_timing = LaunchTiming{p.first, p.second};
   const hipError_t err = launch();
   g_launch_timing = LaunchTiming{};
+  if (err != hipSuccess) --c->op_used;  // no kernel, no events to read
   return err;
 }
 
