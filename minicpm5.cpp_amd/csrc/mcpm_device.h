@@ -128,12 +128,29 @@ __device__ __forceinline__ void quant_block_row16(const float (&v)[16], bool awa
   gsum = s;
 }
 
+// v of lane ^ 16 and of lane ^ 32 by gfx950's row swaps (v_permlane16_swap /
+// v_permlane32_swap on two copies of v), in VALU instead of an LDS-routed
+// permute.  permlane16_swap(v, v) gives rows (0, 0, 2, 2) and (1, 1, 3, 3) of
+// v; permlane32_swap(v, v) gives rows (0, 1, 0, 1) and (2, 3, 2, 3).
+__device__ __forceinline__ float lane_xor16(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float((threadIdx.x & 16) ? p[0] : p[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float((threadIdx.x & 32) ? p[0] : p[1]);
+}
+
 // wave_tree_sum with the same pairwise order (lane t += lane t+s for s =
-// 32..1; lane 0 holds the total): s = 32, 16 across rows, s <= 8 by DPP row
-// shifts (only lanes < s read, and those stay inside their row).
+// 32..1; lane 0 holds the total): s = 32, 16 across rows (lane t < s reads
+// lane t + s = t ^ s; the other lanes' values are not read again by lane 0's
+// chain), s <= 8 by DPP row shifts (only lanes < s read, and those stay
+// inside their row).
 __device__ __forceinline__ float wave_tree_sum_fast(float v) {
-  v = v + __shfl_down(v, 32);
-  v = v + __shfl_down(v, 16);
+  v = v + lane_xor32(v);
+  v = v + lane_xor16(v);
   v = v + dpp_f<0x108>(v);  // row_shl:8
   v = v + dpp_f<0x104>(v);  // row_shl:4
   v = v + dpp_f<0x102>(v);  // row_shl:2

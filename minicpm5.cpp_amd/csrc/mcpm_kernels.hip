@@ -175,8 +175,8 @@ inline int attn_max_splits(int lo, int hi) {
 // across rows.
 __device__ __forceinline__ float wave_max_fast(float v) {
   v = row16_max(v);
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
+  v = fmaxf(v, lane_xor16(v));
+  v = fmaxf(v, lane_xor32(v));
   return v;
 }
 
