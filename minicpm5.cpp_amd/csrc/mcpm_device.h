@@ -20,17 +20,62 @@ __device__ __forceinline__ uint16_t ld_stream_u16(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// Lane moves within rows of 16 lanes (DPP): quad_perm [1,0,3,2] (lane ^ 1),
+// quad_perm [2,3,0,1] (lane ^ 2), row rotate by 4 and by 8.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+// Maximum over the 16 lanes of the row, on every lane of the row.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+  v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+  v = fmaxf(v, dpp_f<DPP_ROR4>(v));
+  v = fmaxf(v, dpp_f<DPP_ROR8>(v));
   return v;
 }
 
+// v of lane ^ 16 and of lane ^ 32 by gfx950's row swaps (v_permlane16_swap /
+// v_permlane32_swap on two copies of v), in VALU instead of an LDS-routed
+// permute.  permlane16_swap(v, v) gives rows (0, 0, 2, 2) and (1, 1, 3, 3) of
+// v; permlane32_swap(v, v) gives rows (0, 1, 0, 1) and (2, 3, 2, 3).
+__device__ __forceinline__ float lane_xor16(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float((threadIdx.x & 16) ? p[0] : p[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float((threadIdx.x & 32) ? p[0] : p[1]);
+}
+
+// Maximum over the wave on every lane (order-free): within rows, then across.
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, lane_xor16(v));
+  return fmaxf(v, lane_xor32(v));
+}
+
 // Pairwise tree over the 64 lanes: lane t += lane t+s for s = 32..1; lane 0
-// holds the total (the oracle's tree_sum over 64 slots).
+// holds the total (the oracle's tree_sum over 64 slots).  s = 32, 16 across
+// rows (lane t < s reads lane t + s = t ^ s; the other lanes' values are not
+// read again by lane 0's chain), s <= 8 by DPP row shifts (only lanes < s
+// read, and those stay inside their row).  Only lane 0's value is defined.
 __device__ __forceinline__ float wave_tree_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_down(v, o);
+  v = v + lane_xor32(v);
+  v = v + lane_xor16(v);
+  v = v + dpp_f<0x108>(v);  // row_shl:8
+  v = v + dpp_f<0x104>(v);  // row_shl:4
+  v = v + dpp_f<0x102>(v);  // row_shl:2
+  v = v + dpp_f<0x101>(v);  // row_shl:1
   return v;
 }
 
@@ -61,32 +106,10 @@ __device__ __forceinline__ void quant_block_wave(const float v[4], bool away, ui
     s += q;
     p |= (static_cast<uint32_t>(q) & 0xffu) << (8 * k);
   }
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
+  s += dpp_i<DPP_XOR1>(s);
+  s += dpp_i<DPP_XOR2>(s);
   packed = p;
   gsum = s;
-}
-
-// Lane moves within rows of 16 lanes (DPP): quad_perm [1,0,3,2] (lane ^ 1),
-// quad_perm [2,3,0,1] (lane ^ 2), row rotate by 4 and by 8.
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;
-
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
-}
-
-// Maximum over the 16 lanes of the row, on every lane of the row.
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_f<DPP_XOR1>(v));
-  v = fmaxf(v, dpp_f<DPP_XOR2>(v));
-  v = fmaxf(v, dpp_f<DPP_ROR4>(v));
-  v = fmaxf(v, dpp_f<DPP_ROR8>(v));
-  return v;
 }
 
 // Quantizes one 256-value block held by a row of 16 lanes (lane j owns values
@@ -128,35 +151,8 @@ __device__ __forceinline__ void quant_block_row16(const float (&v)[16], bool awa
   gsum = s;
 }
 
-// v of lane ^ 16 and of lane ^ 32 by gfx950's row swaps (v_permlane16_swap /
-// v_permlane32_swap on two copies of v), in VALU instead of an LDS-routed
-// permute.  permlane16_swap(v, v) gives rows (0, 0, 2, 2) and (1, 1, 3, 3) of
-// v; permlane32_swap(v, v) gives rows (0, 1, 0, 1) and (2, 3, 2, 3).
-__device__ __forceinline__ float lane_xor16(float v) {
-  const unsigned u = __float_as_uint(v);
-  const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  return __uint_as_float((threadIdx.x & 16) ? p[0] : p[1]);
-}
-__device__ __forceinline__ float lane_xor32(float v) {
-  const unsigned u = __float_as_uint(v);
-  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __uint_as_float((threadIdx.x & 32) ? p[0] : p[1]);
-}
-
-// wave_tree_sum with the same pairwise order (lane t += lane t+s for s =
-// 32..1; lane 0 holds the total): s = 32, 16 across rows (lane t < s reads
-// lane t + s = t ^ s; the other lanes' values are not read again by lane 0's
-// chain), s <= 8 by DPP row shifts (only lanes < s read, and those stay
-// inside their row).
-__device__ __forceinline__ float wave_tree_sum_fast(float v) {
-  v = v + lane_xor32(v);
-  v = v + lane_xor16(v);
-  v = v + dpp_f<0x108>(v);  // row_shl:8
-  v = v + dpp_f<0x104>(v);  // row_shl:4
-  v = v + dpp_f<0x102>(v);  // row_shl:2
-  v = v + dpp_f<0x101>(v);  // row_shl:1
-  return v;
-}
+// The same tree (kept under the name its callers use).
+__device__ __forceinline__ float wave_tree_sum_fast(float v) { return wave_tree_sum(v); }
 
 // block_rms_from_partials with one barrier: every wave runs the tree over the
 // 256 slots itself (slots l, l+64, l+128, l+192 on lane l, then the wave tree),
