@@ -154,14 +154,21 @@ __device__ int smp_search(const uint32_t* __restrict__ key, const float* __restr
     if (tid < m) sb[tid] = bs[b0 + tid];
     __syncthreads();
     if (tid == 0) {
-      for (int j = 0; j < m; ++j) {
-        const double nxt = off + sb[j];
-        const bool hit = FLOAT_CMP ? (static_cast<float>(nxt) >= thr_f) : (thr_d <= nxt);
-        if (hit) {
-          found = b0 + j;
-          break;
+      // the sums in order, read 8 at a time ahead of their adds (the adds
+      // stay one chain: this position's sum is the previous one's plus it)
+      for (int j0 = 0; j0 < m && found < 0; j0 += 8) {
+        double v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = sb[min(j0 + q, m - 1)];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          if (found < 0 && j0 + q < m) {
+            const double nxt = off + v[q];
+            const bool hit = FLOAT_CMP ? (static_cast<float>(nxt) >= thr_f) : (thr_d <= nxt);
+            if (hit) found = b0 + j0 + q;
+            else off = nxt;
+          }
         }
-        off = nxt;
       }
       s_int[0] = found;
     }
@@ -183,13 +190,18 @@ __device__ int smp_search(const uint32_t* __restrict__ key, const float* __restr
   int pos = -1;
   double pre = 0.0;
   if (tid == 0) {
-    for (int j = 0; j < cnt; ++j) {
-      pre = pre + static_cast<double>(sv[j]);
-      const double c = off + pre;
-      const bool hit = FLOAT_CMP ? (static_cast<float>(c) >= thr_f) : (thr_d <= c);
-      if (hit) {
-        pos = k0 + j;
-        break;
+    for (int j0 = 0; j0 < cnt && pos < 0; j0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = sv[min(j0 + q, cnt - 1)];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if (pos < 0 && j0 + q < cnt) {
+          pre = pre + static_cast<double>(v[q]);
+          const double c = off + pre;
+          const bool hit = FLOAT_CMP ? (static_cast<float>(c) >= thr_f) : (thr_d <= c);
+          if (hit) pos = k0 + j0 + q;
+        }
       }
     }
   }
