@@ -139,45 +139,86 @@ __global__ void __launch_bounds__(SMP_B) k_smp_bsum(const uint32_t* __restrict__
 // first block whose end sum reaches it, then the first position of that
 // block whose running sum does; positions at or past `limit` do not count.
 // Returns (thread 0) the position, or -1 when no position below limit does;
-// `run` gets that position's running sum.
+// `run` gets that position's running sum.  The block phase either scans the
+// block sums in order (recording each block's end sum in rec[] when rec is
+// given and the blocks fit) or, with nrec >= 0, looks the block up among the
+// end sums a previous scan recorded: the same sums, so the same block.
+constexpr int SMP_REC = 2048;  // block end sums k_smp_pick keeps (vocabularies up to 524,288)
+
 template <bool FLOAT_CMP>
 __device__ int smp_search(const uint32_t* __restrict__ key, const float* __restrict__ p, int n, int topp,
                           const double* __restrict__ bs, int nblk, double thr_d, float thr_f, int limit, double* sb,
-                          float* sv, int* s_int, double* s_dbl, double& run) {
+                          float* sv, int* s_int, double* s_dbl, double& run, double* rec, int nrec) {
   const int tid = threadIdx.x;
-  // block search over the block sums (staged through LDS), thread 0
   double off = 0.0;
   int found = -1;
-  for (int b0 = 0; b0 < nblk && found < 0; b0 += SMP_B) {
-    const int m = min(SMP_B, nblk - b0);
-    __syncthreads();
-    if (tid < m) sb[tid] = bs[b0 + tid];
-    __syncthreads();
-    if (tid == 0) {
-      // the sums in order, read 8 at a time ahead of their adds (the adds
-      // stay one chain: this position's sum is the previous one's plus it)
-      for (int j0 = 0; j0 < m && found < 0; j0 += 8) {
-        double v[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = sb[min(j0 + q, m - 1)];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (found < 0 && j0 + q < m) {
-            const double nxt = off + v[q];
-            const bool hit = FLOAT_CMP ? (static_cast<float>(nxt) >= thr_f) : (thr_d <= nxt);
-            if (hit) found = b0 + j0 + q;
-            else off = nxt;
-          }
-        }
+  if (nrec >= 0) {
+    // first recorded block whose end sum reaches the threshold
+    int best = 0x7fffffff;
+    for (int j = tid; j < nrec; j += SMP_B) {
+      const double e = rec[j];
+      const bool hit = FLOAT_CMP ? (static_cast<float>(e) >= thr_f) : (thr_d <= e);
+      if (hit) {
+        best = j;
+        break;
       }
-      s_int[0] = found;
     }
+    if (tid == 0) s_int[0] = 0x7fffffff;
     __syncthreads();
-    found = s_int[0];
+    if (best != 0x7fffffff) atomicMin(s_int, best);
+    __syncthreads();
+    found = s_int[0] == 0x7fffffff ? -1 : s_int[0];
+    off = found > 0 ? rec[found - 1] : found == 0 ? 0.0 : rec[nrec - 1];
+    __syncthreads();
+  } else {
+    // block search over the block sums (staged through LDS), thread 0
+    const bool keep = rec && nblk <= SMP_REC;
+    for (int b0 = 0; b0 < nblk && found < 0; b0 += SMP_B) {
+      const int m = min(SMP_B, nblk - b0);
+      __syncthreads();
+      if (tid < m) sb[tid] = bs[b0 + tid];
+      __syncthreads();
+      if (tid == 0) {
+        // the sums in order, read 8 at a time ahead of their adds (the adds
+        // stay one chain: this position's sum is the previous one's plus it)
+        // (the eight adds of a batch run unconditionally, then the first hit
+        // among them is picked: past it nothing is used)
+        for (int j0 = 0; j0 < m && found < 0; j0 += 8) {
+          double c[8];
+          double acc = off;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            acc = acc + sb[min(j0 + q, m - 1)];
+            c[q] = acc;
+          }
+          const int nv = min(8, m - j0);
+          int hq = 8;
+#pragma unroll
+          for (int q = 7; q >= 0; --q) {
+            const bool hit = FLOAT_CMP ? (static_cast<float>(c[q]) >= thr_f) : (thr_d <= c[q]);
+            if (q < nv && hit) hq = q;
+          }
+          if (keep) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+              if (q < nv && q <= hq) rec[b0 + j0 + q] = c[q];
+          }
+          // the sum before the hit, or after the batch (selects: no indexed array)
+          const int lim = min(hq, nv);
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (q < lim) off = c[q];
+          if (hq < 8) found = b0 + j0 + hq;
+        }
+        s_int[0] = found;
+      }
+      __syncthreads();
+      found = s_int[0];
+    }
+    if (tid == 0) s_dbl[0] = off;
+    __syncthreads();
+    off = s_dbl[0];
   }
-  if (tid == 0) s_dbl[0] = off;
-  __syncthreads();
-  off = s_dbl[0];
   if (found < 0) {
     run = off;  // the total
     return -1;
@@ -191,18 +232,26 @@ __device__ int smp_search(const uint32_t* __restrict__ key, const float* __restr
   double pre = 0.0;
   if (tid == 0) {
     for (int j0 = 0; j0 < cnt && pos < 0; j0 += 8) {
-      float v[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = sv[min(j0 + q, cnt - 1)];
+      double pr[8];
+      double acc = pre;
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        if (pos < 0 && j0 + q < cnt) {
-          pre = pre + static_cast<double>(v[q]);
-          const double c = off + pre;
-          const bool hit = FLOAT_CMP ? (static_cast<float>(c) >= thr_f) : (thr_d <= c);
-          if (hit) pos = k0 + j0 + q;
-        }
+        acc = acc + static_cast<double>(sv[min(j0 + q, cnt - 1)]);
+        pr[q] = acc;
       }
+      const int nv = min(8, cnt - j0);
+      int hq = 8;
+#pragma unroll
+      for (int q = 7; q >= 0; --q) {
+        const double c = off + pr[q];
+        const bool hit = FLOAT_CMP ? (static_cast<float>(c) >= thr_f) : (thr_d <= c);
+        if (q < nv && hit) hq = q;
+      }
+      if (hq < 8) pos = k0 + j0 + hq;
+      const int last = hq < 8 ? hq : nv - 1;  // the hit's running sum, or the batch's last
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (q <= last) pre = pr[q];
     }
   }
   run = off + pre;
@@ -215,30 +264,36 @@ __global__ void __launch_bounds__(SMP_B) k_smp_pick(const uint32_t* __restrict__
                                                     StepState* st, int* __restrict__ out_tokens) {
   __shared__ double sb[SMP_B];
   __shared__ float sv[SMP_B];
-  __shared__ int s_int[1];
+  __shared__ int s_int[2];
   __shared__ double s_dbl[1];
+  __shared__ double rec[SMP_REC];  // block end sums of the cut's scan, for the walk's lookup
   // the cut: first position whose running sum, rounded to float, reaches top_p
+  // (the scan records the end sums of the blocks it passes, up to the cut's)
   int cnt = n;
   double C = 0.0;
   if (topp) {
-    const int k = smp_search<true>(key, p, n, topp, bs, nblk, 0.0, top_p, n, sb, sv, s_int, s_dbl, C);
+    const int k = smp_search<true>(key, p, n, topp, bs, nblk, 0.0, top_p, n, sb, sv, s_int, s_dbl, C, rec, -1);
     if (k >= 0) cnt = k + 1;  // else: every position, C = the total
   } else {
-    (void)smp_search<true>(key, p, n, topp, bs, nblk, 0.0, __builtin_inff(), n, sb, sv, s_int, s_dbl, C);
+    (void)smp_search<true>(key, p, n, topp, bs, nblk, 0.0, __builtin_inff(), n, sb, sv, s_int, s_dbl, C, rec, -1);
   }
   // thread 0 holds cnt and C; the walk's threshold to every thread (after
   // every thread's last read of the search's broadcast slots)
   __syncthreads();
   if (threadIdx.x == 0) {
     s_int[0] = cnt;
+    s_int[1] = cnt > 0 ? (cnt - 1) / SMP_B + 1 : 0;  // blocks the cut's scan recorded: through the cut's block
     s_dbl[0] = static_cast<double>(r) * C;
   }
   __syncthreads();
   cnt = s_int[0];
+  const int nrec = nblk <= SMP_REC ? min(s_int[1], nblk) : -1;
   const double t = s_dbl[0];
   __syncthreads();
+  // the walk: t = r*C < C, so its block is at or before the cut's, whose end
+  // sums the scan recorded
   double run = 0.0;
-  int k = smp_search<false>(key, p, n, topp, bs, nblk, t, 0.0f, cnt, sb, sv, s_int, s_dbl, run);
+  int k = smp_search<false>(key, p, n, topp, bs, nblk, t, 0.0f, cnt, sb, sv, s_int, s_dbl, run, rec, nrec);
   if (threadIdx.x == 0) {
     if (k < 0) k = cnt - 1;
     const int tok = topp ? id[k] : k;
