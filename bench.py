@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Batch-1 greedy decode of the MiniCPM5-2.4B-shaped Q4_K_M model on one MI355X.
 
-Workload (the BASELINE full-model configuration): 40 layers, hidden 2304,
+Workload (the full 2.4B-shaped model): 40 layers, hidden 2304,
 32 q / 8 kv heads of 64, FFN 5760 SwiGLU, vocab 130560 with a tied Q6_K LM
 head, Q6_K attn_v / ffn_down, Q4_K elsewhere, F32 norms; random-init weights
 N(0, 0.02) from a fixed seed; a 32-token random-ID prompt, then greedy decode.
@@ -33,7 +33,7 @@ FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16
 # HBM bytes per launch by kernel class from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # runs, scaled by the same counters on a device copy of known size
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_2p4b_traffic.json")
-SEED = 20260105  # BASELINE seed 20260101 + configuration index 4
+SEED = 20260105  # base seed 20260101 + 4, the full-model workload's index
 PROMPT = 32
 
 
@@ -245,7 +245,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(batch-1 decode does not shard, see DESIGN.md)", file=sys.stderr)
+              "(batch-1 decode of one model runs on one GPU)", file=sys.stderr)
         sys.exit(2)
 
     cfg = mcpm.config_2p4b()

@@ -41,7 +41,7 @@ public:
     // chat driver keeps the cache across turns and prefills only the new
     // tokens (pos0 = tokens already cached) instead of re-running the history.
     void prefill(const std::vector<int>& tokens, int pos0);
-    // A synthetic model image (seeded random weights, BASELINE shapes).
+    // A synthetic model image (seeded random weights, the benchmark's shapes).
     bool load_synthetic(const mcpm_model_config& cfg, uint64_t seed, int mix, bool verbose = false);
     const mcpm_model_config& config() const { return cfg_; }
 

@@ -1,7 +1,7 @@
 /*
  * mcpm_oracle.h -- CPU oracle for the MiniCPM5 batch-1 decode path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: it is loaded by the
+ * TEST INFRASTRUCTURE ONLY.  This library checks the product: it is loaded by the
  * tests, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, never by
  * the product library (minicpm5.cpp_amd/), which must fail loudly without its
  * HIP build instead of falling back here.

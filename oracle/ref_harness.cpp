@@ -2,7 +2,7 @@
 //
 // TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles this file together with
 // the reference's src/ops/{ops,ops_avx2,ops_scalar_optimized}.cpp, read where
-// they lie under /root/reference (nothing is copied), into
+// they lie in the reference's tree (nothing is copied), into
 // oracle/_ref/librefops.so.  Tests use it to pin the oracle against the
 // reference's compiled numerics; bench.py may time it as the CPU baseline.
 //

@@ -11,7 +11,7 @@ regenerated from seeds by the library's deterministic generator
 the SHA-256 of its generated weight bytes so a changed generator is detected
 instead of silently compared.  Outputs are the reference's.
 
-Fixtures (BASELINE configurations, seeds 20260101 + config index):
+Fixtures (the benchmark's single-op and model workloads, seeds 20260101 + workload index):
   c1_q4k_gemv.npz        single Q4_K GEMV 5760x2304 (quantize_row_q8_K + matmul)
   c2_ffn_block.npz       RMSNorm -> gate/up Q4_K -> SwiGLU -> down Q6_K (FFN 5760, K padded to 5888)
   c3_attention.npz       QKV Q4_K, RoPE 1e4, attention at contexts 512 / 2048 / 4096

@@ -315,7 +315,7 @@ def test_argmax_first_index(ctx):
     assert ctx.download(od, np.int32, 1)[0] == int(np.argmax(x))
 
 
-# -------------------------------------------------- BASELINE configurations
+# ------------------------------------ single-op workloads C1-C3 (2.4B shapes)
 
 def _weights(seed, tid, rows, cols, gtype, real_cols=None):
     real_cols = real_cols or cols
