@@ -197,6 +197,58 @@ def ops_measure(ctx, eng, cfg, bd, cold_mb=640):
     return out
 
 
+def read_floor_measure(ctx, bd, pool_mb=1024, grids=(512, 1024, 2048, 4096)):
+    """The floor of one launch that reads as many bytes as a GEMV class: a
+    read-only kernel (mcpm_stream_read: 16-byte non-temporal loads, a
+    grid-stride loop) over the class's bytes per launch, each launch on the
+    next region of a pool_mb rotation (so the bytes come from HBM, as the
+    weights do in decode), the best of a few grid sizes; kernel durations from
+    HIP events at each kernel's start and end, as the class timings are."""
+    pool_bytes = pool_mb << 20
+    pool = ctx.alloc(pool_bytes)
+    sink = ctx.alloc(max(grids) * 4)
+    out = {"pool_MB": round(pool_bytes / 1e6, 1), "classes": {}}
+    gemv_us = floor_us = 0.0
+    try:
+        mcpm.check(ctx.lib.mcpm_fill_device(ctx.h, pool.ptr, 1, pool_bytes))
+        for name in ("qkv", "oproj", "gate_up", "down", "lm_head"):
+            d = bd[name]
+            nbytes = -(-d["bytes_per_launch"] // 16) * 16
+            nreg = pool_bytes // nbytes
+            reps = max(16, min(400, (4 << 30) // nbytes))
+
+            def run(n, g):
+                for r in range(n):
+                    mcpm.check(ctx.lib.mcpm_stream_read(ctx.h, pool.ptr + (r % nreg) * nbytes, nbytes, g,
+                                                        sink.ptr))
+
+            best = None
+            for g in grids:
+                run(8, g)
+                ctx.op_time()
+                ctx.set_op_timing(True)
+                run(reps, g)
+                ms, n = ctx.op_time()
+                ctx.set_op_timing(False)
+                us = 1e3 * ms / max(n, 1)
+                if best is None or us < best[0]:
+                    best = (us, g)
+            lpt = d["launches_per_token"]
+            gemv_us += d["avg_us"] * lpt
+            floor_us += best[0] * lpt
+            out["classes"][name] = {"bytes": nbytes, "floor_us": round(best[0], 3), "grid": best[1],
+                                    "floor_GBps": round(nbytes / (best[0] * 1e-6) / 1e9, 1),
+                                    "kernel_us": round(d["avg_us"], 3),
+                                    "floor_over_kernel": round(best[0] / d["avg_us"], 4)}
+    finally:
+        sink.free()
+        pool.free()
+    out["gemv_us_per_token"] = round(gemv_us, 1)
+    out["floor_us_per_token"] = round(floor_us, 1)
+    out["floor_over_gemv_per_token"] = round(floor_us / gemv_us, 4)
+    return out
+
+
 def cpu_baseline(image, cfg_vocab, budget_s=15.0):
     """The reference's own CPU ops (oracle/_ref, AVX2 + OpenMP) when built,
     else the oracle's C restatement, timed on a bounded decode sample."""
@@ -317,6 +369,12 @@ def main():
             f"{c1['cold']['us']:.2f} us cold ({c1['cold']['GBps']:.0f} GB/s); "
             f"C2 FFN block {ops['c2_ffn_block']['us']:.2f} us; C3 QKV+attention "
             + ", ".join(f"{k}: {v['us']:.2f} us" for k, v in ops["c3_qkv_attention"].items()))
+        rf = read_floor_measure(ctx, bd)
+        ops["read_floor"] = rf
+        log("read floor (one read-only launch of each GEMV class's bytes): "
+            + ", ".join(f"{k} {v['floor_us']:.2f} us vs {v['kernel_us']:.2f}" for k, v in rf["classes"].items())
+            + f"; GEMVs {rf['gemv_us_per_token']:.0f} us/token, floor {rf['floor_us_per_token']:.0f} us/token "
+            f"({100 * rf['floor_over_gemv_per_token']:.0f} %)")
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

@@ -72,6 +72,14 @@ int mcpm_copy_to_host(mcpm_ctx *ctx, void *dst, const void *src, size_t bytes);
  * that scales the HBM byte counters in the measurements). */
 int mcpm_copy_device(mcpm_ctx *ctx, void *dst, const void *src, size_t bytes);
 int mcpm_fill_device(mcpm_ctx *ctx, void *dst, int byte_value, size_t bytes);
+/* Read-only pass over `bytes` of device memory at `src` (a positive multiple
+ * of 16, 16-byte aligned) by `grid` work groups of 256 lanes (1 .. 65536),
+ * one word per work group written to `out` (device memory, `grid` words);
+ * stream-ordered, timed like the per-op entries (mcpm_set_op_timing).  Its
+ * duration is the floor of one launch that reads as many bytes as a GEMV.
+ * No counterpart in the reference: a measurement kernel, as mcpm_copy_device
+ * is for the byte counters. */
+int mcpm_stream_read(mcpm_ctx *ctx, const void *src, size_t bytes, int grid, uint32_t *out);
 
 /* ------------------------------------------------------------ weights ---- */
 

@@ -315,6 +315,15 @@ int mcpm_copy_device(mcpm_ctx* c, void* dst, const void* src, size_t bytes) {
   return MCPM_OK;
 }
 
+int mcpm_stream_read(mcpm_ctx* c, const void* src, size_t bytes, int grid, uint32_t* out) {
+  if (!c || !src || !out) return fail(MCPM_ERR_ARG, "mcpm_stream_read: null argument");
+  if (bytes == 0 || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+    return fail(MCPM_ERR_ARG, "mcpm_stream_read: bytes must be a positive multiple of 16 and src 16-byte aligned");
+  if (grid < 1 || grid > 65536) return fail(MCPM_ERR_ARG, "mcpm_stream_read: grid must be 1 .. 65536");
+  MCPM_HIP(op_launch(c, [&] { return launch_stream_read(src, bytes, grid, out, c->stream); }));
+  return MCPM_OK;
+}
+
 int mcpm_fill_device(mcpm_ctx* c, void* dst, int v, size_t bytes) {
   if (!c || (!dst && bytes)) return fail(MCPM_ERR_ARG, "mcpm_fill_device: null argument");
   MCPM_HIP(hipMemsetAsync(dst, v, bytes, c->stream));

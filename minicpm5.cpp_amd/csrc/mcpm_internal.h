@@ -290,6 +290,7 @@ hipError_t launch_quant_batch_attn(const AttnPart& part, size_t tok_stride_o, si
 hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s);
 hipError_t launch_dequant_rows(const WView& w, int row0, int n_rows, int cols, float* out, hipStream_t s);
 hipError_t launch_gemv_f32(const float* w, const float* x, float* out, int rows, int cols, hipStream_t s);
+hipError_t launch_stream_read(const void* src, size_t bytes, int grid, uint32_t* out, hipStream_t s);
 hipError_t launch_gemv_q8_0(const WView& w, const float* x, float* out, int rows, int cols, hipStream_t s);
 hipError_t launch_argmax_partial(const float* x, int n, float2* part, int nparts, hipStream_t s);
 hipError_t launch_argmax_final(const float2* part, int nparts, int* out_token, StepState* st, int* out_tokens,

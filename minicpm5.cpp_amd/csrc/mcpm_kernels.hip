@@ -652,6 +652,33 @@ hipError_t launch_gemv_f32(const float* w, const float* x, float* out, int rows,
   return hipGetLastError();
 }
 
+// Read-only pass: every 16-byte word of src once (non-temporal loads, as the
+// GEMVs stream their weights), a grid-stride loop over `grid` work groups; one
+// xor per work group goes to out so the loads stay.  Its duration is the floor
+// of one launch that reads as many bytes as a GEMV class.
+__global__ void __launch_bounds__(256) k_stream_read(const u32x4* __restrict__ src, size_t n16,
+                                                     uint32_t* __restrict__ out) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  uint32_t acc = 0;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride) {
+    const u32x4 v = __builtin_nontemporal_load(src + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  __shared__ uint32_t s[256];
+  s[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t a = 0;
+    for (int t = 0; t < 256; ++t) a ^= s[t];
+    out[blockIdx.x] = a;
+  }
+}
+
+hipError_t launch_stream_read(const void* src, size_t bytes, int grid, uint32_t* out, hipStream_t s) {
+  launch_kernel(k_stream_read, dim3(grid), dim3(256), 0, s, static_cast<const u32x4*>(src), bytes / 16, out);
+  return hipGetLastError();
+}
+
 // gemv_q8_0 (src/ops/ops.cpp:58-79): per block s = sum over i of float(q_i)*x_i
 // (i ascending, multiply then add); row = row + s*d over blocks in order.
 // One lane per row.

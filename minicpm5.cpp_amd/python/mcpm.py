@@ -70,6 +70,7 @@ _SIGS = {
     "mcpm_sync": (_I, [_P]),
     "mcpm_device_info": (_I, [_P, C.POINTER(_I), C.c_char_p, _SZ]),
     "mcpm_device_alloc": (_I, [_P, _SZ, C.POINTER(_P)]),
+    "mcpm_stream_read": (_I, [_P, _P, _SZ, _I, _P]),
     "mcpm_device_free": (_I, [_P, _P]),
     "mcpm_copy_to_device": (_I, [_P, _P, _P, _SZ]),
     "mcpm_copy_to_host": (_I, [_P, _P, _P, _SZ]),

@@ -437,3 +437,35 @@ def test_op_timing_counts_gemv_kernels(ctx):
     finally:
         ctx.set_op_timing(False)
         ctx.sync()
+
+
+def test_stream_read_covers_every_word(ctx):
+    """mcpm_stream_read (the read floor's kernel): work group b xors the
+    16-byte words i with (i // 256) % grid == b, so every word is read once;
+    bad sizes, alignment and grids are refused before any launch."""
+    rng = np.random.default_rng(20260105)
+    n16 = 3 * 4096 + 17
+    words = rng.integers(0, 2**32, size=n16 * 4, dtype=np.uint64).astype(np.uint32)
+    announce("stream read")
+    src = ctx.upload(words)
+    for grid in (1, 7, 64, 300):
+        sink = ctx.zeros(grid * 4)
+        try:
+            mcpm.check(ctx.lib.mcpm_stream_read(ctx.h, src.ptr, n16 * 16, grid, sink.ptr))
+            got = ctx.download(sink, np.uint32, grid)
+            per16 = np.bitwise_xor.reduce(words.reshape(n16, 4), axis=1)
+            owner = (np.arange(n16) // 256) % grid
+            want = np.zeros(grid, np.uint32)
+            np.bitwise_xor.at(want, owner, per16)
+            assert np.array_equal(got, want), grid
+        finally:
+            sink.free()
+    sink = ctx.zeros(64 * 4)
+    try:
+        for ptr, nbytes, grid in ((src.ptr, 40, 4), (src.ptr + 4, 64, 4), (src.ptr, 64, 0), (src.ptr, 0, 4),
+                                  (src.ptr, 64, 65537)):
+            assert ctx.lib.mcpm_stream_read(ctx.h, ptr, nbytes, grid, sink.ptr) == -2  # MCPM_ERR_ARG
+    finally:
+        sink.free()
+        src.free()
+        ctx.sync()
