@@ -13,7 +13,9 @@ Printed: one JSON line with tokens/s, the achieved HBM bandwidth of the
 dominant kernel against the 8 TB/s peak (HIP events around its launches, on
 the engine stream), and the reference's CPU path timed on this host's cores;
 beside them the long-context prefill and sampled decode, and the single-op
-configurations (one GEMV cold and warm, the FFN block, QKV + attention).
+configurations (one GEMV cold and warm, the FFN block, QKV + attention)
+with, for each GEMV class, one read-only launch of its bytes as the floor a
+single launch of that size can reach.
 """
 import argparse
 import json
