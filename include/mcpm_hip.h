@@ -279,10 +279,17 @@ int64_t mcpm_engine_kernel_bytes(const mcpm_engine *e, int kernel_class);
  * N(0, 0.02) and norm gains 1 + N(0, 0.1) from a counter-based generator
  * keyed by (seed, tensor, index), quantized with this library's Q4_K / Q6_K /
  * Q8_0 encoders.  mix 0: Q6_K for every attn_v and ffn_down (literal
- * Q4_K_M reading); mix 1: llama.cpp's use_more_bits layers only.
- * tied: one Q6_K token_embd shared with the LM head.  When path is NULL the
- * image is returned in *image (free with mcpm_free_host) and its size in
- * *image_bytes. */
+ * Q4_K_M reading); mix 1: llama.cpp's use_more_bits layers only; with
+ * cfg->tied_embeddings one Q6_K token_embd serves as the LM head, else a
+ * separate Q6_K output.weight follows it.  mix 2: the layout of the
+ * reference's own file (include/minicpm_metadata.h:30-32): an untied Q6_K
+ * output.weight, a Q4_K token_embd.weight, use_more_bits for attn_v and
+ * ffn_down, tensors in that file's order, and a tokenizer.ggml.tokens
+ * vocabulary the reference's tokenizer reads (src/tokenizer.cpp:10-60);
+ * tied_embeddings is ignored.  A tensor's values depend on its name only, so
+ * mixes and layouts agree wherever they store the same tensor with the same
+ * type.  When path is NULL the image is returned in *image (free with
+ * mcpm_free_host) and its size in *image_bytes. */
 int mcpm_synth_gguf(const mcpm_model_config *cfg, uint64_t seed, int mix, const char *path, void **image,
                     size_t *image_bytes);
 void mcpm_free_host(void *p);

@@ -68,17 +68,25 @@ bool read_scalar(Reader& r, uint32_t t, GgufValue& v) {
 
 size_t gguf_tensor_bytes(uint32_t type, const std::vector<uint64_t>& dims) {
   if (dims.empty()) return 0;
+  // every product is checked against 2^62 so no step wraps (0: not a valid size)
+  constexpr uint64_t kLimit = uint64_t{1} << 62;
   uint64_t rows = 1;
-  for (size_t i = 1; i < dims.size(); ++i) rows *= dims[i];
+  for (size_t i = 1; i < dims.size(); ++i) {
+    if (dims[i] != 0 && rows > kLimit / dims[i]) return 0;
+    rows *= dims[i];
+  }
   const uint64_t cols = dims[0];
+  uint64_t per_row = 0;  // bytes of one row
   switch (type) {
-    case 0: return static_cast<size_t>(cols * rows * 4);
-    case 1: return static_cast<size_t>(cols * rows * 2);
-    case 8: return cols % 32 ? 0 : static_cast<size_t>(cols / 32 * 34 * rows);
-    case 12: return cols % 256 ? 0 : static_cast<size_t>(cols / 256 * 144 * rows);
-    case 14: return cols % 256 ? 0 : static_cast<size_t>(cols / 256 * 210 * rows);
+    case 0: per_row = cols > kLimit / 4 ? 0 : cols * 4; break;
+    case 1: per_row = cols > kLimit / 2 ? 0 : cols * 2; break;
+    case 8: per_row = cols % 32 ? 0 : cols / 32 * 34; break;
+    case 12: per_row = cols % 256 ? 0 : cols / 256 * 144; break;
+    case 14: per_row = cols % 256 ? 0 : cols / 256 * 210; break;
     default: return 0;
   }
+  if (rows != 0 && per_row > kLimit / rows) return 0;
+  return static_cast<size_t>(per_row * rows);
 }
 
 const GgufTensor* GgufFile::find(const std::string& name) const {
@@ -136,9 +144,15 @@ bool gguf_parse(const uint8_t* data, size_t size, GgufFile& out, std::string& er
       v.arr_type = r.get<uint32_t>();
       v.arr_len = r.get<uint64_t>();
       if (v.arr_type == GGUF_STRING) {
+        if (v.arr_len > (size - r.off) / 8) {  // each string takes at least its 8-byte length
+          err = "bad array in key " + key;
+          return false;
+        }
+        v.strs.reserve(v.arr_len);
         for (uint64_t k = 0; k < v.arr_len && r.ok; ++k) {
           std::string tmp;
           r.str(tmp);
+          v.strs.push_back(std::move(tmp));
         }
       } else {
         const size_t es = scalar_size(v.arr_type);
@@ -179,9 +193,15 @@ bool gguf_parse(const uint8_t* data, size_t size, GgufFile& out, std::string& er
     }
   }
   const uint64_t data_start = (r.off + out.alignment - 1) / out.alignment * out.alignment;
+  if (data_start > size) {
+    err = "truncated GGUF: no data section";
+    return false;
+  }
   for (auto& t : out.tensors) {
     t.bytes = gguf_tensor_bytes(t.type, t.dims);
-    if (data_start + t.offset + t.bytes > size) {
+    // in this order no sum can wrap: offset and size each checked against
+    // what is left of the file
+    if (t.offset > size - data_start || t.bytes > size - data_start - t.offset) {
       err = "tensor " + t.name + " extends past the end of the file";
       return false;
     }
@@ -211,6 +231,15 @@ void GgufWriter::kv_str(const std::string& k, const std::string& v) {
   kv_.emplace_back(k, x);
 }
 
+void GgufWriter::kv_str_array(const std::string& k, const std::vector<std::string>& v) {
+  GgufValue x;
+  x.type = GGUF_ARRAY;
+  x.arr_type = GGUF_STRING;
+  x.arr_len = v.size();
+  x.strs = v;
+  kv_.emplace_back(k, x);
+}
+
 void GgufWriter::add_tensor(const std::string& name, uint32_t type, const std::vector<uint64_t>& dims) {
   GgufTensor t;
   t.name = name;
@@ -225,8 +254,14 @@ size_t GgufWriter::layout(std::vector<size_t>& abs) {
   size_t h = 4 + 4 + 8 + 8;
   for (const auto& kv : kv_) {
     h += 8 + kv.first.size() + 4;
-    if (kv.second.type == GGUF_STRING) h += 8 + kv.second.str.size();
-    else h += scalar_size(kv.second.type);
+    if (kv.second.type == GGUF_STRING) {
+      h += 8 + kv.second.str.size();
+    } else if (kv.second.type == GGUF_ARRAY) {
+      h += 4 + 8;
+      for (const auto& e : kv.second.strs) h += 8 + e.size();
+    } else {
+      h += scalar_size(kv.second.type);
+    }
   }
   for (const auto& t : tensors_) h += 8 + t.name.size() + 4 + 8 * t.dims.size() + 4 + 8;
   header_bytes_ = h;
@@ -263,6 +298,12 @@ void GgufWriter::write_header(uint8_t* image) const {
     put(&kv.second.type, 4);
     if (kv.second.type == GGUF_STRING) {
       put_str(kv.second.str);
+    } else if (kv.second.type == GGUF_ARRAY) {
+      const uint32_t at = GGUF_STRING;
+      const uint64_t n = kv.second.strs.size();
+      put(&at, 4);
+      put(&n, 8);
+      for (const auto& e : kv.second.strs) put_str(e);
     } else if (kv.second.type == GGUF_FLOAT32) {
       const float f = static_cast<float>(kv.second.num);
       put(&f, 4);

@@ -28,6 +28,7 @@ struct GgufValue {
   std::string str;      // GGUF_STRING
   uint32_t arr_type = 0;  // GGUF_ARRAY element type
   uint64_t arr_len = 0;
+  std::vector<std::string> strs;  // string arrays (kept by the reader and the writer)
 };
 
 struct GgufTensor {
@@ -63,6 +64,8 @@ class GgufWriter {
   void kv_u32(const std::string& k, uint32_t v);
   void kv_f32(const std::string& k, float v);
   void kv_str(const std::string& k, const std::string& v);
+  // An array of strings (as tokenizer.ggml.tokens, src/tokenizer.cpp:33-48).
+  void kv_str_array(const std::string& k, const std::vector<std::string>& v);
   // Adds a tensor; its bytes are produced later by the fill callback of
   // write(), in tensor order, at the given offset of the output image.
   void add_tensor(const std::string& name, uint32_t type, const std::vector<uint64_t>& dims);

@@ -150,7 +150,8 @@ void free_engine(mcpm_engine* e) {
 }
 
 int load_f32(mcpm_ctx* ctx, const GgufTensor* t, int n, float** out) {
-  if (!t || t->type != MCPM_TYPE_F32 || static_cast<int64_t>(t->dims[0]) != n)
+  if (!t || t->type != MCPM_TYPE_F32 || static_cast<int64_t>(t->dims[0]) != n ||
+      t->bytes != static_cast<size_t>(n) * sizeof(float))
     return fail(MCPM_ERR_FORMAT, "missing or malformed F32 tensor " + (t ? t->name : std::string("?")));
   MCPM_HIP(hipMalloc(out, n * sizeof(float)));
   MCPM_HIP(hipMemcpyAsync(*out, t->data, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
@@ -200,7 +201,8 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
   const GgufTensor* to = f.find("output.weight");
   c.tied_embeddings = to ? 0 : 1;
   const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
-  if (c.n_layers <= 0 || c.dim <= 0 || c.dim % QK_K || c.dim / QK_K > MAX_NB || qd % QK_K || qd / QK_K > MAX_NB ||
+  if (c.n_layers <= 0 || c.dim <= 0 || c.vocab <= 0 || c.n_heads <= 0 || c.head_dim <= 0 || qd <= 0 ||
+      c.dim % QK_K || c.dim / QK_K > MAX_NB || qd % QK_K || qd / QK_K > MAX_NB ||
       c.ffn <= 0 || c.ffn_pad < c.ffn || c.ffn_pad % QK_K || c.ffn_pad / QK_K > MAX_NB || c.n_kv_heads <= 0 ||
       c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 8 || c.head_dim % 8 || c.head_dim > 128 ||
       kvd % 8 || c.n_kv_heads > 256)
@@ -247,6 +249,7 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->logits), static_cast<size_t>(c.vocab) * 4);
   if (!rc) {
     GemvArgs a{};
+    a.reg[0].w = view_of(e->out_w);  // the kernel instance (and its occupancy) follows the head's type
     a.total_rows = c.vocab;
     a.nreg = 1;
     a.nb = c.dim / QK_K;
@@ -396,6 +399,7 @@ int enqueue_token(mcpm_engine* e) {
     a.gamma = e->out_norm;
     a.eps = c.eps;
     a.argmax_part = e->argmax_part;
+    a.argmax_parts = e->lm_grid;
     MCPM_HIP(timed(e, MCPM_KC_LM_HEAD, [&] { return launch_gemv(a, PRO_NORM_EVEN, EPI_LOGITS, n_cu, s); }));
   }
   if (!e->sample_mode) MCPM_HIP(launch_argmax_final(e->argmax_part, e->lm_grid, nullptr, e->st, e->out_tokens, s));

@@ -997,6 +997,8 @@ hipError_t launch_one(const GemvArgs& a, int n_items, const Shape& sh, int n_cu,
   if (TILE && sh.NW != GEMV_TILE_WAVES) return hipErrorInvalidValue;  // the kernel's launch bound
   if (GRP && (sh.S * a.nb > 256 * sh.KB || sh.S > 64)) return hipErrorInvalidValue;
   const int grid = grid_for<PRO, EPI, TILE, WT, GRP>(n_items, sh, n_cu, lds);
+  // the argmax partials: one per wave of the grid, as many as the caller sized
+  if (EPI == EPI_LOGITS && grid * sh.NW != a.argmax_parts) return hipErrorInvalidValue;
   if (grid <= 0) return hipSuccess;
   launch_kernel(k_gemv<PRO, EPI, TILE, WT, GRP>, dim3(grid), dim3(64 * sh.NW), lds, s, a, n_items, sh.S, sh.KB);
   return hipGetLastError();
@@ -1041,7 +1043,7 @@ int gemv_grid(const GemvArgs& a0, int n_cu) {
   const Shape sh = pick_shape(a, PRO_NORM_EVEN, EPI_LOGITS, n_cu);
   const int n_items = n_items_of(a, sh);
   const size_t lds = lds_bytes(a, sh, PRO_NORM_EVEN);
-  const bool q4 = weight_kind(a) == WT_Q4;
+  const bool q4 = weight_kind(a) == WT_Q4;  // a.reg[0].w must be the head's weights
   constexpr int P = PRO_NORM_EVEN, E = EPI_LOGITS;
   const int grid = sh.tile ? (q4 ? grid_for<P, E, true, WT_Q4>(n_items, sh, n_cu, lds)
                                  : grid_for<P, E, true, WT_Q6>(n_items, sh, n_cu, lds))

@@ -210,7 +210,8 @@ struct GemvArgs {
   int kvd;
   float* resid;
   float* h_out;
-  float2* argmax_part;   // per WG (value, index as float bits)
+  float2* argmax_part;   // per wave (value, index as float bits)
+  int argmax_parts;      // EPI_LOGITS: entries of argmax_part (the launch must write exactly these)
 };
 
 // Device step state shared by the engine's kernels.

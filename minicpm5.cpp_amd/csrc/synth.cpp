@@ -211,6 +211,41 @@ static void quantize_rows_impl(int type, const float* src, int64_t rows, int64_t
   }
 }
 
+// A vocabulary of n strings for tokenizer.ggml.tokens, the key the reference's
+// tokenizer reads (src/tokenizer.cpp:10-60): a few chat control tokens, the
+// 256 byte tokens "<0xHH>", one token per byte in GPT-2's byte-to-unicode
+// mapping (printable bytes 33-126, 161-172, 174-255 as themselves, the other
+// 68 bytes as code points 256, 257, ... in byte order), so that any text
+// tokenizes, then distinct filler strings.  The words carry no meaning: the
+// weights are random.
+std::vector<std::string> synth_vocabulary(int n) {
+  std::vector<std::string> v = {"<unk>", "<s>", "</s>", "<|im_start|>", "<|im_end|>", "<think>", "</think>",
+                                "<tool_call>", "</tool_call>", "/think", "/no_think"};
+  char buf[16];
+  for (int b = 0; b < 256; ++b) {
+    std::snprintf(buf, sizeof buf, "<0x%02X>", b);
+    v.emplace_back(buf);
+  }
+  auto utf8 = [](uint32_t cp) {
+    std::string s;
+    if (cp < 0x80) {
+      s += static_cast<char>(cp);
+    } else {  // every code point here is below 0x800
+      s += static_cast<char>(0xC0 | (cp >> 6));
+      s += static_cast<char>(0x80 | (cp & 0x3F));
+    }
+    return s;
+  };
+  uint32_t next = 256;
+  for (int b = 0; b < 256; ++b) {
+    const bool printable = (b >= 33 && b <= 126) || (b >= 161 && b <= 172) || (b >= 174);
+    v.push_back(utf8(printable ? static_cast<uint32_t>(b) : next++));
+  }
+  for (int i = static_cast<int>(v.size()); i < n; ++i) v.push_back("w" + std::to_string(i));
+  v.resize(static_cast<size_t>(n));
+  return v;
+}
+
 }  // namespace mcpm
 
 using namespace mcpm;
@@ -242,7 +277,8 @@ void mcpm_free_host(void* p) { std::free(p); }
 
 int mcpm_synth_gguf(const mcpm_model_config* cfg, uint64_t seed, int mix, const char* path, void** image,
                     size_t* image_bytes) {
-  if (!cfg || cfg->n_layers <= 0 || cfg->dim % 256 || cfg->ffn <= 0 || cfg->vocab <= 0 || cfg->n_heads <= 0 ||
+  if (!cfg || mix < 0 || mix > 2 || cfg->n_layers <= 0 || cfg->dim % 256 || cfg->ffn <= 0 || cfg->vocab <= 0 ||
+      cfg->n_heads <= 0 ||
       cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads || cfg->head_dim <= 0 || cfg->head_dim % 2)
     return fail(MCPM_ERR_ARG, "mcpm_synth_gguf: invalid config");
   const int ffn_pad = (cfg->ffn + 255) / 256 * 256;
@@ -269,27 +305,72 @@ int mcpm_synth_gguf(const mcpm_model_config* cfg, uint64_t seed, int mix, const 
   w.kv_u32("general.seed_lo", static_cast<uint32_t>(seed));
   w.kv_u32("general.quant_mix", static_cast<uint32_t>(mix));
 
-  // The LM head is the token embedding (tied), stored Q6_K.
-  w.add_tensor("token_embd.weight", Q6, {D, static_cast<uint64_t>(cfg->vocab)});
-  w.add_tensor("output_norm.weight", F32, {D});
-  if (!cfg->tied_embeddings) w.add_tensor("output.weight", Q6, {D, static_cast<uint64_t>(cfg->vocab)});
+  const uint64_t V = static_cast<uint64_t>(cfg->vocab);
   const int n = cfg->n_layers;
-  for (int l = 0; l < n; ++l) {
-    // llama.cpp's use_more_bits rule for mix 1; mix 0 gives every layer Q6_K v/down.
+  // llama.cpp's use_more_bits rule for mix 1 and 2; mix 0 gives every layer Q6_K v/down.
+  auto v_type = [&](int l) {
     const bool more = (l < n / 8) || (l >= 7 * n / 8) || ((l - n / 8) % 3 == 2);
-    const uint32_t vt = (mix == 0 || more) ? Q6 : Q4;
-    const std::string p = "blk." + std::to_string(l) + ".";
-    w.add_tensor(p + "attn_norm.weight", F32, {D});
-    w.add_tensor(p + "attn_q.weight", Q4, {D, static_cast<uint64_t>(qd)});
-    w.add_tensor(p + "attn_k.weight", Q4, {D, static_cast<uint64_t>(kvd)});
-    w.add_tensor(p + "attn_v.weight", vt, {D, static_cast<uint64_t>(kvd)});
-    w.add_tensor(p + "attn_output.weight", Q4, {static_cast<uint64_t>(qd), D});
-    w.add_tensor(p + "ffn_norm.weight", F32, {D});
-    w.add_tensor(p + "ffn_gate.weight", Q4, {D, static_cast<uint64_t>(cfg->ffn)});
-    w.add_tensor(p + "ffn_up.weight", Q4, {D, static_cast<uint64_t>(cfg->ffn)});
-    w.add_tensor(p + "ffn_down.weight", vt, {static_cast<uint64_t>(ffn_pad), D});
+    return (mix == 0 || more) ? Q6 : Q4;
+  };
+  if (mix == 2) {
+    // The reference's own file (include/minicpm_metadata.h:30-32 and the
+    // tensor table after it): an untied Q6_K output.weight, a Q4_K
+    // token_embd.weight, and per layer the tensors in name order; plus the
+    // vocabulary its tokenizer reads.
+    w.kv_str("tokenizer.ggml.model", "gpt2");
+    w.kv_str_array("tokenizer.ggml.tokens", synth_vocabulary(cfg->vocab));
+    w.add_tensor("output.weight", Q6, {D, V});
+    w.add_tensor("output_norm.weight", F32, {D});
+    w.add_tensor("token_embd.weight", Q4, {D, V});
+    for (int l = 0; l < n; ++l) {
+      const std::string p = "blk." + std::to_string(l) + ".";
+      w.add_tensor(p + "attn_k.weight", Q4, {D, static_cast<uint64_t>(kvd)});
+      w.add_tensor(p + "attn_norm.weight", F32, {D});
+      w.add_tensor(p + "attn_output.weight", Q4, {static_cast<uint64_t>(qd), D});
+      w.add_tensor(p + "attn_q.weight", Q4, {D, static_cast<uint64_t>(qd)});
+      w.add_tensor(p + "attn_v.weight", v_type(l), {D, static_cast<uint64_t>(kvd)});
+      w.add_tensor(p + "ffn_down.weight", v_type(l), {static_cast<uint64_t>(ffn_pad), D});
+      w.add_tensor(p + "ffn_gate.weight", Q4, {D, static_cast<uint64_t>(cfg->ffn)});
+      w.add_tensor(p + "ffn_norm.weight", F32, {D});
+      w.add_tensor(p + "ffn_up.weight", Q4, {D, static_cast<uint64_t>(cfg->ffn)});
+    }
+  } else {
+    // The LM head is the token embedding (tied), stored Q6_K.
+    w.add_tensor("token_embd.weight", Q6, {D, V});
+    w.add_tensor("output_norm.weight", F32, {D});
+    if (!cfg->tied_embeddings) w.add_tensor("output.weight", Q6, {D, V});
+    for (int l = 0; l < n; ++l) {
+      const std::string p = "blk." + std::to_string(l) + ".";
+      w.add_tensor(p + "attn_norm.weight", F32, {D});
+      w.add_tensor(p + "attn_q.weight", Q4, {D, static_cast<uint64_t>(qd)});
+      w.add_tensor(p + "attn_k.weight", Q4, {D, static_cast<uint64_t>(kvd)});
+      w.add_tensor(p + "attn_v.weight", v_type(l), {D, static_cast<uint64_t>(kvd)});
+      w.add_tensor(p + "attn_output.weight", Q4, {static_cast<uint64_t>(qd), D});
+      w.add_tensor(p + "ffn_norm.weight", F32, {D});
+      w.add_tensor(p + "ffn_gate.weight", Q4, {D, static_cast<uint64_t>(cfg->ffn)});
+      w.add_tensor(p + "ffn_up.weight", Q4, {D, static_cast<uint64_t>(cfg->ffn)});
+      w.add_tensor(p + "ffn_down.weight", v_type(l), {static_cast<uint64_t>(ffn_pad), D});
+    }
   }
   std::vector<size_t> offs;
+  if (mix == 2 && cfg->n_layers == 42 && cfg->dim == 2048 && cfg->n_heads == 16 && cfg->n_kv_heads == 2 &&
+      cfg->head_dim == 128 && cfg->ffn == 6144 && cfg->vocab == 130560) {
+    // At the reference's own geometry the tensor data starts where it starts
+    // in the reference's file (output.weight at 5,145,568,
+    // include/minicpm_metadata.h:30), so the tensor offsets compiled into the
+    // reference (TENSORS_INFO) address this file's tensors: one string
+    // key/value pads the header to that length.
+    constexpr size_t kRefDataStart = 5145568;
+    const std::string key = "general.padding";
+    const size_t entry = 8 + key.size() + 4 + 8;  // key length, key, type, string length
+    const size_t h = w.layout(offs) - [&] {
+      size_t data = 0;
+      for (const auto& t : w.tensors()) data += (t.bytes + 31) / 32 * 32;
+      return data;
+    }();
+    if (h + entry > kRefDataStart) return fail(MCPM_ERR_ARG, "mcpm_synth_gguf: header too large to pad");
+    w.kv_str(key, std::string(kRefDataStart - h - entry, ' '));
+  }
   const size_t total = w.layout(offs);
   uint8_t* img = static_cast<uint8_t*>(std::calloc(total, 1));
   if (!img) return fail(MCPM_ERR_NOMEM, "mcpm_synth_gguf: host allocation failed");

@@ -1,4 +1,4 @@
-// kv_session.cpp -- KVSession over MiniCPM5Engine's generate_*_at calls.
+// kv_session.cpp -- KVSession over the engine's generate_*_at calls (mcpm_host).
 #include "kv_session.h"
 
 #include <algorithm>
@@ -28,9 +28,9 @@ std::vector<int> KVSession::generate_response(const std::vector<int>& conversati
     const std::vector<int> rest(conversation.begin() + static_cast<std::ptrdiff_t>(keep), conversation.end());
     const int pos0 = static_cast<int>(keep);
     std::vector<int> out =
-        sampling.greedy ? engine_.generate_greedy_at(rest, pos0, n_gen)
-                        : engine_.generate_sampled_at(rest, pos0, n_gen, sampling.temperature, sampling.top_p,
-                                                      sampling.seed + static_cast<uint32_t>(turns_));
+        sampling.greedy ? mcpm_host::generate_greedy_at(engine_, rest, pos0, n_gen)
+                        : mcpm_host::generate_sampled_at(engine_, rest, pos0, n_gen, sampling.temperature,
+                                                         sampling.top_p, sampling.seed + static_cast<uint32_t>(turns_));
     // rows now valid: the conversation, then every generated token but the last
     cached_.assign(conversation.begin(), conversation.end());
     cached_.insert(cached_.end(), out.begin(), out.end() - 1);

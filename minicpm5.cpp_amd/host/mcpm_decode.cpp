@@ -102,7 +102,12 @@ int main(int argc, char** argv) {
         return 2;
     }
 
+    // The reference CLI's order (src/main.cpp:107-111): the KV cache first,
+    // then the model.
+    int max_seq = n_prompt + n_tokens;
+    for (int t : turns) max_seq += t + n_tokens;
     MiniCPM5Engine engine;
+    engine.init_kv_cache(max_seq);
     bool ok;
     if (!gguf.empty()) {
         ok = engine.load_model(gguf, verbose);
@@ -120,13 +125,10 @@ int main(int argc, char** argv) {
         c.rope_base = 10000.0f;
         c.eps = 1e-6f;
         c.tied_embeddings = 1;
-        ok = engine.load_synthetic(c, static_cast<uint64_t>(synth_seed), 0, verbose);
+        ok = mcpm_host::load_synthetic(engine, c, static_cast<uint64_t>(synth_seed), 0, verbose);
     }
     if (!ok) return 1;
-    const mcpm_model_config& cfg = engine.config();
-    int max_seq = n_prompt + n_tokens;
-    for (int t : turns) max_seq += t + n_tokens;
-    engine.init_kv_cache(max_seq);
+    const mcpm_model_config cfg = mcpm_host::config(engine);
 
     std::vector<int> prompt = prompt_ids;
     if (prompt.empty()) {
@@ -173,8 +175,8 @@ int main(int argc, char** argv) {
     const auto t0 = std::chrono::steady_clock::now();
     double decode_s = 0.0;
     if (device_loop) {
-        out = sample ? engine.generate_sampled(prompt, n_tokens, temperature, top_p, sample_seed)
-                     : engine.generate_greedy(prompt, n_tokens);
+        out = sample ? mcpm_host::generate_sampled(engine, prompt, n_tokens, temperature, top_p, sample_seed)
+                     : mcpm_host::generate_greedy(engine, prompt, n_tokens);
         decode_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     } else {
         auto argmax = [](const std::vector<float>& v) {
@@ -185,7 +187,7 @@ int main(int argc, char** argv) {
         };
         int pos = 0, next = 0;
         if (use_prefill && prompt.size() > 1) {
-            engine.prefill(std::vector<int>(prompt.begin(), prompt.end() - 1), 0);
+            mcpm_host::prefill(engine, std::vector<int>(prompt.begin(), prompt.end() - 1), 0);
             pos = static_cast<int>(prompt.size()) - 1;
         }
         for (size_t i = static_cast<size_t>(pos); i < prompt.size(); ++i)

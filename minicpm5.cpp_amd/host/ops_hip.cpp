@@ -4,6 +4,8 @@
 // reference's CPU kernels.
 #include "ops.h"
 
+#include "mcpm_hip.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -119,9 +121,6 @@ void fit(std::vector<T>& v, size_t n) {
 
 }  // namespace
 
-namespace mcpm_host {
-mcpm_ctx* context() { return ctx(); }
-}  // namespace mcpm_host
 
 float silu(float x) { return x / (1.0f + std::exp(-x)); }
 

@@ -388,6 +388,9 @@ class Engine:
     def set_prefill(self, enable: bool):
         check(self.lib.mcpm_engine_set_prefill(self.h, int(enable)))
 
+    def uses_prefill(self) -> bool:
+        return bool(self.lib.mcpm_engine_uses_prefill(self.h))
+
     def prefill(self, tokens, pos0: int = 0):
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         check(self.lib.mcpm_engine_prefill(self.h, t.ctypes.data_as(C.POINTER(C.c_int)), t.size, pos0))

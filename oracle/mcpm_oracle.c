@@ -96,7 +96,8 @@ static void quantize_block(const float *x, or_block_q8_K *dst, int ties_away) {
     }
     /* The source reads amax / 127.0f; the reference's -ffast-math build
      * (-freciprocal-math) evaluates it as amax * (1/127.0f).  Pinned against
-     * the compiled reference in tests/test_oracle_vs_ref.py. */
+     * the compiled reference in tests/test_oracle.py (test_quantize_golden,
+     * test_quantize_row_q8k). */
     dst->d = amax * (1.0f / 127.0f);
     const float mul = 127.0f / amax;
     for (int i = 0; i < OR_QK_K; ++i) {
@@ -639,7 +640,9 @@ int or_model_init_kv(or_model *m, int max_seq_len) {
 }
 
 /* MiniCPM5Engine::forward (src/model.cpp:142-242) with explicit shapes. */
-int or_model_forward(or_model *m, int token, int pos, float *logits) {
+/* Every layer of one token (src/model.cpp:142-227); the hidden state is left
+ * in m->x.  Returns 0, or -1 when pos is past the KV capacity. */
+static int or_model_layers(or_model *m, int token, int pos) {
     const or_config *c = &m->c;
     const int qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
     or_get_embedding(m->x, m->embd_type, m->embd, c->dim, token);
@@ -660,6 +663,16 @@ int or_model_forward(or_model *m, int token, int pos, float *logits) {
         or_matmul_q8k(L->wd_type, L->wd, m->hq, m->dn, c->dim, c->ffn_pad);
         for (int i = 0; i < c->dim; ++i) m->x[i] = m->x[i] + m->dn[i];
     }
+    return 0;
+}
+
+/* A prompt token whose logits nobody reads: the layers (so its K and V rows
+ * reach the cache) without the LM head. */
+int or_model_forward_kv(or_model *m, int token, int pos) { return or_model_layers(m, token, pos); }
+
+int or_model_forward(or_model *m, int token, int pos, float *logits) {
+    const or_config *c = &m->c;
+    if (or_model_layers(m, token, pos) != 0) return -1;
     or_rmsnorm(m->xn, m->x, m->out_norm, c->dim, c->eps);
     float *lg = logits ? logits : (float *)malloc(sizeof(float) * (size_t)c->vocab);
     or_matmul(m->out_type, m->out_w, m->xn, lg, c->vocab, c->dim);
@@ -669,6 +682,14 @@ int or_model_forward(or_model *m, int token, int pos, float *logits) {
 }
 
 const float *or_model_hidden(const or_model *m) { return m->x; }
+
+int or_model_read_kv(const or_model *m, int layer, int pos0, int n, float *k, float *v) {
+    const size_t kvd = (size_t)m->c.n_kv_heads * (size_t)m->c.head_dim;
+    if (!m->kc || layer < 0 || layer >= m->c.n_layers || pos0 < 0 || n < 0 || pos0 + n > m->max_seq) return -1;
+    if (k) memcpy(k, m->kc[layer] + (size_t)pos0 * kvd, (size_t)n * kvd * sizeof(float));
+    if (v) memcpy(v, m->vc[layer] + (size_t)pos0 * kvd, (size_t)n * kvd * sizeof(float));
+    return 0;
+}
 
 void or_model_free(or_model *m) {
     if (!m) return;

@@ -124,8 +124,12 @@ or_model *or_model_create(const or_config *cfg, const void *embd, int embd_type,
 int or_model_init_kv(or_model *m, int max_seq_len);
 /* One token through the model; logits (vocab floats) may be NULL. Returns argmax. */
 int or_model_forward(or_model *m, int token, int pos, float *logits);
+/* The layers only (K/V rows into the cache), no LM head; 0 or -1. */
+int or_model_forward_kv(or_model *m, int token, int pos);
 /* Hidden state after the last layer (dim floats), for tests. */
 const float *or_model_hidden(const or_model *m);
+/* K and V cache rows [pos0, pos0+n) of one layer into k, v (either may be NULL); 0 or -1. */
+int or_model_read_kv(const or_model *m, int layer, int pos0, int n, float *k, float *v);
 void or_model_free(or_model *m);
 
 /* mt19937 + uniform_real_distribution<float>(0,1) as libstdc++ computes it,

@@ -71,7 +71,9 @@ _ORACLE_SIGS = {
     "or_model_create": (_P, [C.POINTER(OrConfig), _P, _I, _P, _P, _I, C.POINTER(OrLayer)]),
     "or_model_init_kv": (_I, [_P, _I]),
     "or_model_forward": (_I, [_P, _I, _I, _P]),
+    "or_model_forward_kv": (_I, [_P, _I, _I]),
     "or_model_hidden": (_P, [_P]),
+    "or_model_read_kv": (_I, [_P, _I, _I, _I, _P, _P]),
     "or_model_free": (None, [_P]),
     "or_mt_seed": (None, [_P, C.c_uint32]),
     "or_mt_next": (C.c_uint32, [_P]),
@@ -274,6 +276,14 @@ class OracleModel:
             return self.lib.ref_model_forward(self.h, ptr(self._x), pos, ptr(logits))
         return self.lib.or_model_forward(self.h, token, pos, ptr(logits))
 
+    def forward_kv(self, token, pos):
+        """The layers of a token whose logits are not read (its K/V rows
+        reach the cache), as the engine's batched prefill leaves them."""
+        if self.ref:
+            lg = np.empty(self.cfg.vocab, np.float32)
+            return self.forward(token, pos, lg)
+        return self.lib.or_model_forward_kv(self.h, token, pos)
+
     def hidden(self):
         f = self.lib.ref_model_hidden if self.ref else self.lib.or_model_hidden
         return np.ctypeslib.as_array(C.cast(f(self.h), C.POINTER(C.c_float)), shape=(self.cfg.dim,)).copy()
@@ -293,6 +303,40 @@ class OracleModel:
             if logits_cb:
                 logits_cb(i, lg)
         return np.array(out, np.int32)
+
+    def generate_sampled(self, prompt, n_gen, temperature, top_p, seed, max_seq=None, logits_cb=None):
+        """The engine's sampled loop (mcpm_engine_generate_sampled): prompt
+        tokens but the last only fill the cache, the last gives the first
+        logits; each logits vector is sampled by or_sample_blocked (the device
+        sampler's arithmetic, src/sampler.cpp:8-73 with blocked double sums)
+        on one draw of std::uniform_real_distribution<float> over
+        std::mt19937(seed) per generated token."""
+        orc = oracle()
+        V = self.cfg.vocab
+        self.init_kv(max_seq or len(prompt) + n_gen)
+        gen = np.zeros(625, np.uint32)  # or_mt19937 state
+        orc.or_mt_seed(gen.ctypes.data, seed)
+        lg = np.empty(V, np.float32)
+        for p, t in enumerate(prompt[:-1]):
+            self.forward_kv(int(t), p)
+        self.forward(int(prompt[-1]), len(prompt) - 1, lg)
+        out = []
+        for i in range(n_gen):
+            if logits_cb:
+                logits_cb(i, lg)
+            nxt = orc.or_sample_blocked(ptr(lg), V, temperature, top_p, orc.or_mt_uniform01(gen.ctypes.data))
+            out.append(nxt)
+            if i < n_gen - 1:
+                self.forward(int(nxt), len(prompt) + i, lg)
+        return np.array(out, np.int32)
+
+    def kv_rows(self, layer, pos0, n):
+        """K and V cache rows [pos0, pos0+n) of one layer (copies)."""
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        k = np.empty(n * kvd, np.float32)
+        v = np.empty(n * kvd, np.float32)
+        assert self.lib.or_model_read_kv(self.h, layer, pos0, n, ptr(k), ptr(v)) == 0
+        return k, v
 
     def close(self):
         if self.h:

@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "mcpm_hip.h"
 #include "ops.h"
 
 namespace {

@@ -16,14 +16,23 @@ Fixtures (the benchmark's single-op and model workloads, seeds 20260101 + worklo
   c2_ffn_block.npz       RMSNorm -> gate/up Q4_K -> SwiGLU -> down Q6_K (FFN 5760, K padded to 5888)
   c3_attention.npz       QKV Q4_K, RoPE 1e4, attention at contexts 512 / 2048 / 4096
   q8k_quant.npz          Q8_K quantizer outputs (ties-even and the fused lround ones)
-  small_model_greedy.npz greedy tokens + logits of a 4-layer model (reference ops, restated forward)
+  small_model_greedy.npz greedy tokens + logits of a 4-layer model in the reference file's layout
+                         (Q4_K token_embd, untied Q6_K output; reference ops, restated forward)
   refshape_*_greedy.npz  the reference's MiniCPM5-2B geometry at 1 and 3 layers: 64 greedy tokens
-                         (reference ops), at the first seed the oracle reproduces for 64 steps
-  full_model_oracle.npz  (--full) the CPU ORACLE's 32+64-step greedy decode of the 2.4B-shaped
-                         model: tokens and the SHA-256 of every step's logits.  Not the reference:
-                         the reference's own output on this 40-layer random-init model is not
-                         reproducible (OpenMP float reduction order, -ffast-math rsqrtss/rcpps
-                         estimates), see tests/test_oracle.py::test_reference_is_not_reproducible.
+                         (reference ops), at the first seed the oracle reproduces for 64 steps;
+                         refshape_layout_greedy.npz the same geometry in the reference file's layout
+  full_model_oracle.npz  (--full) the CPU ORACLE's greedy decode of the 2.4B-shaped model, the
+                         benchmark's 32-token prompt and 256 steps: tokens and the SHA-256 of every
+                         step's logits.  Not the reference: the reference's own output on this
+                         40-layer random-init model is not reproducible (OpenMP float reduction
+                         order, -ffast-math rsqrtss/rcpps estimates), see
+                         tests/test_oracle.py::test_reference_is_not_reproducible.
+  c5_long_sampled.npz    (--full) the CPU ORACLE's long-context sampled decode of the same model: a
+                         1024-token random prompt, 512 tokens at temperature 0.8 / top-p 0.95 from
+                         std::mt19937(seed) through the device sampler's arithmetic
+                         (or_sample_blocked), the KV cache reaching 1535 of 1536 rows: tokens, the
+                         logits SHA-256 of every 32nd step and the last, and the SHA-256 of the K and
+                         V rows of layers 0, 20 and 39.
 
 The reference is run with one OpenMP thread, its only deterministic setting.
 """
@@ -140,7 +149,7 @@ def q8k(ref):
                         rmsnorm_fused=fused.view(np.uint8))
 
 
-def model_greedy(name, cfg, n_prompt, n_gen, seed, use_reference=True, search=1):
+def model_greedy(name, cfg, n_prompt, n_gen, seed, use_reference=True, search=1, mix=0, min_distinct=0):
     """Greedy decode of a synthetic model.  With use_reference the tokens are
     the reference's (its ops, one thread) and the oracle's agreement is
     recorded; `search` > 1 tries up to that many seeds and keeps the first
@@ -148,11 +157,14 @@ def model_greedy(name, cfg, n_prompt, n_gen, seed, use_reference=True, search=1)
     with the longest agreement."""
     best = None
     for s in range(seed, seed + search):
-        img = mcpm.synth_gguf(cfg, seed=s, mix=0)
+        img = mcpm.synth_gguf(cfg, seed=s, mix=mix)
         prompt = np.random.default_rng(s).integers(0, cfg.vocab, n_prompt).astype(np.int32)
         rm = O.OracleModel(img, use_reference_ops=use_reference)
         logits = []
         tokens = rm.generate_greedy(prompt, n_gen, lambda i, l: logits.append(l.copy()))
+        if len(set(tokens.tolist())) < min_distinct:
+            print(f"{name}: seed {s} gives {len(set(tokens.tolist()))} distinct tokens, skipped", flush=True)
+            continue
         agree = n_gen
         if use_reference:
             ot = O.OracleModel(img).generate_greedy(prompt, n_gen)
@@ -162,11 +174,12 @@ def model_greedy(name, cfg, n_prompt, n_gen, seed, use_reference=True, search=1)
             best = (agree, s, img, prompt, tokens, logits)
         if agree == n_gen:
             break
+    assert best is not None, f"{name}: no seed gave {min_distinct} distinct tokens"
     agree, s, img, prompt, tokens, logits = best
     L = np.stack(logits)
     srt = np.sort(L, axis=1)
     out = dict(seed=s, config=np.array([cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn,
-                                        cfg.vocab], np.int64), rope_base=np.float32(cfg.rope_base),
+                                        cfg.vocab], np.int64), rope_base=np.float32(cfg.rope_base), mix=mix,
                image_sha=sha(img), prompt=prompt, tokens=tokens, oracle_agree_steps=agree,
                top2_margin=(srt[:, -1] - srt[:, -2]), logit_sum=L.astype(np.float64).sum(1),
                logit_absmax=np.abs(L).max(1), logits_sha=np.array([sha(l) for l in L]))
@@ -178,29 +191,73 @@ def model_greedy(name, cfg, n_prompt, n_gen, seed, use_reference=True, search=1)
     return tokens
 
 
+def c5_long_sampled():
+    """The long-context sampled configuration on the CPU oracle (see the
+    module docstring); ~30 minutes on 8 cores."""
+    s = SEED + 4  # the full_model_oracle.npz model
+    cfg = mcpm.config_2p4b()
+    img = mcpm.synth_gguf(cfg, seed=s, mix=0)
+    prompt = np.random.default_rng(SEED + 5).integers(0, cfg.vocab, 1024).astype(np.int32)
+    n_gen, cap, sample_seed = 512, 1536, SEED + 5
+    steps = list(range(0, n_gen, 32)) + [n_gen - 1]
+    shas = {}
+
+    def cb(i, lg):
+        if i in steps:
+            shas[i] = sha(lg)
+            print(f"c5: step {i}", flush=True)
+
+    om = O.OracleModel(img)
+    tokens = om.generate_sampled(prompt, n_gen, 0.8, 0.95, sample_seed, max_seq=cap, logits_cb=cb)
+    written = len(prompt) + n_gen - 1
+    layers = [0, cfg.n_layers // 2, cfg.n_layers - 1]
+    kv = [om.kv_rows(l, 0, written) for l in layers]
+    om.close()
+    np.savez_compressed(os.path.join(OUT, "c5_long_sampled.npz"), seed=s, image_sha=sha(img), prompt=prompt,
+                        tokens=tokens, temperature=np.float32(0.8), top_p=np.float32(0.95), sample_seed=sample_seed,
+                        kv_capacity=cap, logits_steps=np.array(steps), logits_sha=np.array([shas[i] for i in steps]),
+                        kv_layers=np.array(layers), kv_rows=written,
+                        k_sha=np.array([sha(k) for k, _ in kv]), v_sha=np.array([sha(v) for _, v in kv]))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--full", action="store_true", help="also the 2.4B-shaped model (slow, ~1.6 GB)")
+    ap.add_argument("--only", help="comma-separated subset: c1,c2,c3,q8k,small,refshape,layout,full,c5")
     args = ap.parse_args()
     O.build()
     ref = O.reference()
     if ref is None:
         sys.exit("oracle/_ref/librefops.so not built: the reference sources are needed")
     ref.ref_set_threads(1)
-    c1(ref)
-    c2(ref)
-    c3(ref)
-    q8k(ref)
-    model_greedy("small_model_greedy.npz", mcpm.make_config(4, 512, 8, 2, 64, 1400, 4000), 16, 48, SEED + 4)
+    only = set(args.only.split(",")) if args.only else None
+    want = lambda k, full=False: (only is None and (args.full or not full)) or (only is not None and k in only)
+    if want("c1"):
+        c1(ref)
+    if want("c2"):
+        c2(ref)
+    if want("c3"):
+        c3(ref)
+    if want("q8k"):
+        q8k(ref)
+    if want("small"):
+        model_greedy("small_model_greedy.npz", mcpm.make_config(4, 512, 8, 2, 64, 1400, 4000), 16, 48, SEED + 4,
+                     search=8, mix=2, min_distinct=12)
     # The reference's own MiniCPM5-2B geometry (hidden 2048, 16/2 heads of 128,
     # FFN 6144, rope base 5e6, include/minicpm_metadata.h:10-17) at reduced depth;
     # at these seeds the reference's greedy decode is stable for 64 steps.
-    model_greedy("refshape_1layer_greedy.npz",
-                 mcpm.make_config(1, 2048, 16, 2, 128, 6144, 130560, rope_base=5e6), 16, 64, SEED + 5, search=6)
-    model_greedy("refshape_3layer_greedy.npz",
-                 mcpm.make_config(3, 2048, 16, 2, 128, 6144, 32000, rope_base=5e6), 16, 64, SEED + 9, search=1)
-    if args.full:
-        model_greedy("full_model_oracle.npz", mcpm.config_2p4b(), 32, 64, SEED + 4, use_reference=False)
+    if want("refshape"):
+        model_greedy("refshape_1layer_greedy.npz",
+                     mcpm.make_config(1, 2048, 16, 2, 128, 6144, 130560, rope_base=5e6), 16, 64, SEED + 5, search=6)
+        model_greedy("refshape_3layer_greedy.npz",
+                     mcpm.make_config(3, 2048, 16, 2, 128, 6144, 32000, rope_base=5e6), 16, 64, SEED + 9, search=1)
+    if want("layout"):
+        model_greedy("refshape_layout_greedy.npz",
+                     mcpm.make_config(3, 2048, 16, 2, 128, 6144, 130560, rope_base=5e6), 16, 64, SEED + 11, mix=2, search=8)
+    if want("full", True):
+        model_greedy("full_model_oracle.npz", mcpm.config_2p4b(), 32, 256, SEED + 4, use_reference=False)
+    if want("c5", True):
+        c5_long_sampled()
     print("fixtures written to", OUT)
 
 

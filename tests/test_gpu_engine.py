@@ -14,12 +14,14 @@ from conftest import announce, assert_bits, golden
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(n_layers=4, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1400, vocab=4000)
+SMALL_MIX = 2  # the reference file's layout: Q4_K token_embd, untied Q6_K output
 
 
 @pytest.fixture(scope="module")
 def small_image():
     g = golden("small_model_greedy.npz")
-    img = mcpm.synth_gguf(mcpm.make_config(**SMALL), seed=int(g["seed"]), mix=0)
+    assert int(g["mix"]) == SMALL_MIX
+    img = mcpm.synth_gguf(mcpm.make_config(**SMALL), seed=int(g["seed"]), mix=SMALL_MIX)
     assert hashlib.sha256(img.tobytes()).hexdigest() == str(g["image_sha"]), "model generator changed"
     return img
 
@@ -36,7 +38,7 @@ def test_config_from_gguf(small_engine):
     c = small_engine.cfg
     assert (c.n_layers, c.dim, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn, c.ffn_pad, c.vocab) == \
         (4, 512, 8, 2, 64, 1400, 1536, 4000)
-    assert c.tied_embeddings == 1
+    assert c.tied_embeddings == 0  # separate output.weight
     assert abs(c.rope_base - 10000.0) < 1e-3
 
 
@@ -63,7 +65,13 @@ def test_greedy_matches_oracle_and_reference(small_engine, small_image, graph):
     om = O.OracleModel(small_image)
     want = om.generate_greedy(g["prompt"], len(g["tokens"]))
     np.testing.assert_array_equal(got, want)
-    np.testing.assert_array_equal(got, g["tokens"])  # the reference's own ops
+    assert len(set(got.tolist())) > 8, "a degenerate (near-constant) token sequence pins little"
+    # the reference's own ops (one thread), for as long as the oracle agrees
+    # with them: the untied head's top-2 margins are small, and the
+    # reference's -ffast-math RMS and lane sums flip an argmax after that
+    k = int(g["oracle_agree_steps"])
+    assert k >= 16
+    np.testing.assert_array_equal(got[:k], g["tokens"][:k])
     small_engine.set_graph(True)
 
 
@@ -134,20 +142,32 @@ def _sha(a):
     return hashlib.sha256(np.ascontiguousarray(a).view(np.uint8).tobytes()).hexdigest()
 
 
-def test_full_model_greedy_64(ctx):
-    """2.4B-shaped model (40 layers, 2304 hidden, 32/8 heads of 64, FFN 5760,
-    vocab 130560, tied Q6_K head, Q6_K v/down): the 32-token prompt and 64
-    greedy steps reproduce the CPU oracle bit for bit -- every step's logits
-    (SHA-256) and every token."""
+@pytest.fixture(scope="module")
+def full_engine(ctx):
+    """The 2.4B-shaped model of the benchmark (40 layers, 2304 hidden, 32/8
+    heads of 64, FFN 5760, vocab 130560, tied Q6_K head, Q6_K v/down), KV
+    capacity 1536."""
     g = golden("full_model_oracle.npz")
     announce("full model synth")
     img = mcpm.synth_gguf(mcpm.config_2p4b(), seed=int(g["seed"]), mix=0)
     assert _sha(img) == str(g["image_sha"]), "model generator changed"
     e = mcpm.Engine(ctx, image=img)
     del img
-    e.init_kv_cache(128)
-    announce("full model greedy 32+64 (device loop)")
-    toks = e.generate_greedy(g["prompt"], 64)
+    e.init_kv_cache(1536)
+    yield e
+    e.free()
+
+
+def test_full_model_greedy_256(full_engine):
+    """The benchmark's greedy workload: the 32-token prompt and 256 greedy
+    steps reproduce the CPU oracle bit for bit -- every token, and every
+    step's logits (SHA-256) through per-token forwards."""
+    g = golden("full_model_oracle.npz")
+    e = full_engine
+    n = len(g["tokens"])
+    assert n == 256
+    announce("full model greedy 32+256 (device loop)")
+    toks = e.generate_greedy(g["prompt"], n)
     np.testing.assert_array_equal(toks, g["tokens"])
     announce("full model per-step logits")
     prompt = [int(t) for t in g["prompt"]]
@@ -159,21 +179,60 @@ def test_full_model_greedy_64(ctx):
             step = pos - (n_p - 1)
             assert _sha(logits) == str(g["logits_sha"][step]), f"logits differ at step {step}"
             assert am == int(g["tokens"][step])
-    e.free()
 
 
-@pytest.mark.parametrize("name", ["refshape_1layer_greedy.npz", "refshape_3layer_greedy.npz"])
+def test_full_model_long_context_sampled(full_engine):
+    """The long-context sampled workload at full size: a 1024-token random
+    prompt through the batched MFMA prefill, then 512 tokens sampled at
+    temperature 0.8 / top-p 0.95 by the device sampler, the KV cache reaching
+    1535 of 1536 rows.  Against the CPU oracle (per-token forwards,
+    or_sample_blocked on the same std::mt19937 draws): every token, the K and
+    V rows of three layers (SHA-256 over all 1535 positions), and the logits
+    (SHA-256) of every 32nd step and the last."""
+    g = golden("c5_long_sampled.npz")
+    e = full_engine
+    assert e.uses_prefill()
+    prompt = g["prompt"]
+    n_gen = len(g["tokens"])
+    announce(f"full model prefill {len(prompt)} + sampled {n_gen}")
+    toks = e.generate_sampled(prompt, n_gen, float(g["temperature"]), float(g["top_p"]), int(g["sample_seed"]))
+    np.testing.assert_array_equal(toks, g["tokens"])
+    rows = int(g["kv_rows"])
+    for i, l in enumerate(g["kv_layers"]):
+        announce(f"full model KV rows layer {int(l)}")
+        k, v = e.read_kv(int(l), 0, rows)
+        assert _sha(k) == str(g["k_sha"][i]), f"K rows of layer {int(l)} differ"
+        assert _sha(v) == str(g["v_sha"][i]), f"V rows of layer {int(l)} differ"
+    # a forward at an already-written position rewrites its K/V row with the
+    # same values and returns that step's logits
+    announce("full model sampled-step logits")
+    n_p = len(prompt)
+    for i, step in enumerate(g["logits_steps"]):
+        step = int(step)
+        tok = int(prompt[-1]) if step == 0 else int(g["tokens"][step - 1])
+        logits, _ = e.forward(tok, n_p - 1 + step)
+        assert _sha(logits) == str(g["logits_sha"][i]), f"logits differ at step {step}"
+
+
+@pytest.mark.parametrize("name", ["refshape_1layer_greedy.npz", "refshape_3layer_greedy.npz",
+                                  "refshape_layout_greedy.npz"])
 def test_reference_geometry_tokens(ctx, name):
     """The reference's own MiniCPM5-2B geometry (hidden 2048, 16/2 heads of
     128, FFN 6144, rope base 5e6) at reduced depth: tokens equal the
-    reference's for as long as the oracle's do (all 64 steps for one layer),
-    and equal the oracle's for all 64 steps."""
+    reference's for as long as the oracle's do (all 64 steps for one layer
+    and for the reference file's layout), and equal the oracle's for all 64
+    steps.  refshape_layout_greedy.npz is the reference file's own layout
+    (include/minicpm_metadata.h:30-32): a Q4_K token_embd, a separate Q6_K
+    output.weight at the full 130560 rows, use_more_bits v/down types."""
     g = golden(name)
     L, D, NH, NKV, HD, F, V = [int(v) for v in g["config"]]
+    mix = int(g["mix"]) if "mix" in g else 0
     cfg = mcpm.make_config(L, D, NH, NKV, HD, F, V, rope_base=float(g["rope_base"]))
-    img = mcpm.synth_gguf(cfg, seed=int(g["seed"]), mix=0)
+    img = mcpm.synth_gguf(cfg, seed=int(g["seed"]), mix=mix)
     assert _sha(img) == str(g["image_sha"]), "model generator changed"
     e = mcpm.Engine(ctx, image=img)
+    if mix == 2:
+        assert e.cfg.tied_embeddings == 0
     e.init_kv_cache(96)
     n = len(g["tokens"])
     announce(f"{name} greedy")

@@ -211,3 +211,122 @@ def test_session_turns_reuse_cache_and_match_oracle():
     om = O.OracleModel(mcpm.synth_gguf(cfg, seed=seed, mix=0))
     assert list(om.generate_greedy(prompt, n_gen)) == turns[0][3]
     om.close()
+
+
+# ------------------------------------------------------------------------
+# The reference's own sources linked against this build (oracle/Makefile
+# `dropin`, built where the reference's sources are; the programs travel as
+# built files).
+
+REF_BIN = os.path.join(ROOT, "oracle", "_ref")
+DRIVER_NATIVE = os.path.join(ROOT, "tests", "cpp", "dropin_driver")
+
+
+def _ref_program(name):
+    path = os.path.join(REF_BIN, name)
+    if not os.access(path, os.X_OK):
+        pytest.skip(f"{name} not built (make -C oracle dropin needs the reference's sources)")
+    return path
+
+
+def _tokens(stdout):
+    line = next(l for l in stdout.splitlines() if l.startswith("tokens:"))
+    return [int(t) for t in line.split()[1:]]
+
+
+@pytest.mark.gpu
+def test_reference_cli_runs_on_the_engine(tmp_path):
+    """The reference's own CLI -- src/main.cpp, chat_session.cpp, sampler.cpp,
+    tokenizer.cpp, chat_template.cpp and tool.cpp compiled unmodified against
+    its own include/ -- linked against libmcpm_model.so in place of
+    src/model.cpp and src/ops/*.cpp: it allocates the KV cache before loading
+    (main.cpp:107-111), reads the vocabulary from a reference-layout GGUF,
+    tokenizes the chat template, runs forward() per prompt token and samples
+    --n tokens on the GPU engine."""
+    cli = _ref_program("minicpm5-cli-engine")
+    cfg = mcpm.make_config(2, 512, 8, 2, 64, 1400, 4000)
+    path = str(tmp_path / "m.gguf")
+    mcpm.synth_gguf(cfg, seed=5, mix=2, path=path)
+    announce("reference CLI on libmcpm_model.so")
+    r = subprocess.run([cli, "-m", path, "--text", "Hello, world", "-n", "8", "-c", "512", "-v"],
+                       capture_output=True, text=True, timeout=300, cwd=str(tmp_path))
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "tokens) direto do arquivo GGUF" in r.stdout  # the reference tokenizer read the vocabulary
+    prompt_line = next(l for l in r.stdout.splitlines() if l.startswith("Prompt:"))
+    assert int(prompt_line.split()[1]) > 10  # the rendered chat template, tokenized
+
+
+@pytest.fixture(scope="module")
+def refgeom_file(tmp_path_factory):
+    """A synthetic model at the reference's own geometry and file layout
+    (42 layers, hidden 2048, 16/2 heads of 128, FFN 6144, vocab 130560, Q4_K
+    token_embd, Q6_K output, tensor data at the reference file's offsets)."""
+    cfg = mcpm.make_config(42, 2048, 16, 2, 128, 6144, 130560, rope_base=5e6)
+    path = str(tmp_path_factory.mktemp("refgeom") / "minicpm5-2b-synthetic.gguf")
+    announce("synthesize the reference-geometry model")
+    mcpm.synth_gguf(cfg, seed=20260115, mix=2, path=path)
+    return cfg, path
+
+
+@pytest.mark.gpu
+def test_dropin_drivers_match_native_engine(refgeom_file, tmp_path):
+    """MiniCPM5Engine driven in main.cpp's order (init_kv_cache, load_model,
+    forward per token) three ways on the reference-geometry file: this
+    build's header + libmcpm_model.so; the reference's include/model.h +
+    libmcpm_model.so (engine drop-in); the reference's include/model.h and
+    its own src/model.cpp -- loading by the tensor offsets compiled into it --
+    + libmcpm_ops.so (operator drop-in).  Each gives the native engine's
+    greedy tokens and bit-identical first-step logits."""
+    import oracle as O
+    cfg, path = refgeom_file
+    prompt, n_gen, ctx = [1, 3, 500, 70000, 130559, 42, 9, 1234], 8, 64
+    announce("native engine on the reference-geometry file")
+    c = mcpm.Context(0)
+    e = mcpm.Engine(c, gguf_path=path)
+    try:
+        assert e.cfg.tied_embeddings == 0 and e.cfg.n_layers == 42
+        e.init_kv_cache(ctx)
+        want = [int(t) for t in e.generate_greedy(prompt, n_gen)]
+        e.init_kv_cache(ctx)
+        for p, t in enumerate(prompt):
+            want_logits, _ = e.forward(t, p)
+    finally:
+        e.free()
+        c.close()
+    programs = [DRIVER_NATIVE, os.path.join(REF_BIN, "dropin_driver_engine"), os.path.join(REF_BIN, "dropin_driver_ops")]
+    ran = 0
+    for prog in programs:
+        if not os.access(prog, os.X_OK):
+            assert prog != DRIVER_NATIVE, "tests/cpp/dropin_driver not built"
+            continue
+        announce(f"{os.path.basename(prog)} on the reference-geometry file")
+        out = str(tmp_path / (os.path.basename(prog) + ".f32"))
+        r = subprocess.run([prog, path, str(ctx), str(n_gen), ",".join(map(str, prompt)), out],
+                           capture_output=True, text=True, timeout=600)
+        assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+        assert _tokens(r.stdout) == want, os.path.basename(prog)
+        np.testing.assert_array_equal(np.fromfile(out, np.float32).view(np.uint32), want_logits.view(np.uint32))
+        ran += 1
+    if ran < len(programs):
+        pytest.skip("the reference-header drivers are not built here (no reference sources)")
+    # and the native engine against the oracle on the first steps
+    announce("oracle on the reference-geometry file")
+    om = O.OracleModel(np.fromfile(path, np.uint8))
+    assert list(om.generate_greedy(prompt, 3)) == want[:3]
+    om.close()
+
+
+@pytest.mark.gpu
+def test_reference_cli_runs_on_the_operators(refgeom_file, tmp_path):
+    """The reference's CLI with its own src/model.cpp (tensor offsets
+    compiled in for its file) and libmcpm_ops.so in place of src/ops/*.cpp:
+    it loads the reference-geometry file by those offsets and runs its
+    forward() through this build's operators on the GPU."""
+    cli = _ref_program("minicpm5-cli-ops")
+    cfg, path = refgeom_file
+    announce("reference CLI on libmcpm_ops.so")
+    r = subprocess.run([cli, "-m", path, "--text", "Hi", "-n", "4", "-c", "256", "-v"],
+                       capture_output=True, text=True, timeout=600, cwd=str(tmp_path))
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    prompt_line = next(l for l in r.stdout.splitlines() if l.startswith("Prompt:"))
+    assert int(prompt_line.split()[1]) > 10

@@ -63,6 +63,34 @@ def test_dequant_bit_exact(ctx, orc, gtype):
     assert_bits(got, want)
 
 
+def test_fp16_conversion_exhaustive_on_device(ctx, orc):
+    """fp16_to_fp32 (include/ops.h:14-31) on the GPU for all 65,536 inputs:
+    Q8_0 blocks whose d runs through every half-precision bit pattern (zeros,
+    subnormals, normals, infinities, NaNs), codes +1 and -1, dequantized by
+    the device (the conversion the GEMV and embedding kernels use) against the
+    oracle's conversion, which is pinned against the reference's on the same
+    65,536 inputs.  Bit-exact for every non-NaN input (d*1 and d*-1 are exact);
+    NaN stays NaN (the reference's portable converter keeps a signalling
+    payload, the hardware conversion and F16C quiet it)."""
+    n_blk = 65536
+    rows = 64
+    cols = n_blk // rows * 32  # 1024 blocks per row
+    blk = np.zeros(n_blk, mcpm.Q8_0)
+    blk["d"] = np.arange(n_blk, dtype=np.uint32).astype(np.uint16)  # block (r, b) holds d = r*1024 + b
+    blk["qs"][:, 0::2] = 1
+    blk["qs"][:, 1::2] = -1
+    announce("fp16 exhaustive via Q8_0 dequant")
+    t = ctx.tensor(blk, mcpm.TYPE_Q8_0, cols, rows)
+    got = t.dequantize().reshape(n_blk, 32)
+    conv = np.array([orc.or_fp16_to_fp32(h) for h in range(n_blk)], np.float32)
+    nan = np.isnan(conv)
+    assert nan.sum() == 2 * 1023  # both signs, every non-zero mantissa
+    assert np.isnan(got[nan]).all()
+    want = np.stack([conv, -conv], axis=1)[~nan]
+    assert_bits(np.ascontiguousarray(got[~nan][:, 0:2]), np.ascontiguousarray(want))
+    assert_bits(np.ascontiguousarray(got[~nan][:, 30:32]), np.ascontiguousarray(want))
+
+
 def test_quantize_row_q8k(ctx, orc):
     rng = np.random.default_rng(2)
     x = rand_act(rng, 256 * 12, 3.0)

@@ -2,6 +2,7 @@
 GGUF writer/reader, the block encoders and the host sampler."""
 import hashlib
 import os
+import subprocess
 
 import numpy as np
 import pytest
@@ -104,3 +105,41 @@ def test_c_abi_rejects_bad_arguments(lib):
     n = mcpm.C.c_size_t()
     assert lib.mcpm_synth_gguf(mcpm.C.byref(cfg), 1, 0, None, mcpm.C.byref(img), mcpm.C.byref(n)) == -2
     assert b"invalid config" in lib.mcpm_last_error()
+
+
+REF = "/root/reference"
+
+
+@pytest.mark.skipif(not os.path.isdir(os.path.join(REF, "src")), reason="the reference's sources are not here")
+def test_reference_sources_link_against_the_mirror(tmp_path):
+    """The two drop-in levels build from the reference's sources, unmodified
+    and compiled against their own include/ (oracle/Makefile `dropin`): its
+    CLI with src/model.cpp and src/ops/*.cpp replaced by libmcpm_model.so,
+    and with only src/ops/*.cpp replaced by libmcpm_ops.so; the order driver
+    against the reference's include/model.h both ways.  The operator-level
+    CLI takes matmul, execute_attention, ... from libmcpm_ops.so (undefined in
+    the executable), the engine-level CLI takes MiniCPM5Engine's calls from
+    libmcpm_model.so; --help runs without a GPU."""
+    out = str(tmp_path)
+    r = subprocess.run(["make", "-C", os.path.join(ROOT, "oracle"), "dropin", f"DROPIN_OUT={out}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    names = ["minicpm5-cli-engine", "minicpm5-cli-ops", "dropin_driver_engine", "dropin_driver_ops"]
+    for n in names:
+        assert os.access(os.path.join(out, n), os.X_OK), n
+
+    def undefined(prog):
+        nm = subprocess.run(["nm", "-D", "-C", "--undefined-only", os.path.join(out, prog)],
+                            capture_output=True, text=True, check=True).stdout
+        return nm
+
+    ops_undef = undefined("minicpm5-cli-ops")
+    for fn in ("matmul(", "matmul_qkv_q8k(", "matmul_gate_up_q8k(", "execute_attention(", "get_embedding(",
+               "rmsnorm_and_quantize_q8k(", "swiglu_and_quantize_q8k(", "apply_rope("):
+        assert fn in ops_undef, fn
+    assert "MiniCPM5Engine::forward" not in ops_undef  # the reference's own src/model.cpp
+    eng_undef = undefined("minicpm5-cli-engine")
+    for fn in ("MiniCPM5Engine::init_kv_cache(int)", "MiniCPM5Engine::load_model(", "MiniCPM5Engine::forward(int, int, int)"):
+        assert fn in eng_undef, fn
+    r = subprocess.run([os.path.join(out, "minicpm5-cli-engine"), "--help"], capture_output=True, text=True)
+    assert r.returncode == 0 and "Usage" in r.stdout
