@@ -254,6 +254,10 @@ def main():
     if want("layout"):
         model_greedy("refshape_layout_greedy.npz",
                      mcpm.make_config(3, 2048, 16, 2, 128, 6144, 130560, rope_base=5e6), 16, 64, SEED + 11, mix=2, search=8)
+    # The oracle's row-parallel loops give the same bits with any thread
+    # count; the reference's single thread above is process-wide (one OpenMP
+    # runtime), so the oracle-only fixtures get the whole team back.
+    ref.ref_set_threads(os.cpu_count() or 8)
     if want("full", True):
         model_greedy("full_model_oracle.npz", mcpm.config_2p4b(), 32, 256, SEED + 4, use_reference=False)
     if want("c5", True):
