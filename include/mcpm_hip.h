@@ -147,6 +147,19 @@ int mcpm_apply_rope(mcpm_ctx *ctx, float *vec, int pos, int n_heads, int head_di
 int mcpm_execute_attention(mcpm_ctx *ctx, float *attn_out, const float *q, const float *k_cur,
                            const float *v_cur, float *k_cache, float *v_cache, int pos, int max_seq_len,
                            int n_heads, int n_kv_heads, int head_dim);
+/* mcpm_execute_attention with no allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * the same kernels and results, with the chunk partials in a fixed per-GPU
+ * device array (2.03 MiB, held until the process ends) instead of the
+ * context's grow-on-demand buffer.  Limit: n_heads * ceil(max_seq_len / 64) *
+ * (head_dim + 2) <= 532,480 floats (e.g. 64 heads of 128 up to 4096
+ * positions, 32 heads of 64 up to 8192); larger shapes return MCPM_ERR_ARG.
+ * Every call on one GPU shares the array, so calls that overlap on one GPU
+ * (two contexts or threads at once) race. */
+int mcpm_execute_attention_noalloc(mcpm_ctx *ctx, float *attn_out, const float *q, const float *k_cur,
+                                   const float *v_cur, float *k_cache, float *v_cache, int pos, int max_seq_len,
+                                   int n_heads, int n_kv_heads, int head_dim);
 /* get_embedding (src/ops/ops.cpp:631-673) for Q4_K and Q6_K tables. */
 int mcpm_get_embedding(mcpm_ctx *ctx, float *out, const mcpm_tensor *embd, int token);
 /* First index of the maximum of x[0..n) into *out (device int). */

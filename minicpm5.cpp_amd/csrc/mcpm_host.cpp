@@ -245,6 +245,10 @@ int mcpm_init(int device, mcpm_ctx** out) {
     mcpm_destroy(c);
     return hip_fail(e, "mcpm_init");
   }
+  if (const int rc = noalloc_setup(device)) {
+    mcpm_destroy(c);
+    return rc;
+  }
   c->rope_cap = 512;
   *out = c;
   return MCPM_OK;

@@ -40,6 +40,9 @@ int upload_tensor(mcpm_ctx* ctx, const void* host_blocks, size_t bytes, int type
 void free_tensor(DevTensor& t);
 int ensure_attn_scratch(mcpm_ctx* ctx, size_t floats);
 int ensure_argmax_scratch(mcpm_ctx* ctx, int n);
+// mcpm_noalloc.hip: the device address of its fixed scratch array on the
+// current device, looked up once per device (called by mcpm_init).
+int noalloc_setup(int device);
 // (cos, sin) of pos * theta_i, theta_i = 1/base^(2i/head_dim), i < head_dim/2
 // (src/ops/ops.cpp:503-508), evaluated with the C library's powf/cosf/sinf.
 void rope_row(int pos, int head_dim, float base, float2* out);

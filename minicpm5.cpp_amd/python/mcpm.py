@@ -101,6 +101,7 @@ _SIGS = {
     "mcpm_swiglu_and_quantize_q8k": (_I, [_P, _P, _P, _P, _I]),
     "mcpm_apply_rope": (_I, [_P, _P, _I, _I, _I, _F]),
     "mcpm_execute_attention": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    "mcpm_execute_attention_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "mcpm_get_embedding": (_I, [_P, _P, _P, _I]),
     "mcpm_argmax": (_I, [_P, _P, _I, _P]),
     "mcpm_sample_device": (_I, [_P, _P, _I, _F, _F, _F, _P]),
