@@ -243,7 +243,7 @@ def read_floor_measure(ctx, bd, pool_mb=1024, grids=(512, 1024, 2048, 4096)):
             out["classes"][name] = {"bytes": nbytes, "floor_us": round(best[0], 3), "grid": best[1],
                                     "floor_GBps": round(nbytes / (best[0] * 1e-6) / 1e9, 1),
                                     "kernel_us": round(d["avg_us"], 3),
-                                    "floor_over_kernel": round(best[0] / d["avg_us"], 4)}
+                                    "floor_over_kernel": round(best[0] / d["avg_us"], 4) if d["avg_us"] else None}
     finally:
         sink.free()
         pool.free()
@@ -380,7 +380,8 @@ def main():
     achieved = d["bytes_per_launch"] / (d["avg_us"] * 1e-6) / 1e9
     for k, v in bd.items():
         log(f"  {k:8s} {v['avg_us']:8.2f} us x {v['launches_per_token']:.0f}/token "
-            f"= {v['us_per_token']:8.1f} us/token  {v['bytes_per_launch'] / (v['avg_us'] * 1e-6) / 1e9 if v['bytes_per_launch'] else 0:7.1f} GB/s")
+            f"= {v['us_per_token']:8.1f} us/token  "
+            f"{v['bytes_per_launch'] / (v['avg_us'] * 1e-6) / 1e9 if v['bytes_per_launch'] and v['avg_us'] else 0:7.1f} GB/s")
 
     if args.copy_calibration_mb > 0:
         nbytes = args.copy_calibration_mb << 20

@@ -20,6 +20,26 @@ __device__ __forceinline__ uint16_t ld_stream_u16(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
 }
 
+// Loads and stores of data that other work groups of the same launch write
+// or read (the fused kernels): the sc1 bit makes them coherent across the
+// XCDs' L2s (written through, read from the coherence point).  The vector
+// load goes through a raw buffer resource on a wave-uniform base so that its
+// cache policy can be set; `byte_off` is the lane's offset from it.
+__device__ __forceinline__ f32x4 ld_coh4(const float* base, uint32_t byte_off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0), 0x7fffffff, 0x00020000);
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until this wave's stores are acknowledged (written through, for
+// sc1 stores): before it tells other work groups that its outputs are there.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Lane moves within rows of 16 lanes (DPP): quad_perm [1,0,3,2] (lane ^ 1),
 // quad_perm [2,3,0,1] (lane ^ 2), row rotate by 4 and by 8.
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;

@@ -96,6 +96,9 @@ struct mcpm_engine {
   bool sample_mode = false;
   void* d_sample = nullptr;
   size_t sample_cap = 0;
+  // the FFN block as one launch (gate/up, grid barrier, down)
+  bool fused_ffn = false;
+  unsigned* gsync = nullptr;  // GRID_SYNC_WORDS words
 };
 
 namespace {
@@ -142,7 +145,7 @@ void free_engine(mcpm_engine* e) {
                   static_cast<void*>(e->h), static_cast<void*>(e->logits), static_cast<void*>(e->argmax_part),
                   static_cast<void*>(e->st), static_cast<void*>(e->out_tokens), static_cast<void*>(e->kc),
                   static_cast<void*>(e->vc), static_cast<void*>(e->rope), static_cast<void*>(e->attn_part),
-                  e->d_sample})
+                  e->d_sample, static_cast<void*>(e->gsync)})
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
   free_prefill(e->pf);
@@ -257,9 +260,14 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
     rc = alloc_dev(reinterpret_cast<void**>(&e->argmax_part), e->lm_grid * sizeof(float2));
   }
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->st), sizeof(StepState));
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->gsync), GRID_SYNC_WORDS * sizeof(unsigned));
   if (rc) {
     free_engine(e);
     return rc;
+  }
+  {
+    const char* f = std::getenv("MCPM_FUSED_FFN");
+    e->fused_ffn = f && std::atoi(f) != 0;
   }
   *out = e;
   return MCPM_OK;
@@ -305,6 +313,18 @@ hipError_t timed(mcpm_engine* e, int kc, F&& launch) {
   const hipError_t err = launch();
   g_launch_timing = LaunchTiming{};
   return err;
+}
+
+// After the stream is idle: a grid barrier of a fused kernel that gave up
+// (spin limit) left its error word set; report it and reset the barrier
+// state for the next launches.
+int check_grid_sync(mcpm_engine* e) {
+  if (!e->fused_ffn) return MCPM_OK;
+  unsigned err = 0;
+  MCPM_HIP(hipMemcpy(&err, e->gsync + 8 * 64 + 64, sizeof err, hipMemcpyDeviceToHost));
+  if (!err) return MCPM_OK;
+  MCPM_HIP(hipMemset(e->gsync, 0, GRID_SYNC_WORDS * sizeof(unsigned)));
+  return fail(MCPM_ERR_HIP, "a fused kernel's grid barrier timed out; results of the call are invalid");
 }
 
 // All kernels of one token, reading token and pos from e->st.
@@ -365,28 +385,34 @@ int enqueue_token(mcpm_engine* e) {
       }
     }
     {
-      GemvArgs a{};
-      a.reg[0] = GemvRegion{view_of(L.wg), nullptr, 0, c.ffn};
-      a.reg[1] = GemvRegion{view_of(L.wu), nullptr, 0, c.ffn};
-      a.nreg = 2;
-      a.pair = 1;
-      a.total_rows = c.ffn;
-      a.nb = c.dim / QK_K;
-      a.x = e->x;
-      a.gamma = L.ffn_norm;
-      a.eps = c.eps;
-      a.h_out = e->h;
-      MCPM_HIP(timed(e, MCPM_KC_GATE_UP, [&] { return launch_gemv(a, PRO_NORM_AWAY, EPI_SWIGLU, n_cu, s); }));
-    }
-    {
-      GemvArgs a{};
-      a.reg[0] = GemvRegion{view_of(L.wd), nullptr, 0, c.dim};
-      a.nreg = 1;
-      a.total_rows = c.dim;
-      a.nb = c.ffn_pad / QK_K;
-      a.x = e->h;
-      a.resid = e->x;
-      MCPM_HIP(timed(e, MCPM_KC_DOWN, [&] { return launch_gemv(a, PRO_QUANT_AWAY, EPI_RESID, n_cu, s); }));
+      GemvArgs gu{};
+      gu.reg[0] = GemvRegion{view_of(L.wg), nullptr, 0, c.ffn};
+      gu.reg[1] = GemvRegion{view_of(L.wu), nullptr, 0, c.ffn};
+      gu.nreg = 2;
+      gu.pair = 1;
+      gu.total_rows = c.ffn;
+      gu.nb = c.dim / QK_K;
+      gu.x = e->x;
+      gu.gamma = L.ffn_norm;
+      gu.eps = c.eps;
+      gu.h_out = e->h;
+      GemvArgs dn{};
+      dn.reg[0] = GemvRegion{view_of(L.wd), nullptr, 0, c.dim};
+      dn.nreg = 1;
+      dn.total_rows = c.dim;
+      dn.nb = c.ffn_pad / QK_K;
+      dn.x = e->h;
+      dn.resid = e->x;
+      hipError_t fe = hipErrorNotSupported;
+      if (e->fused_ffn) {
+        const GridSync gs{e->gsync, e->gsync + 8 * 64, e->gsync + 8 * 64 + 64, 1u << 20};
+        fe = timed(e, MCPM_KC_GATE_UP, [&] { return launch_ffn_fused(gu, dn, n_cu, gs, s); });
+        if (fe != hipSuccess && fe != hipErrorNotSupported) MCPM_HIP(fe);
+      }
+      if (fe == hipErrorNotSupported) {
+        MCPM_HIP(timed(e, MCPM_KC_GATE_UP, [&] { return launch_gemv(gu, PRO_NORM_AWAY, EPI_SWIGLU, n_cu, s); }));
+        MCPM_HIP(timed(e, MCPM_KC_DOWN, [&] { return launch_gemv(dn, PRO_QUANT_AWAY, EPI_RESID, n_cu, s); }));
+      }
     }
   }
   {
@@ -638,6 +664,7 @@ int mcpm_engine_forward(mcpm_engine* e, int token, int pos, int max_seq_len, flo
                             e->ctx->stream));
   if (argmax) MCPM_HIP(hipMemcpyAsync(e->h_st, e->st, sizeof(StepState), hipMemcpyDeviceToHost, e->ctx->stream));
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  if (const int rc2 = check_grid_sync(e)) return rc2;
   if (argmax) *argmax = e->h_st[0].token;
   return MCPM_OK;
 }
@@ -715,7 +742,7 @@ static int generate_at(mcpm_engine* e, const int* toks, int n, int pos0, int n_g
   e->next_pos = pos0 + n + n_gen - 1;
   MCPM_HIP(hipMemcpyAsync(out_tokens, e->out_tokens, n_gen * sizeof(int), hipMemcpyDeviceToHost, e->ctx->stream));
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-  return MCPM_OK;
+  return check_grid_sync(e);
 }
 
 int mcpm_engine_generate_greedy(mcpm_engine* e, const int* prompt, int n_prompt, int n_gen, int* out_tokens) {
@@ -793,7 +820,7 @@ int mcpm_engine_tokens(mcpm_engine* e, int* out, int n) {
   if (!e || !out || n < 0 || n > e->gen_count) return fail(MCPM_ERR_ARG, "mcpm_engine_tokens: bad argument");
   MCPM_HIP(hipMemcpyAsync(out, e->out_tokens, n * sizeof(int), hipMemcpyDeviceToHost, e->ctx->stream));
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-  return MCPM_OK;
+  return check_grid_sync(e);
 }
 
 int mcpm_engine_set_kernel_timing(mcpm_engine* e, int kernel_class) {

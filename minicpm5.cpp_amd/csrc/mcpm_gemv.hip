@@ -110,8 +110,16 @@ struct ProRegs {
   float d[NR];     // Q8_K d
 };
 
-template <int PRO>
+// Coherence of a GEMV phase's accesses to data other work groups of the same
+// launch write or read (the fused kernels), a bitmask: COH_IN the
+// activations, COH_OUT the epilogue outputs.  Other data (written by earlier
+// launches, or read and written by the same lane) takes plain accesses.
+constexpr int COH_IN = 1, COH_OUT = 2;
+
+template <int PRO, int COH = 0>
 __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wave, int lane, ProRegs& X) {
+  static_assert(!((COH & COH_IN) && PRO == PRO_ATTN_EVEN), "coherent partial reads are not implemented");
+  constexpr bool cin = (COH & COH_IN) != 0;
   const int nb = a.nb, row = lane >> 4, j = lane & 15;
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
@@ -128,7 +136,10 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
       } else {
         const f32x4* xp = reinterpret_cast<const f32x4*>(a.x + b * QK_K + 16 * j);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) X.x[r][i] = xp[i];
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (cin) X.x[r][i] = ld_coh4(a.x, static_cast<uint32_t>((b * QK_K + 16 * j + 4 * i) * 4));
+          else X.x[r][i] = xp[i];
+        }
         if constexpr (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN) {
           const f32x4* gp = reinterpret_cast<const f32x4*>(a.gamma + b * QK_K + 16 * j);
 #pragma unroll
@@ -164,7 +175,10 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
     for (int g = 0; g < MAX_NB / 8; ++g) {
       if (8 * g < nb) {  // uniform
 #pragma unroll
-        for (int k = 0; k < 8; ++k) X.xp[8 * g + k] = a.x[min(8 * g + k, nb - 1) * QK_K + t];
+        for (int k = 0; k < 8; ++k) {
+          const float* xv = a.x + min(8 * g + k, nb - 1) * QK_K + t;
+          X.xp[8 * g + k] = cin ? ld_coh(xv) : *xv;
+        }
       }
     }
   }
@@ -617,30 +631,38 @@ __device__ __forceinline__ int xcd_contiguous(int b, int G) {
 // the 4 waves (pair q = lane + 64*wave + 256*k), one chain area in LDS that
 // wave 0 runs after a work-group barrier.  It gives each SIMD one step where
 // a wave-sized item would need two (the down projection: 23 blocks).
-template <int PRO, int EPI, bool TILE, int WT, bool GRP = false>
-__global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES))
-    k_gemv(const GemvArgs a, int n_items, int S, int KB) {
-  static_assert(TILE || !GRP, "GRP is a TILE shape");
-  extern __shared__ uint32_t L[];
-  const int lane = threadIdx.x & 63;
-  const int wave = sgpr(static_cast<int>(threadIdx.x >> 6));
-  const int NW = TILE ? GEMV_TILE_WAVES : static_cast<int>(blockDim.x >> 6);
-  const int nb = a.nb;
-  const LdsPlan P = lds_plan(nb, S, TILE, PRO == PRO_ATTN_EVEN, GRP ? 1 : NW);
-  const int stride = GRP ? gridDim.x : gridDim.x * NW;
-  const Region A = region_of(a.reg[0]), B = region_of(a.reg[1]), C = region_of(a.reg[2]);
+// The (item, step) sequence of one wave of a launch, with the launch's work
+// group index and count given (a kernel's own, or a fused kernel's virtual
+// ones), and the epilogue inputs its rows need.
+template <int EPI, bool TILE, int WT, bool GRP, int COH>
+struct GemvPlan {
+  const GemvArgs& a;
+  int n_items, S, KB, lane, wave, NW, nb, stride, first, n_steps, pos;
+  float invS;
+  Region A, B, C;
 
-  // This wave's steps: item first + (t / KB) * stride, step t % KB.  Steps
-  // past the last re-read the last one (cached, results unused), so every
-  // load is issued unconditionally and no wait depends on a branch.
-  const int first = GRP ? xcd_contiguous(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x))
-                        : static_cast<int>(blockIdx.x) * NW + wave;
-  const int n_mine = first < n_items ? (n_items - 1 - first) / stride + 1 : 0;
-  const int n_steps = n_mine * KB;
-  const float invS = 1.0f / static_cast<float>(S);
+  __device__ __forceinline__ GemvPlan(const GemvArgs& a_, int n_items_, int S_, int KB_, int vb, int vg)
+      : a(a_), n_items(n_items_), S(S_), KB(KB_) {
+    lane = threadIdx.x & 63;
+    wave = sgpr(static_cast<int>(threadIdx.x >> 6));
+    NW = TILE ? GEMV_TILE_WAVES : static_cast<int>(blockDim.x >> 6);
+    nb = a.nb;
+    stride = GRP ? vg : vg * NW;
+    A = region_of(a.reg[0]);
+    B = region_of(a.reg[1]);
+    C = region_of(a.reg[2]);
+    // This wave's steps: item first + (t / KB) * stride, step t % KB.  Steps
+    // past the last re-read the last one (cached, results unused), so every
+    // load is issued unconditionally and no wait depends on a branch.
+    first = GRP ? xcd_contiguous(vb, vg) : vb * NW + wave;
+    const int n_mine = first < n_items ? (n_items - 1 - first) / stride + 1 : 0;
+    n_steps = n_mine * KB;
+    invS = 1.0f / static_cast<float>(S);
+    pos = (EPI == EPI_QKV) ? a.state[1] : 0;
+  }
 
   // slot and block of this lane at step k of an item
-  auto slot_at = [&](int k, int& s, int& b) {
+  __device__ __forceinline__ void slot_at(int k, int& s, int& b) const {
     if constexpr (TILE) {
       const int q = GRP ? lane + 64 * wave + 256 * k : lane + 64 * k;
       const int bq = static_cast<int>((static_cast<float>(q) + 0.5f) * invS);  // q / S, exact for q < 2^16
@@ -650,20 +672,18 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
       s = lane;
       b = k;
     }
-  };
-  auto ref_at = [&](int t, int& b, int& s) {
+  }
+  __device__ __forceinline__ RowRef ref_at(int t, int& b, int& s) const {
     const int tt = min(t, max(n_steps - 1, 0));
     const int it = n_steps > 0 ? first + (tt / KB) * stride : 0;
     slot_at(tt % KB, s, b);
     return row_of<WT>(a, A, B, C, S, it, s);
-  };
-
+  }
   // Epilogue inputs of the row this lane finishes (ROW: its row; TILE: slot
   // `lane`), loaded with each step's weights so the epilogue reads no memory:
   // the residual (RESID) or the RoPE cos/sin (QKV).  Every step loads them,
   // at clamped indices, so no load depends on a branch.
-  const int pos = (EPI == EPI_QKV) ? a.state[1] : 0;
-  auto prefetch_epi = [&](int t, float2& e) {
+  __device__ __forceinline__ void prefetch_epi(int t, float2& e) const {
     const int tt = min(t, max(n_steps - 1, 0));
     const int it = n_steps > 0 ? first + (tt / KB) * stride : 0;
     const RowRef te = row_of<WT>(a, A, B, C, S, it, min(lane, S - 1));
@@ -673,10 +693,46 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
       const int i = te.r % a.head_dim;
       e = a.rope_cs[static_cast<size_t>(pos) * (a.head_dim / 2) + (i >> 1)];
     }
-  };
+  }
+};
+
+// A wave's first step (weights and epilogue inputs), loaded ahead: a fused
+// kernel issues it before waiting for the producer of the activations.
+template <int WT>
+struct FirstStep {
+  Blk<WT> K;
+  float2 e;
+  RowRef t;
+  int b, s;
+};
+
+template <int EPI, bool TILE, int WT, bool GRP, int COH>
+__device__ __forceinline__ void gemv_first_step(const GemvPlan<EPI, TILE, WT, GRP, COH>& pl, FirstStep<WT>& f) {
+  f.e = make_float2(0.0f, 0.0f);
+  f.t = pl.ref_at(0, f.b, f.s);
+  load_blk(f.K, f.t, min(f.b, pl.nb - 1));
+  pl.prefetch_epi(0, f.e);
+}
+
+// One GEMV launch's work for virtual work group vb of vg: the body of k_gemv,
+// and a phase of the fused kernels.  COH: the activations come from other
+// work groups of the same launch and the outputs go to them (sc1 loads and
+// stores); PRE: the first step was loaded by gemv_first_step (in `pre`).
+// Ends with the wave's last stores issued (not waited for).
+template <int PRO, int EPI, bool TILE, int WT, bool GRP = false, int COH = 0, bool PRE = false>
+__device__ __forceinline__ void gemv_core(const GemvArgs& a, int n_items, int S, int KB, int vb, int vg, uint32_t* L,
+                                          const FirstStep<WT>* pre) {
+  static_assert(TILE || !GRP, "GRP is a TILE shape");
+  const GemvPlan<EPI, TILE, WT, GRP, COH> pl(a, n_items, S, KB, vb, vg);
+  const int lane = pl.lane, wave = pl.wave, NW = pl.NW, nb = pl.nb;
+  const LdsPlan P = lds_plan(nb, S, TILE, PRO == PRO_ATTN_EVEN, GRP ? 1 : NW);
+  const int stride = pl.stride, first = pl.first, n_steps = pl.n_steps, pos = pl.pos;
+  const Region &A = pl.A, &B = pl.B, &C = pl.C;
+  auto ref_at = [&](int t, int& b, int& s) { return pl.ref_at(t, b, s); };
+  auto prefetch_epi = [&](int t, float2& e) { pl.prefetch_epi(t, e); };
 
   ProRegs X;
-  prologue_load<PRO>(a, NW, wave, lane, X);
+  prologue_load<PRO, COH>(a, NW, wave, lane, X);
   // A CU's vector loads return in issue order, so an activation load queued
   // behind weight loads (HBM) waits for them.  Every wave's activation loads
   // go first: a bare barrier (no wait for the data) before any weight load.
@@ -684,9 +740,18 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
   Blk<WT> K0, K1;
   float2 e0 = make_float2(0.0f, 0.0f), e1 = make_float2(0.0f, 0.0f);
   int b0, s0, b1, s1;
-  RowRef t0 = ref_at(0, b0, s0), t1;
-  load_blk(K0, t0, min(b0, nb - 1));  // in flight during the prologue
-  prefetch_epi(0, e0);
+  RowRef t0, t1;
+  if constexpr (PRE) {
+    K0 = pre->K;
+    e0 = pre->e;
+    t0 = pre->t;
+    b0 = pre->b;
+    s0 = pre->s;
+  } else {
+    t0 = ref_at(0, b0, s0);
+    load_blk(K0, t0, min(b0, nb - 1));  // in flight during the prologue
+    prefetch_epi(0, e0);
+  }
   prologue_compute<PRO>(a, NW, wave, lane, X, L, P);
 
   float acc[8], accm = 0.0f;
@@ -702,14 +767,18 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
     const RowRef t = row_of<WT>(a, A, B, C, S, it, min(s, S - 1));
     const bool writer = s < S && t.valid;
     const int r = t.r;
+    auto put = [](float* p, float x) {
+      if constexpr ((COH & COH_OUT) != 0) st_coh(p, x);
+      else *p = x;
+    };
     if constexpr (EPI == EPI_STORE) {
-      if (writer) t.out[r] = v;
+      if (writer) put(t.out + r, v);
     } else if constexpr (EPI == EPI_RESID) {
-      if (writer) a.resid[r] = e.x + v;
+      if (writer) put(a.resid + r, e.x + v);
     } else if constexpr (EPI == EPI_SWIGLU) {
       if (writer && s < S / 2) {
         const float silu = v / (1.0f + exp_f32(-v));
-        a.h_out[r] = silu * up;
+        put(a.h_out + r, silu * up);
       }
     } else if constexpr (EPI == EPI_QKV) {
       // adjacent-pair RoPE (src/ops/ops.cpp:502-516) on q (region 0) and k
@@ -721,15 +790,15 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
           float o;
           if ((i & 1) == 0) o = v * cs.x - partner * cs.y;
           else o = partner * cs.y + v * cs.x;
-          if (t.reg == 0) t.out[r] = o;
-          else a.k_cache[static_cast<size_t>(pos) * a.kvd + r] = o;
+          if (t.reg == 0) put(t.out + r, o);
+          else put(a.k_cache + static_cast<size_t>(pos) * a.kvd + r, o);
         } else {
-          a.v_cache[static_cast<size_t>(pos) * a.kvd + r] = v;
+          put(a.v_cache + static_cast<size_t>(pos) * a.kvd + r, v);
         }
       }
     } else if constexpr (EPI == EPI_LOGITS) {
       if (writer) {
-        t.out[r] = v;
+        put(t.out + r, v);
         if (v > best_v || (v == best_v && r < best_i)) {
           best_v = v;
           best_i = r;
@@ -879,8 +948,100 @@ __global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES)
         best_i = oi;
       }
     }
-    if (lane == 0) a.argmax_part[blockIdx.x * NW + wave] = make_float2(best_v, __int_as_float(best_i));
+    if (lane == 0) a.argmax_part[vb * NW + wave] = make_float2(best_v, __int_as_float(best_i));
   }
+}
+
+template <int PRO, int EPI, bool TILE, int WT, bool GRP = false>
+__global__ void __launch_bounds__(64 * (TILE ? GEMV_TILE_WAVES : GEMV_MAX_WAVES))
+    k_gemv(const GemvArgs a, int n_items, int S, int KB) {
+  extern __shared__ uint32_t L[];
+  gemv_core<PRO, EPI, TILE, WT, GRP>(a, n_items, S, KB, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x),
+                                     L, nullptr);
+}
+
+// --------------------------------------------------------- fused kernels ----
+// A grid barrier inside one launch whose work groups are all resident (grid
+// <= CUs, one work group per CU): eight arrival counters, one per XCD (work
+// group b runs on XCD b % 8 and arrives on counter b % 8), 256 bytes apart,
+// and a launch count `gen` that work group 0 advances after the launch's
+// last barrier (every work group has read it by then).  Barrier k of launch
+// gen waits until counter x reaches (gen*nbar + k + 1) * (work groups on XCD
+// x), compared by signed difference so that the counters may wrap.  Every
+// wait is bounded: past the spin limit, or when another work group has given
+// up, it sets the error word and returns false, and the kernel returns.
+__device__ __forceinline__ unsigned ld_coh_u(const unsigned* p) {
+  return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival: every wave's outputs acknowledged (all its memory operations
+// complete: issue no loads meant to overlap the wait before this), then one
+// arrival per work group.
+__device__ __forceinline__ void grid_arrive(const GridSync& g) {
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(g.ctr + 64 * (blockIdx.x & 7), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits for every work group's arrival at barrier k of launch gen; loads
+// issued between grid_arrive and this call overlap the wait.
+__device__ bool grid_wait(const GridSync& g, unsigned gen, int nbar, int k) {
+  __shared__ int s_ok;
+  const int G = static_cast<int>(gridDim.x);
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const unsigned round = gen * static_cast<unsigned>(nbar) + static_cast<unsigned>(k) + 1u;
+    const unsigned members = static_cast<unsigned>(G / 8 + (lane < G % 8 ? 1 : 0));
+    bool ok = true;
+    unsigned spins = 0;
+    for (;;) {
+      bool mine = true;
+      if (lane < 8) mine = static_cast<int>(ld_coh_u(g.ctr + 64 * lane) - round * members) >= 0;
+      if (__all(mine)) break;
+      if (++spins > g.spin_limit || ld_coh_u(g.err)) {
+        if (lane == 0) __hip_atomic_store(g.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = false;
+        break;
+      }
+    }
+    if (lane == 0) s_ok = ok;
+  }
+  __syncthreads();
+  return s_ok;
+}
+
+// The FFN block of one layer in one launch (src/model.cpp:195-225): gate/up
+// (RMSNorm + Q8_K prologue, SwiGLU epilogue, h written through), then the
+// down projection (Q8_K of h, residual add).  Each work group loads its first
+// down step (weights and residual) before the grid barrier, so that latency
+// overlaps the barrier instead of following it.  Both phases are TILE shapes
+// of 4 waves; virtual work group counts gu_grid and dn_grid <= the grid.
+template <int WT_DN, bool GRP_DN>
+__global__ void __launch_bounds__(64 * GEMV_TILE_WAVES)
+    k_ffn_fused(const GemvArgs gu, int gu_items, int gu_S, int gu_KB, int gu_grid, const GemvArgs dn, int dn_items,
+                int dn_S, int dn_KB, int dn_grid, GridSync gs) {
+  extern __shared__ uint32_t L[];
+  const int b = static_cast<int>(blockIdx.x);
+  __shared__ unsigned s_gen;
+  if (threadIdx.x == 0) s_gen = ld_coh_u(gs.gen);
+  // gate/up: x from the previous launch; h written through for the others
+  if (b < gu_grid)
+    gemv_core<PRO_NORM_AWAY, EPI_SWIGLU, true, WT_Q4, false, COH_OUT>(gu, gu_items, gu_S, gu_KB, b, gu_grid, L,
+                                                                      nullptr);
+  grid_arrive(gs);  // also makes s_gen visible to every wave
+  const unsigned gen = s_gen;
+  // the first down step's weights and residual, in flight during the wait
+  // (issued earlier, at the start, they slow gate/up down more than they save)
+  const GemvPlan<EPI_RESID, true, WT_DN, GRP_DN, COH_IN> pl(dn, dn_items, dn_S, dn_KB, b, dn_grid);
+  FirstStep<WT_DN> pre;
+  if (b < dn_grid) gemv_first_step(pl, pre);
+  if (!grid_wait(gs, gen, 1, 0)) return;
+  if (b == 0 && threadIdx.x == 0) __hip_atomic_fetch_add(gs.gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // down: h from the other work groups; each row's residual read and written by one lane
+  if (b < dn_grid)
+    gemv_core<PRO_QUANT_AWAY, EPI_RESID, true, WT_DN, GRP_DN, COH_IN, true>(dn, dn_items, dn_S, dn_KB, b, dn_grid,
+                                                                            L, &pre);
 }
 
 // ------------------------------------------------------------- dispatch ----
@@ -1050,6 +1211,33 @@ int gemv_grid(const GemvArgs& a0, int n_cu) {
                            : (q4 ? grid_for<P, E, false, WT_Q4>(n_items, sh, n_cu, lds)
                                  : grid_for<P, E, false, WT_Q6>(n_items, sh, n_cu, lds));
   return grid * sh.NW;
+}
+
+hipError_t launch_ffn_fused(const GemvArgs& gu0, const GemvArgs& dn0, int n_cu, const GridSync& gs, hipStream_t s) {
+  if (gu0.nb <= 0 || gu0.nb > MAX_NB || dn0.nb <= 0 || dn0.nb > MAX_NB || !gu0.pair || gu0.reg[0].w.type != MCPM_TYPE_Q4_K ||
+      gu0.reg[1].w.type != MCPM_TYPE_Q4_K || dn0.nreg != 1)
+    return hipErrorInvalidValue;
+  GemvArgs gu = gu0, dn = dn0;
+  const Shape sg = pick_shape(gu, PRO_NORM_AWAY, EPI_SWIGLU, n_cu);
+  const Shape sd = pick_shape(dn, PRO_QUANT_AWAY, EPI_RESID, n_cu);
+  if (!sg.tile || sg.grp || !sd.tile) return hipErrorNotSupported;  // the fused kernel runs TILE phases only
+  const int gi = n_items_of(gu, sg), di = n_items_of(dn, sd);
+  const int gg = (gi + GEMV_TILE_WAVES - 1) / GEMV_TILE_WAVES, dg = sd.grp ? di : (di + GEMV_TILE_WAVES - 1) / GEMV_TILE_WAVES;
+  // one work group per CU, all resident; always n_cu of them, so that every
+  // launch on the same barrier state counts the same arrivals per XCD
+  if (gg > n_cu || dg > n_cu) return hipErrorNotSupported;
+  const int grid = n_cu;
+  const size_t lds = std::max(lds_bytes(gu, sg, PRO_NORM_AWAY), lds_bytes(dn, sd, PRO_QUANT_AWAY));
+  const bool q6 = dn.reg[0].w.type == MCPM_TYPE_Q6_K;
+#define MCPM_FUSED(WT, G)                                                                                            \
+  launch_kernel(k_ffn_fused<WT, G>, dim3(grid), dim3(64 * GEMV_TILE_WAVES), lds, s, gu, gi, sg.S, sg.KB, gg, dn, di, \
+                sd.S, sd.KB, dg, gs)
+  if (q6 && sd.grp) MCPM_FUSED(WT_Q6, true);
+  else if (q6) MCPM_FUSED(WT_Q6, false);
+  else if (sd.grp) MCPM_FUSED(WT_Q4, true);
+  else MCPM_FUSED(WT_Q4, false);
+#undef MCPM_FUSED
+  return hipGetLastError();
 }
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s) {

@@ -224,6 +224,22 @@ struct StepState {
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s);
 
+// The grid barrier state of the fused kernels (device memory, zeroed at
+// allocation): ctr[64 * x] arrivals of XCD x, the launch count, and an error
+// word set when a wait passed spin_limit polls.
+struct GridSync {
+  unsigned* ctr;
+  unsigned* gen;
+  unsigned* err;
+  unsigned spin_limit;
+};
+constexpr size_t GRID_SYNC_WORDS = 8 * 64 + 64 + 64;
+// The FFN block (gate/up, then down) of one layer in one launch; gu and dn as
+// for launch_gemv's PRO_NORM_AWAY/EPI_SWIGLU and PRO_QUANT_AWAY/EPI_RESID.
+// hipErrorNotSupported when a phase's shape does not fit one resident round
+// of work groups (the caller launches the two kernels then).
+hipError_t launch_ffn_fused(const GemvArgs& gu, const GemvArgs& dn, int n_cu, const GridSync& gs, hipStream_t s);
+
 // The temperature / top-p sampler on the device (mcpm_sampler.hip): scratch
 // bytes for n logits, and its passes for one uniform draw r.  The token goes
 // to *out_token (device) when given, and when st is given it becomes the next

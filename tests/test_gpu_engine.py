@@ -306,3 +306,38 @@ def test_generate_at_reuses_cached_rows(ctx, prefill):
     for (kg, vg), (kw, vw) in zip(kv_got, kv_want):
         assert_bits(kg, kw)
         assert_bits(vg, vw)
+
+
+def test_fused_ffn_block_matches_oracle(ctx, small_image, monkeypatch):
+    """MCPM_FUSED_FFN=1: each layer's FFN block (gate/up, then down) as one
+    launch with a grid barrier between the phases, the down weights loaded
+    before the barrier.  Same tokens and bit-identical logits as the oracle,
+    on the small model and on the first 32 steps of the 2.4B-shaped model."""
+    monkeypatch.setenv("MCPM_FUSED_FFN", "1")
+    g = golden("small_model_greedy.npz")
+    announce("fused FFN: small model greedy")
+    e = mcpm.Engine(ctx, image=small_image)
+    try:
+        e.init_kv_cache(256)
+        got = e.generate_greedy(g["prompt"], len(g["tokens"]))
+        want = O.OracleModel(small_image).generate_greedy(g["prompt"], len(g["tokens"]))
+        np.testing.assert_array_equal(got, want)
+        om = O.OracleModel(small_image)
+        om.init_kv(64)
+        lg = np.empty(4000, np.float32)
+        for pos, t in enumerate(g["prompt"]):
+            logits, _ = e.forward(int(t), pos)
+            om.forward(int(t), pos, lg)
+            assert_bits(logits, lg)
+    finally:
+        e.free()
+    gf = golden("full_model_oracle.npz")
+    announce("fused FFN: 2.4B-shaped model greedy 32+32")
+    img = mcpm.synth_gguf(mcpm.config_2p4b(), seed=int(gf["seed"]), mix=0)
+    e = mcpm.Engine(ctx, image=img)
+    del img
+    try:
+        e.init_kv_cache(128)
+        np.testing.assert_array_equal(e.generate_greedy(gf["prompt"], 32), gf["tokens"][:32])
+    finally:
+        e.free()
