@@ -248,8 +248,11 @@ def test_reference_cli_runs_on_the_engine(tmp_path):
     path = str(tmp_path / "m.gguf")
     mcpm.synth_gguf(cfg, seed=5, mix=2, path=path)
     announce("reference CLI on libmcpm_model.so")
+    # the CLI seeds its sampler from std::random_device, and a sampled token of
+    # the synthetic vocabulary can be a lone byte: its output is read as bytes
     r = subprocess.run([cli, "-m", path, "--text", "Hello, world", "-n", "8", "-c", "512", "-v"],
-                       capture_output=True, text=True, timeout=300, cwd=str(tmp_path))
+                       capture_output=True, text=True, encoding="utf-8", errors="replace", timeout=300,
+                       cwd=str(tmp_path))
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     assert "tokens) direto do arquivo GGUF" in r.stdout  # the reference tokenizer read the vocabulary
     prompt_line = next(l for l in r.stdout.splitlines() if l.startswith("Prompt:"))
@@ -326,7 +329,8 @@ def test_reference_cli_runs_on_the_operators(refgeom_file, tmp_path):
     cfg, path = refgeom_file
     announce("reference CLI on libmcpm_ops.so")
     r = subprocess.run([cli, "-m", path, "--text", "Hi", "-n", "4", "-c", "256", "-v"],
-                       capture_output=True, text=True, timeout=600, cwd=str(tmp_path))
+                       capture_output=True, text=True, encoding="utf-8", errors="replace", timeout=600,
+                       cwd=str(tmp_path))
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     prompt_line = next(l for l in r.stdout.splitlines() if l.startswith("Prompt:"))
     assert int(prompt_line.split()[1]) > 10
