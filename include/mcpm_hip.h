@@ -169,7 +169,8 @@ int mcpm_argmax(mcpm_ctx *ctx, const float *x, int n, int *out);
  * the top-p cut over the (p desc, id asc) order, the walk; its running sums
  * are taken in double over blocks of 256 positions (the reference's run
  * sequentially in float; see mcpm_sampler.hip), so its choice can differ
- * from mcpm_sample_logits only for draws within rounding of a boundary. */
+ * from mcpm_sample_logits only for draws within rounding of a boundary.
+ * n up to 524,288 (larger: MCPM_ERR_ARG). */
 int mcpm_sample_device(mcpm_ctx *ctx, const float *x, int n, float temperature, float top_p, float r, int *out);
 
 /* Per-op kernel timing, a measurement aid with no counterpart in the

@@ -677,6 +677,8 @@ static int set_sample_mode(mcpm_engine* e, bool on) {
 }
 
 static int ensure_sampler(mcpm_engine* e) {
+  if (e->cfg.vocab > sampler_max_n())
+    return fail(MCPM_ERR_UNSUPPORTED, "sampled decode: vocabulary larger than the device sampler's 524,288");
   const size_t need = sampler_bytes(e->cfg.vocab);
   if (need <= e->sample_cap) return MCPM_OK;
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));

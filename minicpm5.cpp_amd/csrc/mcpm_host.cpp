@@ -614,7 +614,7 @@ int mcpm_argmax(mcpm_ctx* c, const float* x, int n, int* out) {
 }
 
 int mcpm_sample_device(mcpm_ctx* c, const float* logits, int n, float temperature, float top_p, float r, int* out) {
-  if (!c || !logits || !out || n <= 0 || !(r >= 0.0f && r < 1.0f))
+  if (!c || !logits || !out || n <= 0 || n > sampler_max_n() || !(r >= 0.0f && r < 1.0f))
     return fail(MCPM_ERR_ARG, "mcpm_sample_device: bad argument");
   const size_t need = sampler_bytes(n);
   if (need > c->sample_cap) {

@@ -245,6 +245,7 @@ hipError_t launch_ffn_fused(const GemvArgs& gu, const GemvArgs& dn, int n_cu, co
 // to *out_token (device) when given, and when st is given it becomes the next
 // input token, is appended to out_tokens and pos advances (as the argmax does).
 size_t sampler_bytes(int n);
+int sampler_max_n();  // largest n launch_sample takes
 hipError_t launch_sample(void* scratch, size_t scratch_bytes, const float* logits, int n, float temperature,
                          float top_p, float r, int* out_token, StepState* st, int* out_tokens, hipStream_t s);
 

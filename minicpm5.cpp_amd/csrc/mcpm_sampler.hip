@@ -35,6 +35,7 @@ namespace {
 
 constexpr int SMP_B = 256;
 
+
 __device__ __forceinline__ float smp_logit(const float* __restrict__ logits, int i, float inv_temp, int apply) {
   const float l = logits[i];
   return apply ? l * inv_temp : l;
@@ -135,166 +136,131 @@ __global__ void __launch_bounds__(SMP_B) k_smp_bsum(const uint32_t* __restrict__
   }
 }
 
-// One work group.  For a threshold (the cut's top_p, or the walk's r*C) the
-// first block whose end sum reaches it, then the first position of that
-// block whose running sum does; positions at or past `limit` do not count.
-// Returns (thread 0) the position, or -1 when no position below limit does;
-// `run` gets that position's running sum.  The block phase either scans the
-// block sums in order (recording each block's end sum in rec[] when rec is
-// given and the blocks fit) or, with nrec >= 0, looks the block up among the
-// end sums a previous scan recorded: the same sums, so the same block.
-constexpr int SMP_REC = 2048;  // block end sums k_smp_pick keeps (vocabularies up to 524,288)
+// One work group: the cut and the walk.  Position k's running sum is the
+// sum of the block sums before its block, added in order (P[j] = P[j-1] +
+// bs[j], double, from 0), plus its in-block running sum (double, in order,
+// from 0).  The sequential chains run on thread 0 into LDS; every search over
+// them is parallel (first index whose sum reaches the threshold).
+//   cut:  the first block j with float(P[j]) >= top_p, then the first
+//         position of it whose float(P[j-1] + in-block sum) >= top_p; the
+//         cut keeps positions up to that one, C = its running sum (no cut: C =
+//         the total).
+//   walk: t = r * C; the first block j at or before the cut's with t <= P[j],
+//         then its first position before the cut with t <= P[j-1] + in-block
+//         sum; none: the cut's last position.
+constexpr int SMP_REC = 2048;  // blocks: vocabularies up to 524,288
 
-template <bool FLOAT_CMP>
-__device__ int smp_search(const uint32_t* __restrict__ key, const float* __restrict__ p, int n, int topp,
-                          const double* __restrict__ bs, int nblk, double thr_d, float thr_f, int limit, double* sb,
-                          float* sv, int* s_int, double* s_dbl, double& run, double* rec, int nrec) {
+// the first i < count with pred(i), or -1 (every thread; a barrier at entry
+// and exit)
+template <class Pred>
+__device__ __forceinline__ int smp_first(int count, Pred pred, int* s_hit) {
   const int tid = threadIdx.x;
-  double off = 0.0;
-  int found = -1;
-  if (nrec >= 0) {
-    // first recorded block whose end sum reaches the threshold
-    int best = 0x7fffffff;
-    for (int j = tid; j < nrec; j += SMP_B) {
-      const double e = rec[j];
-      const bool hit = FLOAT_CMP ? (static_cast<float>(e) >= thr_f) : (thr_d <= e);
-      if (hit) {
-        best = j;
-        break;
-      }
-    }
-    if (tid == 0) s_int[0] = 0x7fffffff;
-    __syncthreads();
-    if (best != 0x7fffffff) atomicMin(s_int, best);
-    __syncthreads();
-    found = s_int[0] == 0x7fffffff ? -1 : s_int[0];
-    off = found > 0 ? rec[found - 1] : found == 0 ? 0.0 : rec[nrec - 1];
-    __syncthreads();
-  } else {
-    // block search over the block sums (staged through LDS), thread 0
-    const bool keep = rec && nblk <= SMP_REC;
-    for (int b0 = 0; b0 < nblk && found < 0; b0 += SMP_B) {
-      const int m = min(SMP_B, nblk - b0);
-      __syncthreads();
-      if (tid < m) sb[tid] = bs[b0 + tid];
-      __syncthreads();
-      if (tid == 0) {
-        // the sums in order, read 8 at a time ahead of their adds (the adds
-        // stay one chain: this position's sum is the previous one's plus it)
-        // (the eight adds of a batch run unconditionally, then the first hit
-        // among them is picked: past it nothing is used)
-        for (int j0 = 0; j0 < m && found < 0; j0 += 8) {
-          double c[8];
-          double acc = off;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            acc = acc + sb[min(j0 + q, m - 1)];
-            c[q] = acc;
-          }
-          const int nv = min(8, m - j0);
-          int hq = 8;
-#pragma unroll
-          for (int q = 7; q >= 0; --q) {
-            const bool hit = FLOAT_CMP ? (static_cast<float>(c[q]) >= thr_f) : (thr_d <= c[q]);
-            if (q < nv && hit) hq = q;
-          }
-          if (keep) {
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-              if (q < nv && q <= hq) rec[b0 + j0 + q] = c[q];
-          }
-          // the sum before the hit, or after the batch (selects: no indexed array)
-          const int lim = min(hq, nv);
-#pragma unroll
-          for (int q = 0; q < 8; ++q)
-            if (q < lim) off = c[q];
-          if (hq < 8) found = b0 + j0 + hq;
-        }
-        s_int[0] = found;
-      }
-      __syncthreads();
-      found = s_int[0];
-    }
-    if (tid == 0) s_dbl[0] = off;
-    __syncthreads();
-    off = s_dbl[0];
-  }
-  if (found < 0) {
-    run = off;  // the total
-    return -1;
-  }
-  // in-block running sum of block `found`
-  const int k0 = found * SMP_B;
-  const int cnt = min(SMP_B, min(n, limit) - k0);
-  if (tid < cnt) sv[tid] = smp_val(key, p, topp, k0 + tid);
   __syncthreads();
-  int pos = -1;
-  double pre = 0.0;
-  if (tid == 0) {
-    for (int j0 = 0; j0 < cnt && pos < 0; j0 += 8) {
-      double pr[8];
-      double acc = pre;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        acc = acc + static_cast<double>(sv[min(j0 + q, cnt - 1)]);
-        pr[q] = acc;
-      }
-      const int nv = min(8, cnt - j0);
-      int hq = 8;
-#pragma unroll
-      for (int q = 7; q >= 0; --q) {
-        const double c = off + pr[q];
-        const bool hit = FLOAT_CMP ? (static_cast<float>(c) >= thr_f) : (thr_d <= c);
-        if (q < nv && hit) hq = q;
-      }
-      if (hq < 8) pos = k0 + j0 + hq;
-      const int last = hq < 8 ? hq : nv - 1;  // the hit's running sum, or the batch's last
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        if (q <= last) pre = pr[q];
+  if (tid == 0) *s_hit = 0x7fffffff;
+  __syncthreads();
+  for (int i = tid; i < count; i += SMP_B) {
+    if (pred(i)) {
+      atomicMin(s_hit, i);
+      break;
     }
   }
-  run = off + pre;
-  return pos;
+  __syncthreads();
+  const int h = *s_hit;
+  return h == 0x7fffffff ? -1 : h;
+}
+
+// in-block running sums of the block at k0 (cnt values, zeros past them)
+// into pr[0..SMP_B), thread 0 in order, the values staged in sv (all threads
+// call).  The chain is straight-line: 16 values read ahead, then 16
+// dependent adds and their stores.
+__device__ __forceinline__ void smp_block_prefix(const uint32_t* __restrict__ key, const float* __restrict__ p,
+                                                 int topp, int k0, int cnt, float* sv, double* pr) {
+  const int tid = threadIdx.x;
+  __syncthreads();
+  sv[tid] = tid < cnt ? smp_val(key, p, topp, k0 + tid) : 0.0f;
+  __syncthreads();
+  if (tid == 0) {
+    double acc = 0.0;
+#pragma unroll 1
+    for (int j0 = 0; j0 < SMP_B; j0 += 16) {
+      f32x4 v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const f32x4*>(sv + j0 + 4 * q);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const double a0 = acc + static_cast<double>(v[q].x);
+        const double a1 = a0 + static_cast<double>(v[q].y);
+        const double a2 = a1 + static_cast<double>(v[q].z);
+        const double a3 = a2 + static_cast<double>(v[q].w);
+        *reinterpret_cast<double2*>(pr + j0 + 4 * q) = double2{a0, a1};
+        *reinterpret_cast<double2*>(pr + j0 + 4 * q + 2) = double2{a2, a3};
+        acc = a3;
+      }
+    }
+  }
+  __syncthreads();
 }
 
 __global__ void __launch_bounds__(SMP_B) k_smp_pick(const uint32_t* __restrict__ key, const int* __restrict__ id,
                                                     const float* __restrict__ p, int n, const double* __restrict__ bs,
                                                     int nblk, int topp, float top_p, float r, int* __restrict__ out_token,
                                                     StepState* st, int* __restrict__ out_tokens) {
-  __shared__ double sb[SMP_B];
-  __shared__ float sv[SMP_B];
-  __shared__ int s_int[2];
-  __shared__ double s_dbl[1];
-  __shared__ double rec[SMP_REC];  // block end sums of the cut's scan, for the walk's lookup
-  // the cut: first position whose running sum, rounded to float, reaches top_p
-  // (the scan records the end sums of the blocks it passes, up to the cut's)
-  int cnt = n;
-  double C = 0.0;
+  __shared__ __attribute__((aligned(16))) double P[SMP_REC];  // inclusive block prefix sums (zero-padded)
+  __shared__ __attribute__((aligned(16))) double pr[SMP_B];   // in-block running sums of one block
+  __shared__ __attribute__((aligned(16))) float sv[SMP_B];
+  __shared__ int s_hit;
+  const int tid = threadIdx.x;
+  const int nb16 = (nblk + 15) & ~15;  // <= SMP_REC (a multiple of 16)
+  for (int j = tid; j < nb16; j += SMP_B) P[j] = j < nblk ? bs[j] : 0.0;
+  __syncthreads();
+  if (tid == 0) {
+    // straight-line: 16 sums read ahead, then 16 dependent adds and stores
+    double acc = 0.0;
+#pragma unroll 1
+    for (int j0 = 0; j0 < nb16; j0 += 16) {
+      double2 v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = *reinterpret_cast<const double2*>(P + j0 + 2 * q);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const double a0 = acc + v[q].x;
+        const double a1 = a0 + v[q].y;
+        *reinterpret_cast<double2*>(P + j0 + 2 * q) = double2{a0, a1};
+        acc = a1;
+      }
+    }
+  }
+  __syncthreads();
+  int cnt = n;                // positions the walk may take
+  double C = P[nblk - 1];     // the cut's running sum (no cut: the total)
+  int pr_block = -1;          // the block whose running sums pr[] holds
   if (topp) {
-    const int k = smp_search<true>(key, p, n, topp, bs, nblk, 0.0, top_p, n, sb, sv, s_int, s_dbl, C, rec, -1);
-    if (k >= 0) cnt = k + 1;  // else: every position, C = the total
-  } else {
-    (void)smp_search<true>(key, p, n, topp, bs, nblk, 0.0, __builtin_inff(), n, sb, sv, s_int, s_dbl, C, rec, -1);
+    const int jc = smp_first(nblk, [&](int j) { return static_cast<float>(P[j]) >= top_p; }, &s_hit);
+    if (jc >= 0) {
+      const int k0 = jc * SMP_B, nb = min(SMP_B, n - k0);
+      const double off = jc > 0 ? P[jc - 1] : 0.0;
+      smp_block_prefix(key, p, topp, k0, nb, sv, pr);
+      pr_block = jc;
+      // the block's end sum reached top_p, and off + pr[nb-1] is that sum:
+      // a position is found
+      const int q = smp_first(nb, [&](int i) { return static_cast<float>(off + pr[i]) >= top_p; }, &s_hit);
+      const int qq = q >= 0 ? q : nb - 1;
+      cnt = k0 + qq + 1;
+      C = off + pr[qq];
+    }
   }
-  // thread 0 holds cnt and C; the walk's threshold to every thread (after
-  // every thread's last read of the search's broadcast slots)
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    s_int[0] = cnt;
-    s_int[1] = cnt > 0 ? (cnt - 1) / SMP_B + 1 : 0;  // blocks the cut's scan recorded: through the cut's block
-    s_dbl[0] = static_cast<double>(r) * C;
+  const double t = static_cast<double>(r) * C;
+  const int nrec = (cnt - 1) / SMP_B + 1;  // blocks through the cut's
+  const int jw = smp_first(nrec, [&](int j) { return t <= P[j]; }, &s_hit);
+  int k = -1;
+  if (jw >= 0) {
+    const int k0 = jw * SMP_B, nb = min(SMP_B, cnt - k0);
+    const double off = jw > 0 ? P[jw - 1] : 0.0;
+    if (jw != pr_block) smp_block_prefix(key, p, topp, k0, min(SMP_B, n - k0), sv, pr);
+    const int q = smp_first(nb, [&](int i) { return t <= off + pr[i]; }, &s_hit);
+    if (q >= 0) k = k0 + q;
   }
-  __syncthreads();
-  cnt = s_int[0];
-  const int nrec = nblk <= SMP_REC ? min(s_int[1], nblk) : -1;
-  const double t = s_dbl[0];
-  __syncthreads();
-  // the walk: t = r*C < C, so its block is at or before the cut's, whose end
-  // sums the scan recorded
-  double run = 0.0;
-  int k = smp_search<false>(key, p, n, topp, bs, nblk, t, 0.0f, cnt, sb, sv, s_int, s_dbl, run, rec, nrec);
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     if (k < 0) k = cnt - 1;
     const int tok = topp ? id[k] : k;
     if (out_token) *out_token = tok;
@@ -342,10 +308,11 @@ SmpLayout smp_layout(int n) {
 }  // namespace
 
 size_t sampler_bytes(int n) { return n > 0 ? smp_layout(n).end : 0; }
+int sampler_max_n() { return SMP_REC * SMP_B; }
 
 hipError_t launch_sample(void* scratch, size_t scratch_bytes, const float* logits, int n, float temperature,
                          float top_p, float r, int* out_token, StepState* st, int* out_tokens, hipStream_t s) {
-  if (n <= 0 || !logits || !scratch) return hipErrorInvalidValue;
+  if (n <= 0 || n > SMP_REC * SMP_B || !logits || !scratch) return hipErrorInvalidValue;
   const SmpLayout L = smp_layout(n);
   if (L.end > scratch_bytes) return hipErrorInvalidValue;
   const int nblk = (n + SMP_B - 1) / SMP_B;

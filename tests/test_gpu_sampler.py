@@ -49,7 +49,7 @@ def test_device_sampler_rejects_bad_arguments(ctx):
     dev = ctx.upload(np.zeros(8, np.float32))
     out = ctx.zeros(4)
     try:
-        for n, r in [(0, 0.5), (8, 1.0), (8, -0.1), (8, float("nan"))]:
+        for n, r in [(0, 0.5), (8, 1.0), (8, -0.1), (8, float("nan")), (524289, 0.5)]:
             with pytest.raises(mcpm.McpmError):
                 mcpm.check(ctx.lib.mcpm_sample_device(ctx.h, dev.ptr, n, 1.0, 0.9, r, out.ptr))
     finally:
