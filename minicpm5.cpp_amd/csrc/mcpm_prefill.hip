@@ -18,13 +18,13 @@
 //    Q6_K: the reference sums sc*q*x over lane m's bytes (q in 0..63) and
 //    subtracts 32*(sc[2m]*bsums[2m] + sc[2m+1]*bsums[2m+1]) -- sub-block m's
 //    offset, added into lane m -- then converts the int32 sum to float.
-//    Written as P + 32*(E - C): P = sum over lane m of sc*(q-32)*x (q - 32 =
-//    ql + 16*(qh - 2), ql the low 4 bits, qh the high 2: two MFMAs with
-//    |sc*ql| <= 1920 and |sc*(qh-2)| <= 256, joined by one fma; |P| < 2^24 so
-//    it is exact), E = sum over lane m of sc*x and C = sub-block m's
-//    sc*bsums pair (one MFMA each, C fed in as E's accumulator, |E - C| <
-//    2^20).  The final fp32 add rounds P + 32*(E - C) once, to nearest even,
-//    as the reference's int32 -> float conversion of the same integer does.
+//    Written as S + 16*T with q = ql + 16*qh (ql the low 4 bits, qh the high
+//    2): S = sum over lane m of sc*ql*x (|sc*ql| <= 1920, |S| < 2^23), T =
+//    sum over lane m of sc*qh*x - 2*C (|sc*qh| <= 384), C = sub-block m's
+//    sc*bsums pair, fed in as T's accumulator from one more MFMA (|T| <
+//    2^22).  Three MFMAs, all exact; fma(16, T, S) rounds S + 16*T once, to
+//    nearest even, as the reference's int32 -> float conversion of the same
+//    integer does.
 //  * Q4_K's min sum (sum over sub-blocks of mn * pair-sum of bsums) is one
 //    more MFMA: A = mn[k/2] for k < 16, B = bsums[k].
 // Attention per token is the decode kernel at that token's position.
@@ -129,6 +129,18 @@ __device__ __forceinline__ h8 a_operand(uint32_t ta, uint32_t tb, h2 sa, h2 sb, 
   return __builtin_bit_cast(h8, r);
 }
 
+// The same with non-negative scales below 64: (1024 + byte) * s - 1024 * s in
+// one packed fma (ma = -1024 * sa, exact in fp16 for sa <= 63), whose single
+// rounding meets the exact product byte * s (<= 945 for Q4_K).
+__device__ __forceinline__ h2 byte_pair_fma(uint32_t t, uint32_t sel, h2 s, h2 ms) {
+  return __builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t, sel)), s, ms);
+}
+__device__ __forceinline__ h8 a_operand_fma(uint32_t ta, uint32_t tb, h2 sa, h2 sb, h2 ma, h2 mb) {
+  const u32x4 r{h2bits(byte_pair_fma(ta, SEL01, sa, ma)), h2bits(byte_pair_fma(ta, SEL23, sa, ma)),
+                h2bits(byte_pair_fma(tb, SEL01, sb, mb)), h2bits(byte_pair_fma(tb, SEL23, sb, mb))};
+  return __builtin_bit_cast(h8, r);
+}
+
 __device__ __forceinline__ h2 splat_h(int v) {
   const _Float16 h = static_cast<_Float16>(static_cast<float>(v));
   return h2{h, h};
@@ -155,7 +167,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int n_rt = (a.rows + 15) >> 4;
   const int n_rg = (n_rt + 3) >> 2;
-  const int rg = static_cast<int>(blockIdx.x) % n_rg, tg = static_cast<int>(blockIdx.x) / n_rg;
+  // XCD-aware tiles: work group b runs on XCD b % 8, which takes the row
+  // groups rg = xcd + 8j only, for every token tile, so each XCD's L2 keeps
+  // one eighth of the matrix for the whole launch.  Work groups past the row
+  // groups of their XCD have nothing to do.
+  const int xcd = static_cast<int>(blockIdx.x) & 7, loc = static_cast<int>(blockIdx.x) >> 3;
+  const int cmax = (n_rg + 7) >> 3;
+  const int rg = xcd + 8 * (loc % cmax), tg = loc / cmax;
+  if (rg >= n_rg) return;  // uniform in the work group, before any barrier
   const int r0 = (4 * rg + wave) * 16, t0 = tg * TOK;
   const bool live = r0 < a.rows;  // uniform in the wave: a wave past the rows only stages
   const size_t rows = static_cast<size_t>(a.rows);
@@ -179,11 +198,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       pbs = *reinterpret_cast<const u32x4*>(a.xbs + (static_cast<size_t>(min(t0 + tid / 2, a.n_tok - 1)) * a.nb + b) * 16 +
                                             (tid & 1) * 8);
   };
+  // sB keeps each token's 256 codes as 32 quads of 8 halves, quad 8g + m =
+  // elements 64g + 4m .. +3 and 64g + 32 + 4m .. +3 (the B operand of lane
+  // group m for the lanes of K-half g): piece k = p % 32 (elements 8k ..
+  // 8k+7, g = k/8, h = (k/4)%2, m = 2*(k%4)) goes to half h of quads m, m+1.
   auto stash = [&](int buf) {
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       const int p = tid + 256 * k;
-      *reinterpret_cast<u32x4*>(&sB[buf][(p / 32) * BROW + (p % 32) * 8]) = pf[k];
+      const int pk = p % 32, gq = pk >> 3, hq = (pk >> 2) & 1, mq = 2 * (pk & 3);
+      _Float16* row = &sB[buf][(p / 32) * BROW + (8 * gq + mq) * 8 + 4 * hq];
+      *reinterpret_cast<uint2*>(row) = uint2{pf[k].x, pf[k].y};
+      *reinterpret_cast<uint2*>(row + 8) = uint2{pf[k].z, pf[k].w};
     }
     if (tid < TOK) sXd[buf][tid] = pxd;
     if (tid < 2 * TOK) *reinterpret_cast<u32x4*>(&sBs[buf][(tid / 2) * 16 + (tid & 1) * 8]) = pbs;
@@ -203,7 +229,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
     }
   }
   const h2 off1024{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-  const h2 off1026{static_cast<_Float16>(1026.0f), static_cast<_Float16>(1026.0f)};
   const f32x4 zero4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // The weight bytes a block's A operands and row scales are built from,
@@ -243,11 +268,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         w.q[4 + cc] = *reinterpret_cast<const u32x4*>(qh + static_cast<size_t>(2 * h + cc) * rows * 16);
     }
   };
-  WRaw wc;
-  load_w(wc, 0);
-  WRaw wn = wc;
-
-  for (int b = 0; b < a.nb; ++b) {
+  // One block: the weight bytes of block b+1 (into nxt) and its activations
+  // are loaded while block b's MFMAs run; cur and nxt trade places each
+  // block, so no copy waits for loads in flight.
+  auto block = [&](int b, const WRaw& wc, WRaw& wn) {
     const int buf = b & 1;
     if (b + 1 < a.nb) {  // in flight during this block's MFMAs
       fetch(b + 1);
@@ -266,10 +290,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         dmw[i] = 0.0f;
       }
     }
-    // A operands of the eight lane groups (and Q4_K's min operand)
-    h8 A[8], AH[8], AM;
-    uint32_t acw[8];  // Q6_K: the offset operand's one nonzero dword per lane group
-    h2 sc[4];         // Q6_K: scales 4g .. 4g+3 of this lane's row, as fp16 pairs
+    // Lane groups in order; each one's A operand is built from the weight
+    // bytes just before its MFMAs (one per token tile, the operand then
+    // dropped), so the build of the next overlaps them.
+    float ds[NT][4], xdv[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      xdv[n] = sXd[buf][16 * n + c16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ds[n][i] = xdv[n] * dw[i];
+    }
+    // the B operand of lane group m for token tile n is quad 8g + m of the
+    // token's row
+    auto bq = [&](int n, int m) {
+      return __builtin_bit_cast(h8, reinterpret_cast<const u32x4*>(&sB[buf][(16 * n + c16) * BROW])[8 * g + m]);
+    };
     if constexpr (WT == 0) {
       const uint32_t s0 = wc.hdr.y, s1 = wc.hdr.z, s2 = wc.hdr.w;
       const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
@@ -278,34 +313,51 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
       const uint32_t sw = g < 2 ? sc_lo : sc_hi;
       const int sh = 16 * (g & 1);
-      const h2 sa = splat_h(static_cast<int>((sw >> sh) & 0xffu));        // sc[2g]
-      const h2 sb = splat_h(static_cast<int>((sw >> (sh + 8)) & 0xffu));  // sc[2g+1]
+      const int ia = static_cast<int>((sw >> sh) & 0xffu), ib = static_cast<int>((sw >> (sh + 8)) & 0xffu);
+      const h2 sa = splat_h(ia), sb = splat_h(ib);                  // sc[2g], sc[2g+1]
+      const h2 ma = splat_h(-1024 * ia), mb = splat_h(-1024 * ib);  // exact: sc <= 63
       const u32x4 q0 = wc.q[0], q1 = wc.q[1];
       const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      // two lane groups at a time: their 2*NT MFMAs are independent and
+      // issue back to back before the first chain step reads a result
 #pragma unroll
-      for (int m = 0; m < 8; ++m)
-        A[m] = a_operand(qw[m] & 0x0f0f0f0fu, (qw[m] >> 4) & 0x0f0f0f0fu, sa, sb, off1024);
+      for (int m = 0; m < 8; m += 2) {
+        const h8 A0 = a_operand_fma(qw[m] & 0x0f0f0f0fu, (qw[m] >> 4) & 0x0f0f0f0fu, sa, sb, ma, mb);
+        const h8 A1 = a_operand_fma(qw[m + 1] & 0x0f0f0f0fu, (qw[m + 1] >> 4) & 0x0f0f0f0fu, sa, sb, ma, mb);
+        f32x4 D0[NT], D1[NT];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          D0[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, bq(n, m), zero4, 0, 0, 0);
+          D1[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, bq(n, m + 1), zero4, 0, 0, 0);
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[n][m][i] = __builtin_fmaf(ds[n][i], D0[n][i], acc[n][m][i]);
+            acc[n][m + 1][i] = __builtin_fmaf(ds[n][i], D1[n][i], acc[n][m + 1][i]);
+          }
+        }
+      }
       // min operand: k = 8g + j < 16 -> mn[k/2]
       const uint32_t mw = (g & 1) ? mn_hi : mn_lo;
       const u32x4 mr{h2bits(byte_pair_h(mw, 0x04000400u, off1024)), h2bits(byte_pair_h(mw, 0x04010401u, off1024)),
                      h2bits(byte_pair_h(mw, 0x04020402u, off1024)), h2bits(byte_pair_h(mw, 0x04030403u, off1024))};
-      AM = g < 2 ? __builtin_bit_cast(h8, mr) : h8{};
+      const h8 AM = g < 2 ? __builtin_bit_cast(h8, mr) : h8{};
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const h8 BM = *reinterpret_cast<const h8*>(&sBs[buf][(16 * n + c16) * 16 + 8 * (g & 1)]);
+        const f32x4 DM = __builtin_amdgcn_mfma_f32_16x16x32_f16(AM, BM, zero4, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) accm[n][i] = __builtin_fmaf(-(xdv[n] * dmw[i]), DM[i], accm[n][i]);
+      }
     } else {
       const int nib = 4 * (g & 1);
       const u32x4 scr = wc.hdr;
       // scales 4g .. 4g+3 (signed bytes) = dword g of the 16 scales
       const uint32_t scw = g == 0 ? scr.x : g == 1 ? scr.y : g == 2 ? scr.z : scr.w;
-      // the offset operand: K entries 0, 1 (lanes 0..15, halves 0, 1) are
-      // -sc[2m], -sc[2m+1] of this lane's row, the rest zero
       const uint32_t scall[4] = {scr.x, scr.y, scr.z, scr.w};
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const uint32_t w2 = scall[m >> 1];
-        const int lo = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1), 8);
-        const int hi = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1) + 8, 8);
-        const h2 pair{static_cast<_Float16>(static_cast<float>(-lo)), static_cast<_Float16>(static_cast<float>(-hi))};
-        acw[m] = g == 0 ? h2bits(pair) : 0u;
-      }
+      h2 sc[4];  // scales 4g .. 4g+3 of this lane's row, as fp16 pairs
 #pragma unroll
       for (int k = 0; k < 4; ++k) sc[k] = splat_h(__builtin_amdgcn_sbfe(static_cast<int>(scw), 8 * k, 8));
       uint32_t lw[16], hw[8];
@@ -325,68 +377,62 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         hw[4 * cc + 2] = v.z;
         hw[4 * cc + 3] = v.w;
       }
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
+      // one lane group's operands; two lane groups' MFMAs are issued before
+      // either chain reads a result
+      auto q6_ops = [&](int m, h8& Al, h8& Ah, h8& AC) {
         const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)];
-        A[m] = a_operand((lw[m] >> nib) & 0x0f0f0f0fu, (lw[8 + m] >> nib) & 0x0f0f0f0fu, sa, sb, off1024);
-        AH[m] = a_operand((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, off1026);
-      }
-    }
-
+        Al = a_operand((lw[m] >> nib) & 0x0f0f0f0fu, (lw[8 + m] >> nib) & 0x0f0f0f0fu, sa, sb, off1024);
+        Ah = a_operand((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, off1024);
+        // the offset operand: K entries 0, 1 (lanes 0..15, halves 0, 1) are
+        // -2*sc[2m], -2*sc[2m+1] of this lane's row, the rest zero
+        const uint32_t w2 = scall[m >> 1];
+        const int lo = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1), 8);
+        const int hi = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1) + 8, 8);
+        const h2 pair{static_cast<_Float16>(static_cast<float>(-2 * lo)),
+                      static_cast<_Float16>(static_cast<float>(-2 * hi))};
+        AC = __builtin_bit_cast(h8, u32x4{g == 0 ? h2bits(pair) : 0u, 0u, 0u, 0u});
+      };
+      // S + 16*T for lane group m and token tile n: S = sc*ql*x, T = sc*qh*x - 2C
+      auto q6_mfma = [&](int m, int n, const h8& Al, const h8& Ah, const h8& AC, f32x4& S, f32x4& T) {
+        const h8 B = bq(n, m);
+        // bsums 2m, 2m+1 of the token as an fp16 pair (lanes 0..15 use them)
+        const uint32_t bsw = reinterpret_cast<const uint32_t*>(&sBs[buf][(16 * n + c16) * 16])[m];
+        const h8 BC = __builtin_bit_cast(h8, u32x4{g == 0 ? bsw : 0u, 0u, 0u, 0u});
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B, zero4, 0, 0, 0);
+        const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC, BC, zero4, 0, 0, 0);  // -2C
+        T = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, B, NC, 0, 0, 0);
+      };
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      const int lt = 16 * n + c16;  // the lane's token column in the tile
-      const uint32_t* xp = reinterpret_cast<const uint32_t*>(&sB[buf][lt * BROW + 64 * g]);
-      const float xdv = sXd[buf][lt];
-      uint32_t bsw[8];  // Q6_K: bsums of the token's block as fp16 pairs (lanes 0..15 use them)
-      if constexpr (WT == 1) {
-        const u32x4* bp = reinterpret_cast<const u32x4*>(&sBs[buf][lt * 16]);
-        const u32x4 b0 = bp[0], b1 = bp[1];
-        bsw[0] = b0.x;
-        bsw[1] = b0.y;
-        bsw[2] = b0.z;
-        bsw[3] = b0.w;
-        bsw[4] = b1.x;
-        bsw[5] = b1.y;
-        bsw[6] = b1.z;
-        bsw[7] = b1.w;
-      }
-      float ds[4];
+      for (int m = 0; m < 8; m += 2) {
+        h8 Al0, Ah0, AC0, Al1, Ah1, AC1;
+        q6_ops(m, Al0, Ah0, AC0);
+        q6_ops(m + 1, Al1, Ah1, AC1);
+        f32x4 S0[NT], T0[NT], S1[NT], T1[NT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ds[i] = xdv * dw[i];
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        // dwords 2m, 2m+1 (low K-half) and 16+2m, 17+2m (high) of the lane's 32
-        const uint2 xl = *reinterpret_cast<const uint2*>(xp + 2 * m);
-        const uint2 xh = *reinterpret_cast<const uint2*>(xp + 16 + 2 * m);
-        const h8 B = __builtin_bit_cast(h8, u32x4{xl.x, xl.y, xh.x, xh.y});
-        f32x4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[m], B, zero4, 0, 0, 0);
-        if constexpr (WT == 1) {
-          const f32x4 DH = __builtin_amdgcn_mfma_f32_16x16x32_f16(AH[m], B, zero4, 0, 0, 0);
-          const h8 AC = __builtin_bit_cast(h8, u32x4{acw[m], 0u, 0u, 0u});
-          const h8 BC = __builtin_bit_cast(h8, u32x4{g == 0 ? bsw[m] : 0u, 0u, 0u, 0u});
-          const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)];
-          const h8 AS = __builtin_bit_cast(h8, u32x4{h2bits(sa), h2bits(sa), h2bits(sb), h2bits(sb)});
-          const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC, BC, zero4, 0, 0, 0);  // -C
-          const f32x4 EC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AS, B, NC, 0, 0, 0);      // E - C
-#pragma unroll
-          for (int i = 0; i < 4; ++i) D[i] = __builtin_fmaf(32.0f, EC[i], __builtin_fmaf(16.0f, DH[i], D[i]));
+        for (int n = 0; n < NT; ++n) {
+          q6_mfma(m, n, Al0, Ah0, AC0, S0[n], T0[n]);
+          q6_mfma(m + 1, n, Al1, Ah1, AC1, S1[n], T1[n]);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[n][m][i] = __builtin_fmaf(ds[i], D[i], acc[n][m][i]);
-      }
-      if constexpr (WT == 0) {
-        const h8 BM = *reinterpret_cast<const h8*>(&sBs[buf][lt * 16 + 8 * (g & 1)]);
-        const f32x4 DM = __builtin_amdgcn_mfma_f32_16x16x32_f16(AM, BM, zero4, 0, 0, 0);
+        for (int n = 0; n < NT; ++n) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) accm[n][i] = __builtin_fmaf(-(xdv * dmw[i]), DM[i], accm[n][i]);
+          for (int i = 0; i < 4; ++i) {
+            acc[n][m][i] = __builtin_fmaf(ds[n][i], __builtin_fmaf(16.0f, T0[n][i], S0[n][i]), acc[n][m][i]);
+            acc[n][m + 1][i] = __builtin_fmaf(ds[n][i], __builtin_fmaf(16.0f, T1[n][i], S1[n][i]), acc[n][m + 1][i]);
+          }
+        }
       }
     }
     }  // live
     // block b+1 into the other buffer, whose last readers passed the previous barrier
     if (b + 1 < a.nb) stash(buf ^ 1);
     __syncthreads();
-    wc = wn;
+  };
+  WRaw w0, w1;
+  load_w(w0, 0);
+  for (int b = 0; b < a.nb; b += 2) {
+    block(b, w0, w1);
+    if (b + 1 < a.nb) block(b + 1, w1, w0);
   }
 
 #pragma unroll
@@ -531,7 +577,8 @@ hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const Qu
   const int NT = nt_e == 1 || nt_e == 2 || nt_e == 4 ? nt_e : (q4 ? 2 : 1);
   const int OCC = occ_e == 1 ? 1 : 2;
   // one work group per 64 rows (four 16-row tiles) x 16*NT tokens
-  const int n_groups = ((rows + 63) / 64) * ((n_tok + 16 * NT - 1) / (16 * NT));
+  // 8 XCDs x (row groups per XCD) x token tiles (see k_gemm_q8k)
+  const int n_groups = 8 * (((rows + 63) / 64 + 7) / 8) * ((n_tok + 16 * NT - 1) / (16 * NT));
   const dim3 grid(n_groups);
 #define MCPM_GEMM(N, O) \
   if (NT == N && OCC == O) { \
