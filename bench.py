@@ -45,6 +45,69 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# Decode kernels of this workload by class (the shapes the launch picker
+# chooses for the 2.4B-shaped model; names as rocprofv3 prints them).
+PROFILE_CLASSES = {
+    "qkv": "k_gemv<3, 1, true, 2, false>",
+    "attn": "k_attention<64>",
+    "oproj": "k_gemv<5, 2, true, 0, false>",
+    "gate_up": "k_gemv<3, 3, true, 0, false>",
+    "down": "k_gemv<2, 2, true, 1, true>",
+    "lm_head": "k_gemv<4, 4, false, 1, false>",
+}
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
+def summarize_profiles(stats_csv, fetch_csv, write_csv, calib_bytes, out_path):
+    """Per-class figures from three rocprofv3 runs of `bench.py --eager`: the
+    kernel-trace statistics (average launch duration) and the FETCH_SIZE and
+    WRITE_SIZE counters (KiB per dispatch, averaged over a class's
+    dispatches), the counters scaled by what they read for the run's device
+    copies of calib_bytes (the largest copy dispatch)."""
+    import csv
+
+    def short(name):
+        name = name.split("(")[0].replace("void ", "").replace("mcpm::", "")
+        return name.strip()
+
+    stats = {short(r["Name"]): r for r in csv.DictReader(open(stats_csv))}
+
+    def counter(path, cname):
+        per, calib = {}, 0.0
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != cname:
+                continue
+            k, v = short(r["Kernel_Name"]), float(r["Counter_Value"])
+            if k == COPY_KERNEL:
+                calib = max(calib, v)
+            per.setdefault(k, []).append(v)
+        return {k: sum(v) / len(v) for k, v in per.items()}, {k: len(v) for k, v in per.items()}, calib
+
+    fetch, nf, cf = counter(fetch_csv, "FETCH_SIZE")
+    write, _, cw = counter(write_csv, "WRITE_SIZE")
+    ff = calib_bytes / (cf * 1024) if cf else None
+    fw = calib_bytes / (cw * 1024) if cw else None
+    classes = {}
+    for cls, kern in PROFILE_CLASSES.items():
+        e = {"kernel": kern}
+        if kern in stats:
+            e["kernel_calls"] = int(stats[kern]["Calls"])
+            e["kernel_avg_us"] = round(float(stats[kern]["AverageNs"]) / 1000.0, 3)
+        if kern in fetch and ff:
+            e.update(dispatches=nf[kern], fetch_kib=round(fetch[kern], 1), write_kib=round(write.get(kern, 0.0), 1),
+                     fetch_bytes=int(fetch[kern] * 1024 * ff), write_bytes=int(write.get(kern, 0.0) * 1024 * (fw or 1.0)))
+        classes[cls] = e
+    out = {"workload": "greedy decode, 2.4B-shaped Q4_K_M decoder, eager launches",
+           "kernel_stats": os.path.basename(stats_csv),
+           "copy_calibration": {"bytes": calib_bytes, "fetch_kib": cf, "write_kib": cw,
+                                "fetch_factor": round(ff, 5) if ff else None, "write_factor": round(fw, 5) if fw else None},
+           "classes": classes}
+    with open(out_path, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    return out
+
+
 def kernel_breakdown(eng, n_tokens=8):
     """Per-class average launch duration (HIP events on the engine stream)."""
     out = {}
@@ -339,7 +402,13 @@ def main():
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run device-to-device copies of this many MB (the reference kernel of known "
                          "size for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--summarize-profiles", nargs=3, metavar=("STATS_CSV", "FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/decode_2p4b_traffic.json from rocprofv3 outputs and exit (no GPU)")
     args = ap.parse_args()
+    if args.summarize_profiles:
+        out = summarize_profiles(*args.summarize_profiles, (args.copy_calibration_mb or 256) << 20, TRAFFIC_FILE)
+        print(json.dumps(out["classes"]))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(batch-1 decode of one model runs on one GPU)", file=sys.stderr)
@@ -422,12 +491,18 @@ def main():
             + f"; GEMVs {rf['gemv_us_per_token']:.0f} us/token, floor {rf['floor_us_per_token']:.0f} us/token "
             f"({100 * rf['floor_over_gemv_per_token']:.0f} %)")
 
-    traffic = None
+    traffic, prof = None, None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f).get("classes", {}).get(dom)
-        if tr:
+        if tr and "fetch_bytes" in tr:
             traffic = int(tr["fetch_bytes"] + tr["write_bytes"])
+        if tr and tr.get("kernel_avg_us"):
+            # the same class's launches timed by rocprofv3 (eager run, the
+            # committed kernel statistics) beside this run's HIP events
+            pa = d["bytes_per_launch"] / (tr["kernel_avg_us"] * 1e-6) / 1e9
+            prof = {"source": "profiles/decode_2p4b_kernel_stats.md", "avg_launch_us": tr["kernel_avg_us"],
+                    "achieved": round(pa, 1), "frac": round(pa / HBM_PEAK_GBPS, 4)}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -457,7 +532,8 @@ def main():
                    "kernels_us_per_token": {k: round(v["us_per_token"], 2) for k, v in bd.items()}},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 3)},
+                     "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 3),
+                     "rocprof": prof},
         "cpu_baseline": cpu,
         "prefill": prefill,
         "sampled_decode": sampled,
