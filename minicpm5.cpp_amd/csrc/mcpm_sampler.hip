@@ -16,6 +16,14 @@
 //   k_smp_max   scaled logits, the block's max
 //   k_smp_exp   e = exp(v - max) (max over the block maxima), the block's
 //               double sum of e in order
+// then, with a top-p cut up to 0.998 (every running sum up to the cut is
+// exact, so no order of addition matters; see k_smp_prob_hist):
+//   k_smp_prob_hist  p, sort keys ~bits(p) and each key bucket's mass
+//   k_smp_seg        bucket masses as prefix sums per segment of 256
+//   k_smp_gather<0>, k_smp_resolve<0>  the cut's bucket, then the cut within it
+//   k_smp_gather<1>, k_smp_resolve<1>  the draw's bucket, then the draw;
+//                    writes the token and advances the step state
+// otherwise:
 //   k_smp_prob  s = float(sum of the block sums in order), p = e / s; with a
 //               top-p cut the sort keys ~bits(p) (ascending = p descending)
 //   (radix sort of (key, id) pairs, stable: equal p keep ascending ids)
@@ -273,10 +281,348 @@ __global__ void __launch_bounds__(SMP_B) k_smp_pick(const uint32_t* __restrict__
   }
 }
 
-// Scratch layout: e, p, key, key2, id, id2 (n each), pmax (nblk floats), bs
-// (nblk doubles), the sort's scratch; every piece on a 256-byte boundary.
+// ---------------------------------------------- top-p without the sort ----
+// When every p up to the cut is a multiple of 2^-52 (p >= 2^-29 or 0), every
+// running sum of the sampler is exact in double (all partial sums are below
+// 2 and multiples of 2^-52), so the blocked sums equal the exact sums of the
+// largest p in (p desc, id asc) order, whatever order they are added in.
+// Elements below 2^-29 hold at most n * 2^-29 <= 2^-10 of the mass for n <=
+// 524,288, so with top_p <= 0.998 (sum of p within 2^-23 of 1) the cut is
+// reached before any of them.  Then the cut and the draw's position need no
+// sort: masses as integers in units of 2^-52 (exact), summed per bucket of
+// the sort key's top 16 bits, locate the buckets of the cut and the draw; a
+// descent over the 8-bit digits of (key, id) within the gathered buckets
+// finds the element at which the exact running sum first passes each test.
+constexpr float SMP_HIST_TOPP = 0.998f;
+constexpr int SMP_NBKT = 65536;  // buckets: key >> 16
+constexpr int SMP_HCOPY = 8;     // copies of the bucket masses (one per XCD of the adding work group)
+constexpr int SMP_HWG = 1024;    // elements per work group of the histogram pass (256 per wave)
+constexpr int SMP_WTAB = 512;    // LDS hash slots per wave (> 256: never full)
+constexpr uint32_t SMP_EMPTY = 0xffffffffu;
+
+struct SmpMeta {
+  unsigned int count;          // gathered elements
+  unsigned int pad;
+  unsigned long long base;     // mass of the buckets before the gathered one
+  unsigned long long c_mass;   // the cut's running sum (units of 2^-52)
+  uint2 cut;                   // the cut's element (key, id)
+};
+
+// p in units of 2^-52 (exact for p >= 2^-29; smaller ones truncated, they
+// come after the cut)
+__device__ __forceinline__ unsigned long long smp_fixed(float p) {
+  const uint32_t b = __float_as_uint(p);
+  const int ex = static_cast<int>((b >> 23) & 0xffu);
+  if (ex == 0) return 0ull;
+  const unsigned long long m = (b & 0x7fffffu) | 0x800000u;
+  const int sh = min(ex - 98, 40);  // p * 2^52 = m * 2^(ex - 150 + 52)
+  return sh >= 0 ? (m << sh) : (sh > -32 ? (m >> -sh) : 0ull);
+}
+__device__ __forceinline__ double smp_mass(unsigned long long m) { return static_cast<double>(m) * 0x1p-52; }
+
+// p = e / s and its sort key (as k_smp_prob), and the masses summed per
+// bucket: first in an LDS hash per wave, then one global atomic per bucket
+// and wave, into the copy of the work group's XCD.
+__global__ void __launch_bounds__(SMP_B) k_smp_prob_hist(const float* __restrict__ e, int n,
+                                                         const double* __restrict__ bs, int nblk,
+                                                         uint32_t* __restrict__ key, unsigned long long* __restrict__ hm) {
+  __shared__ double sb[SMP_B];
+  __shared__ float s_sum;
+  __shared__ uint32_t tk[4][SMP_WTAB];
+  __shared__ unsigned long long tm[4][SMP_WTAB];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const double t = smp_total(bs, nblk, sb);
+  if (tid == 0) s_sum = static_cast<float>(t);
+  for (int i = lane; i < SMP_WTAB; i += 64) {
+    tk[wave][i] = SMP_EMPTY;
+    tm[wave][i] = 0ull;
+  }
+  __syncthreads();
+  const float sv = s_sum;
+  uint32_t* wk = tk[wave];
+  unsigned long long* wm = tm[wave];
+#pragma unroll
+  for (int k = 0; k < SMP_HWG / SMP_B; ++k) {
+    // the wave takes 64 consecutive elements per round
+    const int i = static_cast<int>(blockIdx.x) * SMP_HWG + wave * (SMP_HWG / 4) + k * 64 + lane;
+    if (i < n) {
+      const float pv = e[i] / sv;
+      const uint32_t kv = ~__float_as_uint(pv);
+      key[i] = kv;
+      const uint32_t bk = kv >> 16;
+      uint32_t h = (bk * 2654435761u) >> 23;  // 9 bits
+      for (;;) {
+        const uint32_t prev = atomicCAS(&wk[h], SMP_EMPTY, bk);
+        if (prev == SMP_EMPTY || prev == bk) break;
+        h = (h + 1) & (SMP_WTAB - 1);
+      }
+      atomicAdd(&wm[h], smp_fixed(pv));
+    }
+  }
+  __syncthreads();
+  unsigned long long* hc = hm + static_cast<size_t>(blockIdx.x & (SMP_HCOPY - 1)) * SMP_NBKT;
+  for (int i = lane; i < SMP_WTAB; i += 64)
+    if (wk[i] != SMP_EMPTY && wm[i] != 0ull) atomicAdd(&hc[wk[i]], wm[i]);
+}
+
+// Block inclusive scan of one value per thread (256 threads), in LDS.
+__device__ __forceinline__ unsigned long long smp_scan256(unsigned long long v, unsigned long long* sc) {
+  const int tid = threadIdx.x;
+  sc[tid] = v;
+  __syncthreads();
+#pragma unroll
+  for (int d = 1; d < SMP_B; d <<= 1) {
+    const unsigned long long a = tid >= d ? sc[tid - d] : 0ull;
+    __syncthreads();
+    sc[tid] += a;
+    __syncthreads();
+  }
+  return sc[tid];
+}
+
+// Work group g of 256: the masses of buckets 256g .. 256g+255 (summed over
+// the copies) as prefix sums within the segment (pfx) and the segment's
+// total (seg); the copies are cleared for the next call.
+__global__ void __launch_bounds__(SMP_B) k_smp_seg(unsigned long long* __restrict__ hm,
+                                                   unsigned long long* __restrict__ pfx,
+                                                   unsigned long long* __restrict__ seg) {
+  __shared__ unsigned long long sc[SMP_B];
+  const int b = static_cast<int>(blockIdx.x) * SMP_B + threadIdx.x;
+  unsigned long long v = 0ull;
+#pragma unroll
+  for (int c = 0; c < SMP_HCOPY; ++c) {
+    unsigned long long* p = hm + static_cast<size_t>(c) * SMP_NBKT + b;
+    v += *p;
+    *p = 0ull;
+  }
+  const unsigned long long cs = smp_scan256(v, sc);
+  pfx[b] = cs;
+  if (threadIdx.x == SMP_B - 1) seg[blockIdx.x] = cs;
+}
+
+// The first bucket whose cumulative mass M passes test(M) (every thread;
+// barriers inside); *before gets the mass of the buckets before it.  -1 when
+// none does.
+template <class Test>
+__device__ __forceinline__ int smp_bucket(const unsigned long long* __restrict__ pfx,
+                                          const unsigned long long* segc, Test test, unsigned long long* before,
+                                          int* s_hit) {
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if (tid == 0) *s_hit = 0x7fffffff;
+  __syncthreads();
+  if (test(segc[tid])) atomicMin(s_hit, tid);
+  __syncthreads();
+  const int sg = *s_hit;
+  if (sg == 0x7fffffff) return -1;
+  const unsigned long long off = sg > 0 ? segc[sg - 1] : 0ull;
+  const unsigned long long v = pfx[sg * SMP_B + tid];
+  __syncthreads();
+  if (tid == 0) *s_hit = 0x7fffffff;
+  __syncthreads();
+  if (test(off + v)) atomicMin(s_hit, tid);
+  __syncthreads();
+  const int j = *s_hit;
+  const int b = sg * SMP_B + (j == 0x7fffffff ? SMP_B - 1 : j);
+  // mass before bucket b: the segment's offset plus the prefix of the bucket before it
+  *before = off + (j > 0 && j != 0x7fffffff ? pfx[sg * SMP_B + j - 1] : 0ull);
+  return b;
+}
+
+// Segment totals as a prefix, in LDS (every thread calls).
+__device__ __forceinline__ void smp_seg_prefix(const unsigned long long* __restrict__ seg, unsigned long long* segc,
+                                               unsigned long long* sc) {
+  const unsigned long long c = smp_scan256(seg[threadIdx.x], sc);
+  segc[threadIdx.x] = c;
+  __syncthreads();
+}
+
+// Every work group alike finds one bucket -- WALK 0: the cut's (the first
+// whose cumulative mass, rounded to float, reaches top_p); WALK 1: the
+// draw's (the first whose cumulative mass reaches t = r * C, C the cut's
+// running sum from the first resolve) -- and appends its elements to the
+// list; work group 0 records the mass before it.
+template <int WALK>
+__global__ void __launch_bounds__(SMP_B) k_smp_gather(const uint32_t* __restrict__ key, int n,
+                                                      const unsigned long long* __restrict__ pfx,
+                                                      const unsigned long long* __restrict__ seg, float top_p, float r,
+                                                      uint2* __restrict__ list, SmpMeta* __restrict__ meta) {
+  __shared__ unsigned long long segc[SMP_B], sc[SMP_B];
+  __shared__ int s_hit;
+  __shared__ unsigned int s_cnt, s_base;
+  smp_seg_prefix(seg, segc, sc);
+  unsigned long long before = 0ull;
+  int bk0;
+  if constexpr (WALK) {
+    // positions exist only in nonempty buckets: with t = 0 the draw is the
+    // first element, in the first bucket of positive mass (the largest p is
+    // at least 1/n)
+    const double t = static_cast<double>(r) * smp_mass(meta->c_mass);
+    bk0 = smp_bucket(pfx, segc, [&](unsigned long long m) { return m > 0ull && t <= smp_mass(m); }, &before, &s_hit);
+  } else {
+    bk0 = smp_bucket(pfx, segc, [&](unsigned long long m) { return static_cast<float>(smp_mass(m)) >= top_p; },
+                     &before, &s_hit);
+  }
+  if (bk0 < 0) bk0 = SMP_NBKT;  // nothing passes (non-finite input): gather nothing
+  if (blockIdx.x == 0 && threadIdx.x == 0) meta->base = before;
+  const int i = static_cast<int>(blockIdx.x) * SMP_B + threadIdx.x;
+  const uint32_t kv = i < n ? key[i] : 0xffffffffu;
+  const bool in = i < n && static_cast<int>(kv >> 16) == bk0;
+  if (threadIdx.x == 0) s_cnt = 0u;
+  __syncthreads();
+  unsigned int slot = 0u;
+  if (in) slot = atomicAdd(&s_cnt, 1u);
+  __syncthreads();
+  if (threadIdx.x == 0 && s_cnt) s_base = atomicAdd(&meta->count, s_cnt);
+  __syncthreads();
+  // the count starts at zero and gathers at most n elements; the bound
+  // keeps a corrupted count from writing past the list
+  if (in && s_base + slot < static_cast<unsigned int>(n)) list[s_base + slot] = make_uint2(kv, static_cast<uint32_t>(i));
+}
+
+// Digit lvl (2..6) of the composite (key, id) within one bucket (the key's
+// top 16 bits are the bucket), most significant first: key bits 15..8, 7..0,
+// then id bits 23..16, 15..8, 7..0.
+__device__ __forceinline__ uint32_t smp_digit(uint2 kv, int lvl) {
+  return lvl < 4 ? (kv.x >> (24 - 8 * lvl)) & 0xffu : (kv.y >> (16 - 8 * (lvl - 4))) & 0xffu;
+}
+__device__ __forceinline__ bool smp_le(uint2 a, uint2 b) { return a.x < b.x || (a.x == b.x && a.y <= b.y); }
+__device__ __forceinline__ unsigned long long smp_elem_mass(uint2 kv) { return smp_fixed(__uint_as_float(~kv.x)); }
+
+struct SmpDescent {
+  unsigned long long hm[SMP_B];  // mass per digit
+  unsigned int hc[SMP_B];        // elements per digit
+  unsigned long long sc[SMP_B];  // scan
+  unsigned int cnt;              // compacted candidates
+  int hit;
+  uint2 found;
+};
+
+// Among the candidates src[0..n0) of one bucket (element order: (key, id)
+// ascending; with `limit`, only those <= lim), the first element at which
+// base + the running mass passes test; returns it and, in *total, the
+// running mass through it.  One digit per level: the masses per digit value,
+// the first digit whose cumulative mass passes, then only that digit's
+// candidates (copied to the other buffer when they are fewer).  found.y ==
+// 0xffffffff when none passes.
+template <class Test>
+__device__ uint2 smp_descend(const uint2* src, unsigned int n0, uint2* buf0, uint2* buf1, unsigned long long base,
+                             Test test, bool limit, uint2 lim, unsigned long long* total, SmpDescent& D) {
+  const int tid = threadIdx.x;
+  const uint2* cur = src;
+  unsigned int n = n0;
+  bool first = true;  // the limit applies while reading src
+  int which = 0;
+  for (int lvl = 2; lvl < 7; ++lvl) {
+    __syncthreads();
+    D.hm[tid] = 0ull;
+    D.hc[tid] = 0u;
+    if (tid == 0) {
+      D.cnt = 0u;
+      D.hit = 0x7fffffff;
+    }
+    __syncthreads();
+    for (unsigned int i = tid; i < n; i += SMP_B) {
+      const uint2 kv = cur[i];
+      if (first && limit && !smp_le(kv, lim)) continue;
+      const uint32_t d = smp_digit(kv, lvl);
+      atomicAdd(&D.hm[d], smp_elem_mass(kv));
+      atomicAdd(&D.hc[d], 1u);
+    }
+    __syncthreads();
+    const unsigned long long c = smp_scan256(D.hm[tid], D.sc);
+    if (D.hc[tid] > 0u && test(base + c)) atomicMin(&D.hit, tid);
+    __syncthreads();
+    const int d = D.hit;
+    if (d == 0x7fffffff) return make_uint2(0u, 0xffffffffu);
+    base += d > 0 ? D.sc[d - 1] : 0ull;
+    const unsigned int nd = D.hc[d];
+    if (nd == 1u || lvl == 6) {
+      // the one element of digit d: the answer
+      for (unsigned int i = tid; i < n; i += SMP_B) {
+        const uint2 kv = cur[i];
+        if (first && limit && !smp_le(kv, lim)) continue;
+        if (smp_digit(kv, lvl) == static_cast<uint32_t>(d)) D.found = kv;
+      }
+      __syncthreads();
+      const uint2 f = D.found;
+      *total = base + smp_elem_mass(f);
+      return f;
+    }
+    if (nd < n || first) {
+      // keep digit d's candidates only (order within the buffer is free)
+      uint2* dst = which ? buf1 : buf0;
+      for (unsigned int i = tid; i < n; i += SMP_B) {
+        const uint2 kv = cur[i];
+        if (first && limit && !smp_le(kv, lim)) continue;
+        if (smp_digit(kv, lvl) == static_cast<uint32_t>(d)) dst[atomicAdd(&D.cnt, 1u)] = kv;
+      }
+      __threadfence();
+      __syncthreads();
+      cur = dst;
+      n = D.cnt;
+      which ^= 1;
+      first = false;
+    }
+  }
+  return make_uint2(0u, 0xffffffffu);  // not reached: level 6 returns
+}
+
+// One work group over the gathered bucket.  WALK 0: the cut (the first
+// position whose running sum, rounded to float, reaches top_p), recorded with
+// its running sum C.  WALK 1: the draw (the first position up to the cut whose
+// running sum reaches r * C); writes the token and advances the step state
+// like the greedy argmax.  Each leaves the list empty for the next gather.
+template <int WALK>
+__global__ void __launch_bounds__(SMP_B) k_smp_resolve(const uint2* __restrict__ list, uint2* __restrict__ buf0,
+                                                       uint2* __restrict__ buf1, SmpMeta* __restrict__ meta, int n_vocab,
+                                                       float top_p, float r, int* __restrict__ out_token,
+                                                       StepState* st, int* __restrict__ out_tokens) {
+  __shared__ SmpDescent D;
+  const unsigned int n = min(meta->count, static_cast<unsigned int>(n_vocab));
+  const unsigned long long base = meta->base;
+  unsigned long long cum = 0ull;
+  if constexpr (!WALK) {
+    const uint2 cut = smp_descend(list, n, buf0, buf1, base,
+                                  [&](unsigned long long m) { return static_cast<float>(smp_mass(m)) >= top_p; },
+                                  false, make_uint2(0u, 0u), &cum, D);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      meta->count = 0u;
+      meta->cut = cut;
+      meta->c_mass = cut.y == 0xffffffffu ? 0ull : cum;
+    }
+  } else {
+    const uint2 cut = meta->cut;
+    const double t = static_cast<double>(r) * smp_mass(meta->c_mass);
+    uint2 w = smp_descend(list, n, buf0, buf1, base, [&](unsigned long long m) { return t <= smp_mass(m); }, true,
+                          cut, &cum, D);
+    if (w.y == 0xffffffffu) w = cut;  // the walk's fallback: the cut's position
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      // non-finite inputs can leave no position found: a token in range still
+      const int tok = w.y < static_cast<uint32_t>(n_vocab) ? static_cast<int>(w.y) : 0;
+      meta->count = 0u;
+      if (out_token) *out_token = tok;
+      if (st) {
+        st->token = tok;
+        st->pos = st->pos + 1;
+        if (out_tokens && st->step < st->n_out) out_tokens[st->step] = tok;
+        st->step = st->step + 1;
+      }
+    }
+  }
+}
+
+// Scratch layout: first, at offsets that do not depend on n, the sort-free
+// path's state that must read zero at every call (bucket masses, the gather
+// count; zeroed with the buffer at allocation and left zero by each call),
+// its segment prefixes and totals; then e, p, key, key2, id, id2 (n each),
+// pmax (nblk floats), bs (nblk doubles), the gathered elements and two
+// candidate buffers (n each), the sort's scratch; every piece on a 256-byte
+// boundary.
 struct SmpLayout {
-  size_t e, p, key, key2, id, id2, pmax, bs, sort, end, sort_bytes;
+  size_t hm, pfx, seg, meta, e, p, key, key2, id, id2, pmax, bs, list, buf0, buf1, sort, end, sort_bytes;
 };
 
 SmpLayout smp_layout(int n) {
@@ -288,6 +634,10 @@ SmpLayout smp_layout(int n) {
     cur += (bytes + 255) & ~static_cast<size_t>(255);
     return at;
   };
+  L.hm = take(static_cast<size_t>(SMP_HCOPY) * SMP_NBKT * 8);
+  L.pfx = take(static_cast<size_t>(SMP_NBKT) * 8);
+  L.seg = take(static_cast<size_t>(SMP_NBKT / SMP_B) * 8);
+  L.meta = take(sizeof(SmpMeta));
   const size_t n4 = static_cast<size_t>(n) * 4;
   L.e = take(n4);
   L.p = take(n4);
@@ -297,6 +647,9 @@ SmpLayout smp_layout(int n) {
   L.id2 = take(n4);
   L.pmax = take(nblk * 4);
   L.bs = take(nblk * 8);
+  L.list = take(static_cast<size_t>(n) * 8);
+  L.buf0 = take(static_cast<size_t>(n) * 8);
+  L.buf1 = take(static_cast<size_t>(n) * 8);
   (void)rocprim::radix_sort_pairs(nullptr, L.sort_bytes, static_cast<uint32_t*>(nullptr),
                                   static_cast<uint32_t*>(nullptr), static_cast<int*>(nullptr),
                                   static_cast<int*>(nullptr), n);
@@ -333,6 +686,25 @@ hipError_t launch_sample(void* scratch, size_t scratch_bytes, const float* logit
   const int topp = (top_p > 0.0f && top_p < 1.0f) ? 1 : 0;
   hipLaunchKernelGGL(k_smp_max, dim3(nblk), dim3(SMP_B), 0, s, logits, n, inv_temp, apply, pmax);
   hipLaunchKernelGGL(k_smp_exp, dim3(nblk), dim3(SMP_B), 0, s, logits, n, inv_temp, apply, pmax, nblk, e, bs);
+  if (topp && top_p <= SMP_HIST_TOPP) {
+    // exact masses: no sort (see k_smp_prob_hist)
+    unsigned long long* hm = reinterpret_cast<unsigned long long*>(base + L.hm);
+    unsigned long long* pfx = reinterpret_cast<unsigned long long*>(base + L.pfx);
+    unsigned long long* seg = reinterpret_cast<unsigned long long*>(base + L.seg);
+    SmpMeta* meta = reinterpret_cast<SmpMeta*>(base + L.meta);
+    uint2* list = reinterpret_cast<uint2*>(base + L.list);
+    uint2* buf0 = reinterpret_cast<uint2*>(base + L.buf0);
+    uint2* buf1 = reinterpret_cast<uint2*>(base + L.buf1);
+    hipLaunchKernelGGL(k_smp_prob_hist, dim3((n + SMP_HWG - 1) / SMP_HWG), dim3(SMP_B), 0, s, e, n, bs, nblk, key, hm);
+    hipLaunchKernelGGL(k_smp_seg, dim3(SMP_NBKT / SMP_B), dim3(SMP_B), 0, s, hm, pfx, seg);
+    hipLaunchKernelGGL(k_smp_gather<0>, dim3(nblk), dim3(SMP_B), 0, s, key, n, pfx, seg, top_p, r, list, meta);
+    hipLaunchKernelGGL(k_smp_resolve<0>, dim3(1), dim3(SMP_B), 0, s, list, buf0, buf1, meta, n, top_p, r, out_token,
+                       st, out_tokens);
+    hipLaunchKernelGGL(k_smp_gather<1>, dim3(nblk), dim3(SMP_B), 0, s, key, n, pfx, seg, top_p, r, list, meta);
+    hipLaunchKernelGGL(k_smp_resolve<1>, dim3(1), dim3(SMP_B), 0, s, list, buf0, buf1, meta, n, top_p, r, out_token,
+                       st, out_tokens);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(k_smp_prob, dim3(nblk), dim3(SMP_B), 0, s, e, n, bs, nblk, topp, key, id, p);
   if (topp) {
     const hipError_t se = rocprim::radix_sort_pairs(sort_tmp, sort_bytes, key, key2, id, id2, n, 0, 32, s);

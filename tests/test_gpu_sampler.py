@@ -19,6 +19,10 @@ CASES = [
     (130560, 3.0, 0.8, 0.95), (130560, 0.02, 1.0, 0.95), (130560, 8.0, 1.3, 0.5),
     (4000, 3.0, 1.0, 1.0), (4000, 3.0, 0.0, 0.0), (4000, 1.0, 0.7, 1e-6),
     (257, 2.0, 0.9, 0.9), (1, 1.0, 0.8, 0.95), (300, 0.0, 1.0, 0.5),
+    # the sort-free top-p path at its limits (top_p 0.998, the largest
+    # vocabulary), one bucket of 130,560 equal p (ordered by id alone), and
+    # just past the limit (the sorted path)
+    (130560, 3.0, 1.0, 0.998), (524288, 2.0, 1.0, 0.95), (130560, 0.0, 1.0, 0.7), (130560, 3.0, 1.0, 0.999),
 ]
 
 
