@@ -98,6 +98,7 @@ struct mcpm_engine {
   size_t sample_cap = 0;
   // the FFN block as one launch (gate/up, grid barrier, down)
   bool fused_ffn = false;
+  bool fused_attn = false;  // QKV and attention in one launch (launch_qkv_attn)
   unsigned* gsync = nullptr;  // GRID_SYNC_WORDS words
 };
 
@@ -268,6 +269,8 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
   {
     const char* f = std::getenv("MCPM_FUSED_FFN");
     e->fused_ffn = f && std::atoi(f) != 0;
+    const char* a = std::getenv("MCPM_FUSED_ATTN");
+    e->fused_attn = a && std::atoi(a) != 0;
   }
   *out = e;
   return MCPM_OK;
@@ -319,7 +322,7 @@ hipError_t timed(mcpm_engine* e, int kc, F&& launch) {
 // (spin limit) left its error word set; report it and reset the barrier
 // state for the next launches.
 int check_grid_sync(mcpm_engine* e) {
-  if (!e->fused_ffn) return MCPM_OK;
+  if (!e->fused_ffn && !e->fused_attn) return MCPM_OK;
   unsigned err = 0;
   MCPM_HIP(hipMemcpy(&err, e->gsync + 8 * 64 + 64, sizeof err, hipMemcpyDeviceToHost));
   if (!err) return MCPM_OK;
@@ -339,6 +342,7 @@ int enqueue_token(mcpm_engine* e) {
     const Layer& L = e->L[l];
     float* kc = e->kc + static_cast<size_t>(l) * e->max_seq * kvd;
     float* vc = e->vc + static_cast<size_t>(l) * e->max_seq * kvd;
+    const AttnPart part = attn_part_of(e->attn_part, c.n_heads, e->max_chunks, c.head_dim);
     {
       GemvArgs a{};
       a.reg[0] = GemvRegion{view_of(L.wq), e->q, 0, qd};
@@ -356,12 +360,20 @@ int enqueue_token(mcpm_engine* e) {
       a.k_cache = kc;
       a.v_cache = vc;
       a.kvd = kvd;
-      MCPM_HIP(timed(e, MCPM_KC_QKV, [&] { return launch_gemv(a, PRO_NORM_AWAY, EPI_QKV, n_cu, s); }));
+      hipError_t fe = hipErrorNotSupported;
+      if (e->fused_attn) {
+        const GridSync gs{e->gsync, e->gsync + 8 * 64, e->gsync + 8 * 64 + 64, 1u << 20};
+        const AttnArgs at{e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part.o, part.mz};
+        fe = timed(e, MCPM_KC_QKV, [&] { return launch_qkv_attn(a, at, n_cu, gs, s); });
+        if (fe != hipSuccess && fe != hipErrorNotSupported) MCPM_HIP(fe);
+      }
+      if (fe == hipErrorNotSupported) {
+        MCPM_HIP(timed(e, MCPM_KC_QKV, [&] { return launch_gemv(a, PRO_NORM_AWAY, EPI_QKV, n_cu, s); }));
+        MCPM_HIP(timed(e, MCPM_KC_ATTN, [&] {
+          return launch_attention(e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part, s);
+        }));
+      }
     }
-    const AttnPart part = attn_part_of(e->attn_part, c.n_heads, e->max_chunks, c.head_dim);
-    MCPM_HIP(timed(e, MCPM_KC_ATTN, [&] {
-      return launch_attention(e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part, s);
-    }));
     {
       // the attention output is combined from its chunk partials in this
       // GEMV's prologue where the shape allows, else by its own kernel

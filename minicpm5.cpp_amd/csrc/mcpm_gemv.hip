@@ -29,6 +29,7 @@
 #include <cstdio>
 #include <cstring>
 
+#include "mcpm_attn.h"
 #include "mcpm_device.h"
 
 namespace mcpm {
@@ -1044,6 +1045,45 @@ __global__ void __launch_bounds__(64 * GEMV_TILE_WAVES)
                                                                             L, &pre);
 }
 
+// QKV and attention of one layer in one launch (src/model.cpp:178-195): the
+// QKV GEMV (RMSNorm + Q8_K prologue, RoPE; q and the K and V rows at pos
+// written through for the other work groups), a grid barrier, then
+// k_attention's splits, work group b taking splits b, b + G, ... (split it:
+// kv head it % n_kv_heads, split it / n_kv_heads).  A work group issues its
+// first split's K and V loads before the barrier, so their latency overlaps
+// the wait, all but the row at pos, which this launch writes: that row is
+// read only after the barrier.  Work groups without a split leave after
+// arriving (work group 0 waits, then advances the barrier's launch count).
+template <int WT, int HDM>
+__global__ void __launch_bounds__(64 * GEMV_TILE_WAVES)
+    k_qkv_attn(const GemvArgs qa, int q_items, int q_S, int q_KB, int q_grid, const AttnArgs at, GridSync gs) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t LQA[];
+  const int b = static_cast<int>(blockIdx.x), G = static_cast<int>(gridDim.x);
+  __shared__ unsigned s_gen;
+  if (threadIdx.x == 0) s_gen = ld_coh_u(gs.gen);
+  if (b < q_grid)
+    gemv_core<PRO_NORM_AWAY, EPI_QKV, true, WT, false, COH_OUT>(qa, q_items, q_S, q_KB, b, q_grid, LQA, nullptr);
+  grid_arrive(gs);  // also makes s_gen visible to every wave
+  const unsigned gen = s_gen;
+  const int T = at.state[1] + 1;
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  const int n_items = at.n_kv_heads * attn_splits(nch);
+  if (b >= n_items && b != 0) return;
+  AttnRegs<HDM / 16> R;
+  if (b < n_items) {
+    const int r4 = at.head_dim / 4;
+    attn_load_chunk<HDM / 16, true>(R, at.kc, at.vc, (b / at.n_kv_heads) * attn_chunks_per_split(nch), T,
+                              at.n_kv_heads * at.head_dim, static_cast<size_t>(b % at.n_kv_heads) * at.head_dim, r4,
+                              ATTN_CHUNK * r4);
+  }
+  if (!grid_wait(gs, gen, 1, 0)) return;
+  if (b == 0 && threadIdx.x == 0) __hip_atomic_fetch_add(gs.gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const AttnLds<HDM> S(reinterpret_cast<float*>(LQA));
+  for (int it = b; it < n_items; it += G)
+    attn_split<HDM, true>(at.q, at.kc, at.vc, T, it % at.n_kv_heads, it / at.n_kv_heads, at.n_heads, at.n_kv_heads,
+                          at.head_dim, at.max_chunks, at.part_o, at.part_mz, S, R, it == b);
+}
+
 // ------------------------------------------------------------- dispatch ----
 
 namespace {
@@ -1263,6 +1303,45 @@ hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, 
   MCPM_PE(PRO_NORM_EVEN, EPI_LOGITS)
   MCPM_PE(PRO_NORM_EVEN, EPI_STORE)
 #undef MCPM_PE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_qkv_attn(const GemvArgs& q0, const AttnArgs& at, int n_cu, const GridSync& gs, hipStream_t s) {
+  if (q0.nb <= 0 || q0.nb > MAX_NB || q0.nreg != 3 || q0.pair || at.head_dim <= 0 || at.head_dim > 128 ||
+      at.head_dim % 4 || at.n_kv_heads <= 0 || at.n_heads % at.n_kv_heads ||
+      at.n_heads / at.n_kv_heads > ATTN_MAX_GROUP || at.head_dim != q0.head_dim)
+    return hipErrorInvalidValue;
+  // the rows at pos are read again through 32-bit buffer offsets
+  if (static_cast<size_t>(at.max_chunks) * ATTN_CHUNK * at.n_kv_heads * at.head_dim * sizeof(float) >= (size_t{1} << 31))
+    return hipErrorNotSupported;
+  GemvArgs qa = q0;
+  const Shape sh = pick_shape(qa, PRO_NORM_AWAY, EPI_QKV, n_cu);
+  if (!sh.tile || sh.grp) return hipErrorNotSupported;  // the fused kernel runs a TILE phase
+  const int qi = n_items_of(qa, sh);
+  const int qg = (qi + GEMV_TILE_WAVES - 1) / GEMV_TILE_WAVES;
+  // one work group per CU, all resident; always n_cu of them, so that every
+  // launch on the same barrier state counts the same arrivals per XCD
+  if (qg > n_cu) return hipErrorNotSupported;
+  const int grid = n_cu;
+  const bool h64 = at.head_dim <= 64;
+  const size_t lds =
+      std::max(lds_bytes(qa, sh, PRO_NORM_AWAY), h64 ? AttnLds<64>::bytes : AttnLds<128>::bytes);
+  const int wt = weight_kind(qa);
+#define MCPM_QA(WW, HH)                                                                                    \
+  if (wt == WW && (HH == 64) == h64) {                                                                     \
+    if (lds > 65536) {                                                                                     \
+      const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_qkv_attn<WW, HH>),       \
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,              \
+                                                  static_cast<int>(lds));                                  \
+      if (attr != hipSuccess) return attr;                                                                 \
+    }                                                                                                      \
+    launch_kernel(k_qkv_attn<WW, HH>, dim3(grid), dim3(64 * GEMV_TILE_WAVES), lds, s, qa, qi, sh.S, sh.KB, \
+                  qg, at, gs);                                                                             \
+    return hipGetLastError();                                                                              \
+  }
+  MCPM_QA(WT_Q4, 64) MCPM_QA(WT_Q6, 64) MCPM_QA(WT_MIX, 64)
+  MCPM_QA(WT_Q4, 128) MCPM_QA(WT_Q6, 128) MCPM_QA(WT_MIX, 128)
+#undef MCPM_QA
   return hipErrorInvalidValue;
 }
 

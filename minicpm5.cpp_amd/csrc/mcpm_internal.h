@@ -240,6 +240,24 @@ constexpr size_t GRID_SYNC_WORDS = 8 * 64 + 64 + 64;
 // of work groups (the caller launches the two kernels then).
 hipError_t launch_ffn_fused(const GemvArgs& gu, const GemvArgs& dn, int n_cu, const GridSync& gs, hipStream_t s);
 
+// The attention inputs of the QKV + attention launch: q, the layer's K and V
+// cache, the step state (position at state[1]) and the chunk partials, as
+// for launch_attention.
+struct AttnArgs {
+  const float* q;
+  const float* kc;
+  const float* vc;
+  const int* state;
+  int n_heads, n_kv_heads, head_dim, max_chunks;
+  float* part_o;
+  float2* part_mz;
+};
+// QKV (as launch_gemv's PRO_NORM_AWAY/EPI_QKV) and the attention of one
+// layer in one launch, with a grid barrier between them.
+// hipErrorNotSupported when the QKV shape does not fit one resident round of
+// work groups (the caller launches the two kernels then).
+hipError_t launch_qkv_attn(const GemvArgs& qkv, const AttnArgs& at, int n_cu, const GridSync& gs, hipStream_t s);
+
 // The temperature / top-p sampler on the device (mcpm_sampler.hip): scratch
 // bytes for n logits, and its passes for one uniform draw r.  The token goes
 // to *out_token (device) when given, and when st is given it becomes the next

@@ -341,3 +341,83 @@ def test_fused_ffn_block_matches_oracle(ctx, small_image, monkeypatch):
         np.testing.assert_array_equal(e.generate_greedy(gf["prompt"], 32), gf["tokens"][:32])
     finally:
         e.free()
+
+
+@pytest.mark.parametrize("case", ["small", "full32", "refshape", "long_8kv"])
+def test_fused_qkv_attention_matches_oracle(ctx, small_image, monkeypatch, case):
+    """MCPM_FUSED_ATTN=1: each layer's QKV GEMV and attention as one launch
+    (q and the new K and V rows written through, a grid barrier, then the
+    attention splits; each work group's first split's K and V rows loaded
+    before the barrier and the row at pos read again after it).  Against the
+    oracle: the small model's tokens and bit-identical logits at 70
+    positions (two chunks), the 2.4B-shaped model's first 32 steps, the
+    reference geometry (heads of 128, groups of 8, Q6_K v), and 2208
+    per-token positions of a model with 8 kv heads, whose 35 chunks give
+    280 splits: more than one per work group."""
+    monkeypatch.setenv("MCPM_FUSED_ATTN", "1")
+    if case == "small":
+        g = golden("small_model_greedy.npz")
+        announce("fused QKV+attention: small model")
+        e = mcpm.Engine(ctx, image=small_image)
+        try:
+            e.init_kv_cache(256)
+            # one launch per layer for QKV and attention together
+            e.set_kernel_timing(mcpm.KC_ATTN)
+            e.forward(1, 0)
+            assert e.kernel_time()[1] == 0
+            e.set_kernel_timing(mcpm.KC_QKV)
+            e.forward(1, 0)
+            assert e.kernel_time()[1] == e.cfg.n_layers
+            e.set_kernel_timing(-1)
+            got = e.generate_greedy(g["prompt"], len(g["tokens"]))
+            np.testing.assert_array_equal(got, O.OracleModel(small_image).generate_greedy(g["prompt"], len(got)))
+            om = O.OracleModel(small_image)
+            om.init_kv(256)
+            lg = np.empty(4000, np.float32)
+            toks = np.random.default_rng(11).integers(0, 4000, 70)
+            for pos, t in enumerate(toks):
+                logits, _ = e.forward(int(t), pos)
+                om.forward(int(t), pos, lg)
+                assert_bits(logits, lg)
+        finally:
+            e.free()
+    elif case == "full32":
+        gf = golden("full_model_oracle.npz")
+        announce("fused QKV+attention: 2.4B-shaped model greedy 32+32")
+        img = mcpm.synth_gguf(mcpm.config_2p4b(), seed=int(gf["seed"]), mix=0)
+        e = mcpm.Engine(ctx, image=img)
+        del img
+        try:
+            e.init_kv_cache(128)
+            np.testing.assert_array_equal(e.generate_greedy(gf["prompt"], 32), gf["tokens"][:32])
+        finally:
+            e.free()
+    elif case == "refshape":
+        g = golden("refshape_layout_greedy.npz")
+        L, D, NH, NKV, HD, F, V = [int(v) for v in g["config"]]
+        cfg = mcpm.make_config(L, D, NH, NKV, HD, F, V, rope_base=float(g["rope_base"]))
+        img = mcpm.synth_gguf(cfg, seed=int(g["seed"]), mix=int(g["mix"]))
+        announce("fused QKV+attention: reference geometry")
+        e = mcpm.Engine(ctx, image=img)
+        try:
+            e.init_kv_cache(96)
+            got = e.generate_greedy(g["prompt"], len(g["tokens"]))
+        finally:
+            e.free()
+        np.testing.assert_array_equal(got, O.OracleModel(img).generate_greedy(g["prompt"], len(g["tokens"])))
+    else:
+        cfg = mcpm.make_config(2, 1024, 16, 8, 64, 2048, 1000)
+        img = mcpm.synth_gguf(cfg, seed=405, mix=0)
+        prompt = [int(t) for t in np.random.default_rng(18).integers(0, 1000, 2200)]
+        announce("fused QKV+attention: 8 kv heads, 2200-token prompt per token")
+        e = mcpm.Engine(ctx, image=img)
+        try:
+            e.set_prefill(False)
+            e.init_kv_cache(2220)
+            got = list(e.generate_greedy(prompt, 8))
+        finally:
+            e.free()
+        om = O.OracleModel(img)
+        want = list(om.generate_greedy(prompt, 8))
+        om.close()
+        assert got == want
