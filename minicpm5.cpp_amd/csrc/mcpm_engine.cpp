@@ -96,6 +96,12 @@ struct mcpm_engine {
   bool sample_mode = false;
   void* d_sample = nullptr;
   size_t sample_cap = 0;
+  // the sampled graph ends with the sampler's passes, for these settings,
+  // when they need no sort (a cut at most 0.998, or none); the draws are
+  // read on the device, d_draws[step], one per generated token
+  float smp_T = 0.0f, smp_P = 0.0f;
+  bool smp_in_graph = false;
+  float* d_draws = nullptr;  // out_cap floats
   // the FFN block as one launch (gate/up, grid barrier, down)
   bool fused_ffn = false;
   bool fused_attn = false;  // QKV and attention in one launch (launch_qkv_attn)
@@ -146,7 +152,7 @@ void free_engine(mcpm_engine* e) {
                   static_cast<void*>(e->h), static_cast<void*>(e->logits), static_cast<void*>(e->argmax_part),
                   static_cast<void*>(e->st), static_cast<void*>(e->out_tokens), static_cast<void*>(e->kc),
                   static_cast<void*>(e->vc), static_cast<void*>(e->rope), static_cast<void*>(e->attn_part),
-                  e->d_sample, static_cast<void*>(e->gsync)})
+                  e->d_sample, static_cast<void*>(e->gsync), static_cast<void*>(e->d_draws)})
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
   free_prefill(e->pf);
@@ -278,13 +284,17 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
 
 int ensure_out_tokens(mcpm_engine* e, int n) {
   if (n <= e->out_cap) return MCPM_OK;
+  if (e->out_tokens || e->d_draws) MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
   if (e->out_tokens) (void)hipFree(e->out_tokens);
+  if (e->d_draws) (void)hipFree(e->d_draws);
   e->out_tokens = nullptr;
+  e->d_draws = nullptr;
   e->out_cap = 0;
+  drop_graph(e);  // the argmax and sampler nodes hold the arrays' pointers
   int rc = alloc_dev(reinterpret_cast<void**>(&e->out_tokens), n * sizeof(int));
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->d_draws), n * sizeof(float));
   if (rc) return rc;
   e->out_cap = n;
-  drop_graph(e);  // the argmax node holds the array pointer
   return MCPM_OK;
 }
 
@@ -441,6 +451,9 @@ int enqueue_token(mcpm_engine* e) {
     MCPM_HIP(timed(e, MCPM_KC_LM_HEAD, [&] { return launch_gemv(a, PRO_NORM_EVEN, EPI_LOGITS, n_cu, s); }));
   }
   if (!e->sample_mode) MCPM_HIP(launch_argmax_final(e->argmax_part, e->lm_grid, nullptr, e->st, e->out_tokens, s));
+  else if (e->smp_in_graph)
+    MCPM_HIP(launch_sample(e->d_sample, e->sample_cap, e->logits, c.vocab, e->smp_T, e->smp_P, 0.0f, nullptr, e->st,
+                           e->out_tokens, s, e->d_draws));
   return MCPM_OK;
 }
 
@@ -681,10 +694,36 @@ int mcpm_engine_forward(mcpm_engine* e, int token, int pos, int max_seq_len, flo
   return MCPM_OK;
 }
 
-// The token graph without (sampled) or with (greedy) the argmax at its end;
-// each is captured once and kept.
+// The token graph with the argmax at its end (greedy) or without it
+// (sampled); each is captured once and kept.  The sampled graph also ends
+// with the sampler's passes when its settings need no sort, and is captured
+// again when the settings change.
 static int set_sample_mode(mcpm_engine* e, bool on) {
   e->sample_mode = on;
+  return MCPM_OK;
+}
+
+static void set_sampling(mcpm_engine* e, float temperature, float top_p) {
+  if (e->graph[1] && (e->smp_T != temperature || e->smp_P != top_p)) {
+    (void)hipGraphExecDestroy(e->graph[1]);
+    e->graph[1] = nullptr;
+  }
+  e->smp_T = temperature;
+  e->smp_P = top_p;
+  const bool topp = top_p > 0.0f && top_p < 1.0f;
+  e->smp_in_graph = !topp || top_p <= sampler_sort_free_top_p();
+}
+
+// Draws of std::uniform_real_distribution<float> over std::mt19937(seed)
+// (src/sampler.cpp:5-6, 68-69), one per token, to d_draws[step0 ..].
+static int upload_draws(mcpm_engine* e, uint32_t seed, int step0, int n) {
+  std::mt19937 rng(seed);
+  std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+  std::vector<float> h(static_cast<size_t>(n));
+  for (float& v : h) v = dist(rng);
+  MCPM_HIP(hipMemcpyAsync(e->d_draws + step0, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice,
+                          e->ctx->stream));
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
   return MCPM_OK;
 }
 
@@ -697,6 +736,7 @@ static int ensure_sampler(mcpm_engine* e) {
   if (e->d_sample) (void)hipFree(e->d_sample);
   e->d_sample = nullptr;
   e->sample_cap = 0;
+  drop_graph(e);  // the sampler's nodes hold the scratch pointer
   int rc = alloc_dev(&e->d_sample, need);
   if (rc) return rc;
   e->sample_cap = need;
@@ -705,9 +745,12 @@ static int ensure_sampler(mcpm_engine* e) {
 
 // The next token from the logits of the step just queued: it becomes the
 // next input token and the next entry of the generated list.
-static int sample_step(mcpm_engine* e, float temperature, float top_p, float r) {
-  MCPM_HIP(launch_sample(e->d_sample, e->sample_cap, e->logits, e->cfg.vocab, temperature, top_p, r, nullptr, e->st,
-                         e->out_tokens, e->ctx->stream));
+// Settings that need the sort run the sampler after the graph (its sort's
+// launches are not captured); the others ran it inside the graph.
+static int sample_step(mcpm_engine* e) {
+  if (e->smp_in_graph) return MCPM_OK;
+  MCPM_HIP(launch_sample(e->d_sample, e->sample_cap, e->logits, e->cfg.vocab, e->smp_T, e->smp_P, 0.0f, nullptr,
+                         e->st, e->out_tokens, e->ctx->stream, e->d_draws));
   return MCPM_OK;
 }
 
@@ -736,18 +779,20 @@ static int generate_at(mcpm_engine* e, const int* toks, int n, int pos0, int n_g
   if (!rc) rc = set_sample_mode(e, sampled);
   if (rc) return rc;
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-  std::mt19937 rng(seed);
-  std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+  if (sampled) {
+    set_sampling(e, temperature, top_p);
+    rc = upload_draws(e, seed, 0, n_gen);
+  }
   const int first = (e->use_prefill && n > 1) ? n - 1 : 0;
-  if (first) rc = mcpm_engine_prefill(e, toks, first, pos0);
+  if (!rc && first) rc = mcpm_engine_prefill(e, toks, first, pos0);
   for (int i = first; i < n && !rc; ++i) {
     rc = queue_state(e, i, toks[i], pos0 + i, 0);
     if (!rc) rc = run_token(e);
   }
-  if (!rc && sampled) rc = sample_step(e, temperature, top_p, dist(rng));
+  if (!rc && sampled) rc = sample_step(e);
   for (int i = 1; i < n_gen && !rc; ++i) {
     rc = run_token(e);
-    if (!rc && sampled) rc = sample_step(e, temperature, top_p, dist(rng));
+    if (!rc && sampled) rc = sample_step(e);
   }
   const int rc2 = set_sample_mode(e, false);
   if (rc) return rc;
@@ -816,11 +861,11 @@ int mcpm_engine_decode_sampled(mcpm_engine* e, int n_steps, float temperature, f
   int rc = ensure_sampler(e);
   if (!rc) rc = set_sample_mode(e, true);
   if (rc) return rc;
-  std::mt19937 rng(seed);
-  std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+  set_sampling(e, temperature, top_p);
+  rc = upload_draws(e, seed, e->gen_count, n_steps);
   for (int i = 0; i < n_steps && !rc; ++i) {
     rc = run_token(e);
-    if (!rc) rc = sample_step(e, temperature, top_p, dist(rng));
+    if (!rc) rc = sample_step(e);
   }
   const int rc2 = set_sample_mode(e, false);
   if (rc) return rc;

@@ -264,8 +264,12 @@ hipError_t launch_qkv_attn(const GemvArgs& qkv, const AttnArgs& at, int n_cu, co
 // input token, is appended to out_tokens and pos advances (as the argmax does).
 size_t sampler_bytes(int n);
 int sampler_max_n();  // largest n launch_sample takes
+float sampler_sort_free_top_p();  // cuts up to this top_p need no sort
+// draws (with st): the draw is read on the device, draws[st->step], in place
+// of r, so the launches can be captured once and replayed for every token.
 hipError_t launch_sample(void* scratch, size_t scratch_bytes, const float* logits, int n, float temperature,
-                         float top_p, float r, int* out_token, StepState* st, int* out_tokens, hipStream_t s);
+                         float top_p, float r, int* out_token, StepState* st, int* out_tokens, hipStream_t s,
+                         const float* draws = nullptr);
 
 // When `start` is set, the GEMV and attention launch helpers record these
 // events at their kernel's start and end (hipExtLaunchKernel), so the elapsed

@@ -159,10 +159,11 @@ template <int WT, int NT, int OCC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) k_gemm_q8k(const GemmArgs a) {
   constexpr int TOK = 16 * NT;        // tokens of the work group's tile
   constexpr int BROW = QK_K + 8;      // halves per token row of sB (padded: rows 132 dwords apart)
+  constexpr int BSROW = 24;           // halves per token of sBs (16 used; rows 12 dwords apart)
   constexpr int PPT = TOK * 32 / 256; // 16-byte pieces of a block's codes per thread
   __shared__ __attribute__((aligned(16))) _Float16 sB[2][TOK * BROW];
   __shared__ float sXd[2][TOK];
-  __shared__ __attribute__((aligned(16))) _Float16 sBs[2][TOK * 16];
+  __shared__ __attribute__((aligned(16))) _Float16 sBs[2][TOK * BSROW];
   const int tid = threadIdx.x, wave = tid >> 6;
   const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int n_rt = (a.rows + 15) >> 4;
@@ -200,19 +201,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   };
   // sB keeps each token's 256 codes as 32 quads of 8 halves, quad 8g + m =
   // elements 64g + 4m .. +3 and 64g + 32 + 4m .. +3 (the B operand of lane
-  // group m for the lanes of K-half g): piece k = p % 32 (elements 8k ..
-  // 8k+7, g = k/8, h = (k/4)%2, m = 2*(k%4)) goes to half h of quads m, m+1.
+  // group m for the lanes of K-half g), stored at slot (8g + m) ^ sw(g) with
+  // sw = 0, 1, 1, 0 for g = 0..3: the lanes of one pass of 8-byte stores (16
+  // or 32) then write distinct banks, where unswapped quads 8 and 16 apart
+  // share them.  Piece k = p % 32 (elements 8k .. 8k+7, g = k/8, h =
+  // (k/4)%2, m = 2*(k%4)) goes to half h of quads m, m+1.
   auto stash = [&](int buf) {
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       const int p = tid + 256 * k;
-      const int pk = p % 32, gq = pk >> 3, hq = (pk >> 2) & 1, mq = 2 * (pk & 3);
-      _Float16* row = &sB[buf][(p / 32) * BROW + (8 * gq + mq) * 8 + 4 * hq];
-      *reinterpret_cast<uint2*>(row) = uint2{pf[k].x, pf[k].y};
-      *reinterpret_cast<uint2*>(row + 8) = uint2{pf[k].z, pf[k].w};
+      const int pk = p % 32, gq = pk >> 3, hq = (pk >> 2) & 1, mq = 2 * (pk & 3), sw = (gq ^ (gq >> 1)) & 1;
+      _Float16* row = &sB[buf][(p / 32) * BROW + 4 * hq];
+      *reinterpret_cast<uint2*>(row + ((8 * gq + mq) ^ sw) * 8) = uint2{pf[k].x, pf[k].y};
+      *reinterpret_cast<uint2*>(row + ((8 * gq + mq + 1) ^ sw) * 8) = uint2{pf[k].z, pf[k].w};
     }
     if (tid < TOK) sXd[buf][tid] = pxd;
-    if (tid < 2 * TOK) *reinterpret_cast<u32x4*>(&sBs[buf][(tid / 2) * 16 + (tid & 1) * 8]) = pbs;
+    if (tid < 2 * TOK) *reinterpret_cast<u32x4*>(&sBs[buf][(tid / 2) * BSROW + (tid & 1) * 8]) = pbs;
   };
   fetch(0);
   stash(0);
@@ -301,9 +305,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       for (int i = 0; i < 4; ++i) ds[n][i] = xdv[n] * dw[i];
     }
     // the B operand of lane group m for token tile n is quad 8g + m of the
-    // token's row
+    // token's row (at slot (8g + m) ^ sw(g))
     auto bq = [&](int n, int m) {
-      return __builtin_bit_cast(h8, reinterpret_cast<const u32x4*>(&sB[buf][(16 * n + c16) * BROW])[8 * g + m]);
+      return __builtin_bit_cast(h8, reinterpret_cast<const u32x4*>(&sB[buf][(16 * n + c16) * BROW])[(8 * g + m) ^ ((g ^ (g >> 1)) & 1)]);
     };
     if constexpr (WT == 0) {
       const uint32_t s0 = wc.hdr.y, s1 = wc.hdr.z, s2 = wc.hdr.w;
@@ -346,7 +350,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       const h8 AM = g < 2 ? __builtin_bit_cast(h8, mr) : h8{};
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        const h8 BM = *reinterpret_cast<const h8*>(&sBs[buf][(16 * n + c16) * 16 + 8 * (g & 1)]);
+        const h8 BM = *reinterpret_cast<const h8*>(&sBs[buf][(16 * n + c16) * BSROW + 8 * (g & 1)]);
         const f32x4 DM = __builtin_amdgcn_mfma_f32_16x16x32_f16(AM, BM, zero4, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) accm[n][i] = __builtin_fmaf(-(xdv[n] * dmw[i]), DM[i], accm[n][i]);
@@ -396,7 +400,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       auto q6_mfma = [&](int m, int n, const h8& Al, const h8& Ah, const h8& AC, f32x4& S, f32x4& T) {
         const h8 B = bq(n, m);
         // bsums 2m, 2m+1 of the token as an fp16 pair (lanes 0..15 use them)
-        const uint32_t bsw = reinterpret_cast<const uint32_t*>(&sBs[buf][(16 * n + c16) * 16])[m];
+        const uint32_t bsw = reinterpret_cast<const uint32_t*>(&sBs[buf][(16 * n + c16) * BSROW])[m];
         const h8 BC = __builtin_bit_cast(h8, u32x4{g == 0 ? bsw : 0u, 0u, 0u, 0u});
         S = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B, zero4, 0, 0, 0);
         const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC, BC, zero4, 0, 0, 0);  // -2C

@@ -49,6 +49,12 @@ __device__ __forceinline__ float smp_logit(const float* __restrict__ logits, int
   return apply ? l * inv_temp : l;
 }
 
+// The uniform draw: draws[st->step] when the draws are in device memory (a
+// captured token graph, one draw per generated token), else the argument.
+__device__ __forceinline__ float smp_draw(float r, const float* __restrict__ draws, const StepState* st) {
+  return draws ? draws[min(max(st->step, 0), st->n_out - 1)] : r;
+}
+
 // the value at position k of the walk's order
 __device__ __forceinline__ float smp_val(const uint32_t* __restrict__ key, const float* __restrict__ p, int topp,
                                          int k) {
@@ -212,7 +218,8 @@ __device__ __forceinline__ void smp_block_prefix(const uint32_t* __restrict__ ke
 __global__ void __launch_bounds__(SMP_B) k_smp_pick(const uint32_t* __restrict__ key, const int* __restrict__ id,
                                                     const float* __restrict__ p, int n, const double* __restrict__ bs,
                                                     int nblk, int topp, float top_p, float r, int* __restrict__ out_token,
-                                                    StepState* st, int* __restrict__ out_tokens) {
+                                                    StepState* st, int* __restrict__ out_tokens,
+                                                    const float* __restrict__ draws) {
   __shared__ __attribute__((aligned(16))) double P[SMP_REC];  // inclusive block prefix sums (zero-padded)
   __shared__ __attribute__((aligned(16))) double pr[SMP_B];   // in-block running sums of one block
   __shared__ __attribute__((aligned(16))) float sv[SMP_B];
@@ -257,7 +264,7 @@ __global__ void __launch_bounds__(SMP_B) k_smp_pick(const uint32_t* __restrict__
       C = off + pr[qq];
     }
   }
-  const double t = static_cast<double>(r) * C;
+  const double t = static_cast<double>(smp_draw(r, draws, st)) * C;
   const int nrec = (cnt - 1) / SMP_B + 1;  // blocks through the cut's
   const int jw = smp_first(nrec, [&](int j) { return t <= P[j]; }, &s_hit);
   int k = -1;
@@ -446,7 +453,8 @@ template <int WALK>
 __global__ void __launch_bounds__(SMP_B) k_smp_gather(const uint32_t* __restrict__ key, int n,
                                                       const unsigned long long* __restrict__ pfx,
                                                       const unsigned long long* __restrict__ seg, float top_p, float r,
-                                                      uint2* __restrict__ list, SmpMeta* __restrict__ meta) {
+                                                      uint2* __restrict__ list, SmpMeta* __restrict__ meta,
+                                                      const float* __restrict__ draws, const StepState* st) {
   __shared__ unsigned long long segc[SMP_B], sc[SMP_B];
   __shared__ int s_hit;
   __shared__ unsigned int s_cnt, s_base;
@@ -457,7 +465,7 @@ __global__ void __launch_bounds__(SMP_B) k_smp_gather(const uint32_t* __restrict
     // positions exist only in nonempty buckets: with t = 0 the draw is the
     // first element, in the first bucket of positive mass (the largest p is
     // at least 1/n)
-    const double t = static_cast<double>(r) * smp_mass(meta->c_mass);
+    const double t = static_cast<double>(smp_draw(r, draws, st)) * smp_mass(meta->c_mass);
     bk0 = smp_bucket(pfx, segc, [&](unsigned long long m) { return m > 0ull && t <= smp_mass(m); }, &before, &s_hit);
   } else {
     bk0 = smp_bucket(pfx, segc, [&](unsigned long long m) { return static_cast<float>(smp_mass(m)) >= top_p; },
@@ -577,7 +585,8 @@ template <int WALK>
 __global__ void __launch_bounds__(SMP_B) k_smp_resolve(const uint2* __restrict__ list, uint2* __restrict__ buf0,
                                                        uint2* __restrict__ buf1, SmpMeta* __restrict__ meta, int n_vocab,
                                                        float top_p, float r, int* __restrict__ out_token,
-                                                       StepState* st, int* __restrict__ out_tokens) {
+                                                       StepState* st, int* __restrict__ out_tokens,
+                                                       const float* __restrict__ draws) {
   __shared__ SmpDescent D;
   const unsigned int n = min(meta->count, static_cast<unsigned int>(n_vocab));
   const unsigned long long base = meta->base;
@@ -594,7 +603,7 @@ __global__ void __launch_bounds__(SMP_B) k_smp_resolve(const uint2* __restrict__
     }
   } else {
     const uint2 cut = meta->cut;
-    const double t = static_cast<double>(r) * smp_mass(meta->c_mass);
+    const double t = static_cast<double>(smp_draw(r, draws, st)) * smp_mass(meta->c_mass);
     uint2 w = smp_descend(list, n, buf0, buf1, base, [&](unsigned long long m) { return t <= smp_mass(m); }, true,
                           cut, &cum, D);
     if (w.y == 0xffffffffu) w = cut;  // the walk's fallback: the cut's position
@@ -662,10 +671,12 @@ SmpLayout smp_layout(int n) {
 
 size_t sampler_bytes(int n) { return n > 0 ? smp_layout(n).end : 0; }
 int sampler_max_n() { return SMP_REC * SMP_B; }
+float sampler_sort_free_top_p() { return SMP_HIST_TOPP; }
 
 hipError_t launch_sample(void* scratch, size_t scratch_bytes, const float* logits, int n, float temperature,
-                         float top_p, float r, int* out_token, StepState* st, int* out_tokens, hipStream_t s) {
-  if (n <= 0 || n > SMP_REC * SMP_B || !logits || !scratch) return hipErrorInvalidValue;
+                         float top_p, float r, int* out_token, StepState* st, int* out_tokens, hipStream_t s,
+                         const float* draws) {
+  if (n <= 0 || n > SMP_REC * SMP_B || !logits || !scratch || (draws && !st)) return hipErrorInvalidValue;
   const SmpLayout L = smp_layout(n);
   if (L.end > scratch_bytes) return hipErrorInvalidValue;
   const int nblk = (n + SMP_B - 1) / SMP_B;
@@ -697,12 +708,14 @@ hipError_t launch_sample(void* scratch, size_t scratch_bytes, const float* logit
     uint2* buf1 = reinterpret_cast<uint2*>(base + L.buf1);
     hipLaunchKernelGGL(k_smp_prob_hist, dim3((n + SMP_HWG - 1) / SMP_HWG), dim3(SMP_B), 0, s, e, n, bs, nblk, key, hm);
     hipLaunchKernelGGL(k_smp_seg, dim3(SMP_NBKT / SMP_B), dim3(SMP_B), 0, s, hm, pfx, seg);
-    hipLaunchKernelGGL(k_smp_gather<0>, dim3(nblk), dim3(SMP_B), 0, s, key, n, pfx, seg, top_p, r, list, meta);
+    hipLaunchKernelGGL(k_smp_gather<0>, dim3(nblk), dim3(SMP_B), 0, s, key, n, pfx, seg, top_p, r, list, meta,
+                       draws, st);
     hipLaunchKernelGGL(k_smp_resolve<0>, dim3(1), dim3(SMP_B), 0, s, list, buf0, buf1, meta, n, top_p, r, out_token,
-                       st, out_tokens);
-    hipLaunchKernelGGL(k_smp_gather<1>, dim3(nblk), dim3(SMP_B), 0, s, key, n, pfx, seg, top_p, r, list, meta);
+                       st, out_tokens, draws);
+    hipLaunchKernelGGL(k_smp_gather<1>, dim3(nblk), dim3(SMP_B), 0, s, key, n, pfx, seg, top_p, r, list, meta,
+                       draws, st);
     hipLaunchKernelGGL(k_smp_resolve<1>, dim3(1), dim3(SMP_B), 0, s, list, buf0, buf1, meta, n, top_p, r, out_token,
-                       st, out_tokens);
+                       st, out_tokens, draws);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(k_smp_prob, dim3(nblk), dim3(SMP_B), 0, s, e, n, bs, nblk, topp, key, id, p);
@@ -713,7 +726,7 @@ hipError_t launch_sample(void* scratch, size_t scratch_bytes, const float* logit
   const uint32_t* kk = topp ? key2 : key;
   hipLaunchKernelGGL(k_smp_bsum, dim3(nblk), dim3(SMP_B), 0, s, kk, p, n, topp, bs);
   hipLaunchKernelGGL(k_smp_pick, dim3(1), dim3(SMP_B), 0, s, kk, id2, p, n, bs, nblk, topp, top_p, r, out_token, st,
-                     out_tokens);
+                     out_tokens, draws);
   return hipGetLastError();
 }
 

@@ -103,25 +103,36 @@ def test_load_from_file_and_errors(ctx, small_image):
     assert ei.value.code == -5
 
 
-def test_sampled_matches_oracle_sampler(small_engine, small_image):
-    prompt = np.arange(10, 26, dtype=np.int32)
-    announce("small sampled T=0.8 top_p=0.95")
-    got = small_engine.generate_sampled(prompt, 24, 0.8, 0.95, 1234)
-    om = O.OracleModel(small_image)
+def _oracle_sampled(image, prompt, n, temperature, top_p, seed):
+    om = O.OracleModel(image)
     om.init_kv(64)
     orc = O.oracle()
     gen = np.zeros(625, np.uint32)  # or_mt19937 state
-    orc.or_mt_seed(gen.ctypes.data, 1234)
+    orc.or_mt_seed(gen.ctypes.data, seed)
     lg = np.empty(4000, np.float32)
     for p, t in enumerate(prompt):
         om.forward(int(t), p, lg)
     out = []
-    for i in range(24):
-        nxt = orc.or_sample_blocked(lg.ctypes.data, 4000, 0.8, 0.95, orc.or_mt_uniform01(gen.ctypes.data))
+    for i in range(n):
+        nxt = orc.or_sample_blocked(lg.ctypes.data, 4000, temperature, top_p, orc.or_mt_uniform01(gen.ctypes.data))
         out.append(nxt)
-        if i < 23:
+        if i < n - 1:
             om.forward(nxt, len(prompt) + i, lg)
-    np.testing.assert_array_equal(got, np.array(out, np.int32))
+    return np.array(out, np.int32)
+
+
+def test_sampled_matches_oracle_sampler(small_engine, small_image):
+    """Sampled generation against the oracle's model and sampler, one after
+    another on one engine: settings whose sampler runs inside the captured
+    token graph (a cut at 0.95 and at 0.5, no cut, a temperature of 1, the
+    draw read on the device per step) and a cut above 0.998 (the sort, after
+    the graph), each change of settings capturing the graph again."""
+    prompt = np.arange(10, 26, dtype=np.int32)
+    for temperature, top_p, seed in [(0.8, 0.95, 1234), (0.9, 0.999, 77), (1.0, 1.0, 5), (0.7, 0.5, 9),
+                                     (0.8, 0.95, 1234)]:
+        announce(f"small sampled T={temperature} top_p={top_p}")
+        got = small_engine.generate_sampled(prompt, 24, temperature, top_p, seed)
+        np.testing.assert_array_equal(got, _oracle_sampled(small_image, prompt, 24, temperature, top_p, seed))
 
 
 @pytest.mark.parametrize("prefill", [False, True])
