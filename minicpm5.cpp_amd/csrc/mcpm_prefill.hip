@@ -30,6 +30,7 @@
 // Attention per token is the decode kernel at that token's position.
 #include <cstdio>
 #include <cstdlib>
+#include <type_traits>
 
 #include "mcpm_device.h"
 
@@ -194,10 +195,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       const size_t tk = static_cast<size_t>(min(t0 + p / 32, a.n_tok - 1));
       pf[k] = *reinterpret_cast<const u32x4*>(a.xh + tk * K + b * QK_K + (p % 32) * 8);
     }
-    if (tid < TOK) pxd = a.xd[static_cast<size_t>(min(t0 + tid, a.n_tok - 1)) * a.nb + b];
-    if (tid < 2 * TOK)
-      pbs = *reinterpret_cast<const u32x4*>(a.xbs + (static_cast<size_t>(min(t0 + tid / 2, a.n_tok - 1)) * a.nb + b) * 16 +
-                                            (tid & 1) * 8);
+    // every thread loads (threads past the d and bsums slots re-read the
+    // last slot's, unused): no branch among the loads, so the waits for them
+    // count exactly
+    const int td = min(tid, TOK - 1), tb = min(tid, 2 * TOK - 1);
+    pxd = a.xd[static_cast<size_t>(min(t0 + td, a.n_tok - 1)) * a.nb + b];
+    pbs = *reinterpret_cast<const u32x4*>(a.xbs + (static_cast<size_t>(min(t0 + tb / 2, a.n_tok - 1)) * a.nb + b) * 16 +
+                                          (tb & 1) * 8);
   };
   // sB keeps each token's 256 codes as 32 quads of 8 halves, quad 8g + m =
   // elements 64g + 4m .. +3 and 64g + 32 + 4m .. +3 (the B operand of lane
@@ -241,8 +245,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   // Q4_K: hdr = the A row's d/dmin/scales, q[0..1] = its chunk planes 2g and
   // 2g+1; Q6_K: hdr = its scales, q[0..3] = ql planes 4h.., q[4..5] = qh
   // planes 2h..; dr[i] = d (and Q4_K's dmin) of D row 4g+i.
+  // (Q4_K's hdr is the 12 scale bytes only: a dword of a vector load left
+  // unused is a register the compiler reuses, and reusing it waits for every
+  // load in flight)
   struct WRaw {
-    u32x4 hdr;
+    typename std::conditional<WT == 0, u32x3, u32x4>::type hdr;
     u32x4 q[WT == 0 ? 2 : 6];
     uint32_t dr[4];
   };
@@ -256,7 +263,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         w.dr[i] = *reinterpret_cast<const uint16_t*>(a.w.p3 + (static_cast<size_t>(b) * rows + r) * 2);
     }
     if constexpr (WT == 0) {
-      w.hdr = *reinterpret_cast<const u32x4*>(a.w.p1 + (static_cast<size_t>(b) * rows + ra) * 16);
+      w.hdr = *reinterpret_cast<const u32x3*>(a.w.p1 + (static_cast<size_t>(b) * rows + ra) * 16 + 4);
       const uint8_t* q = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
       w.q[0] = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g) * rows * 16);
       w.q[1] = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g + 1) * rows * 16);
@@ -277,10 +284,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   // block, so no copy waits for loads in flight.
   auto block = [&](int b, const WRaw& wc, WRaw& wn) {
     const int buf = b & 1;
-    if (b + 1 < a.nb) {  // in flight during this block's MFMAs
-      fetch(b + 1);
-      load_w(wn, b + 1);
-    }
+    // in flight during this block's MFMAs; issued unconditionally (the last
+    // block loads itself again, unused), so the wait for wc's loads counts
+    // the same number of younger loads on every path and leaves these in
+    // flight
+    const int bn = min(b + 1, a.nb - 1);
+    fetch(bn);
+    load_w(wn, bn);
     if (live) {
     // d (and dmin) of the four D rows of this lane
     float dw[4], dmw[4];
@@ -310,7 +320,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       return __builtin_bit_cast(h8, reinterpret_cast<const u32x4*>(&sB[buf][(16 * n + c16) * BROW])[(8 * g + m) ^ ((g ^ (g >> 1)) & 1)]);
     };
     if constexpr (WT == 0) {
-      const uint32_t s0 = wc.hdr.y, s1 = wc.hdr.z, s2 = wc.hdr.w;
+      const uint32_t s0 = wc.hdr.x, s1 = wc.hdr.y, s2 = wc.hdr.z;
       const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
       const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
       const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
@@ -428,16 +438,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       }
     }
     }  // live
-    // block b+1 into the other buffer, whose last readers passed the previous barrier
-    if (b + 1 < a.nb) stash(buf ^ 1);
+    // block b+1 into the other buffer, whose last readers passed the previous
+    // barrier (after the last block: a copy of it, never read)
+    stash(buf ^ 1);
     __syncthreads();
   };
   WRaw w0, w1;
   load_w(w0, 0);
-  for (int b = 0; b < a.nb; b += 2) {
+  // pairs of blocks with no branch inside, then the odd block
+  int b = 0;
+  for (; b + 1 < a.nb; b += 2) {
     block(b, w0, w1);
-    if (b + 1 < a.nb) block(b + 1, w1, w0);
+    block(b + 1, w1, w0);
   }
+  if (b < a.nb) block(b, w0, w1);
 
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
