@@ -149,20 +149,32 @@ __device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int hh = wave; hh < group; hh += 4) {
     const float* kt = &sK[lane * KS];
+    const float* qh = sQ + hh * HDM;
     float dot[NT];
 #pragma unroll
     for (int k = 0; k < NT; ++k) dot[k] = 0.0f;
-#pragma unroll 4
+    // the next 4 dimensions' K and q are read while this step's fmas run
+    // (the last step reads itself again)
+    f32x4 kc4 = *reinterpret_cast<const f32x4*>(kt), qc4[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) qc4[k] = *reinterpret_cast<const f32x4*>(qh + k * QSZ);
+#pragma unroll 2
     for (int i = 0; i < hd; i += 4) {
-      const f32x4 k4 = *reinterpret_cast<const f32x4*>(kt + i);
+      const int in = min(i + 4, hd - 4);
+      const f32x4 kn4 = *reinterpret_cast<const f32x4*>(kt + in);
+      f32x4 qn4[NT];
+#pragma unroll
+      for (int k = 0; k < NT; ++k) qn4[k] = *reinterpret_cast<const f32x4*>(qh + k * QSZ + in);
 #pragma unroll
       for (int k = 0; k < NT; ++k) {
-        const f32x4 q4 = *reinterpret_cast<const f32x4*>(sQ + k * QSZ + hh * HDM + i);
-        dot[k] = __builtin_fmaf(q4.x, k4.x, dot[k]);
-        dot[k] = __builtin_fmaf(q4.y, k4.y, dot[k]);
-        dot[k] = __builtin_fmaf(q4.z, k4.z, dot[k]);
-        dot[k] = __builtin_fmaf(q4.w, k4.w, dot[k]);
+        dot[k] = __builtin_fmaf(qc4[k].x, kc4.x, dot[k]);
+        dot[k] = __builtin_fmaf(qc4[k].y, kc4.y, dot[k]);
+        dot[k] = __builtin_fmaf(qc4[k].z, kc4.z, dot[k]);
+        dot[k] = __builtin_fmaf(qc4[k].w, kc4.w, dot[k]);
       }
+      kc4 = kn4;
+#pragma unroll
+      for (int k = 0; k < NT; ++k) qc4[k] = qn4[k];
     }
 #pragma unroll
     for (int k = 0; k < NT; ++k) {
@@ -196,8 +208,34 @@ __device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* 
     if (oi < gh) {
       const int hh = oi / hd, i = oi - hh * hd;
       const float* eh = &sE[hh * ATTN_CHUNK];
-#pragma unroll 4
-      for (int j = 0; j < nt_lo; ++j) {
+      // positions in groups of 4, the next group's softmax terms and V
+      // values read while this group's fmas run, then the rest one by one
+      const int n4 = nt_lo & ~3;
+      if (n4 > 0) {
+        auto ld4 = [&](int j0, f32x4 (&e4)[NT], f32x4& v4) {
+#pragma unroll
+          for (int k = 0; k < NT; ++k) e4[k] = *reinterpret_cast<const f32x4*>(eh + k * ESZ + j0);
+          v4 = f32x4{sV[j0 * HDM + i], sV[(j0 + 1) * HDM + i], sV[(j0 + 2) * HDM + i], sV[(j0 + 3) * HDM + i]};
+        };
+        f32x4 ec[NT], vcur;
+        ld4(0, ec, vcur);
+#pragma unroll 2
+        for (int j0 = 0; j0 < n4; j0 += 4) {
+          f32x4 en[NT], vnx;
+          ld4(min(j0 + 4, n4 - 4), en, vnx);
+#pragma unroll
+          for (int k = 0; k < NT; ++k) {
+            acc[k] = __builtin_fmaf(ec[k].x, vcur.x, acc[k]);
+            acc[k] = __builtin_fmaf(ec[k].y, vcur.y, acc[k]);
+            acc[k] = __builtin_fmaf(ec[k].z, vcur.z, acc[k]);
+            acc[k] = __builtin_fmaf(ec[k].w, vcur.w, acc[k]);
+          }
+          vcur = vnx;
+#pragma unroll
+          for (int k = 0; k < NT; ++k) ec[k] = en[k];
+        }
+      }
+      for (int j = n4; j < nt_lo; ++j) {
         const float v = sV[j * HDM + i];
 #pragma unroll
         for (int k = 0; k < NT; ++k) acc[k] = __builtin_fmaf(eh[k * ESZ + j], v, acc[k]);
@@ -258,10 +296,10 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
   constexpr int KS = HDM + 4;
   constexpr int NT = ATTN_TOK;
   constexpr int QSZ = ATTN_MAX_GROUP * HDM, ESZ = ATTN_MAX_GROUP * ATTN_CHUNK;
-  __shared__ float sK[ATTN_CHUNK * KS];
-  __shared__ float sV[ATTN_CHUNK * HDM];
-  __shared__ float sQ[NT * QSZ];
-  __shared__ float sE[NT * ESZ];
+  __shared__ __attribute__((aligned(16))) float sK[ATTN_CHUNK * KS];
+  __shared__ __attribute__((aligned(16))) float sV[ATTN_CHUNK * HDM];
+  __shared__ __attribute__((aligned(16))) float sQ[NT * QSZ];
+  __shared__ __attribute__((aligned(16))) float sE[NT * ESZ];
   __shared__ float2 sMZ[NT * ATTN_MAX_GROUP];
   const int tid = threadIdx.x;
   const int kvh = blockIdx.x, c = blockIdx.y;
