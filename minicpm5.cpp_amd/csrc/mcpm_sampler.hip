@@ -102,16 +102,31 @@ __global__ void __launch_bounds__(SMP_B) k_smp_exp(const float* __restrict__ log
   }
 }
 
-// the sum of the block sums, in order, by thread 0 (block sums staged in LDS)
+// the sum of the block sums, in order, by thread 0 (block sums staged in LDS,
+// zero-padded to a multiple of 16: adding +0.0 to a sum of non-negative
+// terms leaves it unchanged).  The chain reads 16 sums ahead, then runs 16
+// dependent adds.
 __device__ __forceinline__ double smp_total(const double* __restrict__ bs, int nblk, double* sb) {
   double t = 0.0;
   for (int b0 = 0; b0 < nblk; b0 += SMP_B) {
     const int m = min(SMP_B, nblk - b0);
     __syncthreads();
-    if (static_cast<int>(threadIdx.x) < m) sb[threadIdx.x] = bs[b0 + threadIdx.x];
+    sb[threadIdx.x] = static_cast<int>(threadIdx.x) < m ? bs[b0 + threadIdx.x] : 0.0;
     __syncthreads();
-    if (threadIdx.x == 0)
-      for (int k = 0; k < m; ++k) t = t + sb[k];
+    if (threadIdx.x == 0) {
+      const int m16 = (m + 15) & ~15;
+#pragma unroll 1
+      for (int k = 0; k < m16; k += 16) {
+        double2 v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = *reinterpret_cast<const double2*>(sb + k + 2 * q);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          t = t + v[q].x;
+          t = t + v[q].y;
+        }
+      }
+    }
   }
   return t;  // thread 0's value
 }
@@ -119,7 +134,7 @@ __device__ __forceinline__ double smp_total(const double* __restrict__ bs, int n
 __global__ void __launch_bounds__(SMP_B) k_smp_prob(const float* __restrict__ e, int n, const double* __restrict__ bs,
                                                     int nblk, int topp, uint32_t* __restrict__ key,
                                                     int* __restrict__ id, float* __restrict__ p) {
-  __shared__ double sb[SMP_B];
+  __shared__ __attribute__((aligned(16))) double sb[SMP_B];
   __shared__ float s_sum;
   const double t = smp_total(bs, nblk, sb);
   if (threadIdx.x == 0) s_sum = static_cast<float>(t);
@@ -333,7 +348,7 @@ __device__ __forceinline__ double smp_mass(unsigned long long m) { return static
 __global__ void __launch_bounds__(SMP_B) k_smp_prob_hist(const float* __restrict__ e, int n,
                                                          const double* __restrict__ bs, int nblk,
                                                          uint32_t* __restrict__ key, unsigned long long* __restrict__ hm) {
-  __shared__ double sb[SMP_B];
+  __shared__ __attribute__((aligned(16))) double sb[SMP_B];
   __shared__ float s_sum;
   __shared__ uint32_t tk[4][SMP_WTAB];
   __shared__ unsigned long long tm[4][SMP_WTAB];
