@@ -115,6 +115,11 @@ struct GemmArgs {
 
 __device__ __forceinline__ uint32_t h2bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 
+// A raw buffer resource over p (byte offsets up to 2 GB).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), 0x7fffffff, 0x00020000);
+}
+
 // fp16 pair (1024 + byte) from bytes of t picked by sel (0x64 high bytes),
 // minus off: small integers, exact
 __device__ __forceinline__ h2 byte_pair_h(uint32_t t, uint32_t sel, h2 off) {
@@ -179,7 +184,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   if (rg >= n_rg) return;  // uniform in the work group, before any barrier
   const int r0 = (4 * rg + wave) * 16, t0 = tg * TOK;
   const bool live = r0 < a.rows;  // uniform in the wave: a wave past the rows only stages
-  const size_t rows = static_cast<size_t>(a.rows);
   const int ra = min(r0 + c16, a.rows - 1);  // A operand row of this lane
   const int K = a.nb * QK_K;
 
@@ -188,20 +192,31 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   // token t/2's bsums.  Tokens past the end re-read the last one (unused).
   u32x4 pf[PPT], pbs;
   float pxd = 0.0f;
+  // Every load of the block loop is a buffer load: the lane's byte offset is
+  // the same for every block (computed once here) and the block's part is a
+  // scalar offset, so the loop spends no vector instructions on addresses.
+  // (Every buffer here is far below 2 GB; indices are clamped as before.)
+  const __amdgpu_buffer_rsrc_t rxh = gemm_rsrc(a.xh), rxd = gemm_rsrc(a.xd), rxbs = gemm_rsrc(a.xbs);
+  uint32_t vo_pf[PPT];
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int p = tid + 256 * k;
+    const uint32_t tk = static_cast<uint32_t>(min(t0 + p / 32, a.n_tok - 1));
+    vo_pf[k] = (tk * static_cast<uint32_t>(K) + static_cast<uint32_t>(p % 32) * 8) * 2;
+  }
+  // every thread loads (threads past the d and bsums slots re-read the
+  // last slot's, unused): no branch among the loads, so the waits for them
+  // count exactly
+  const int td = min(tid, TOK - 1), tb = min(tid, 2 * TOK - 1);
+  const uint32_t vo_xd = static_cast<uint32_t>(min(t0 + td, a.n_tok - 1)) * static_cast<uint32_t>(a.nb) * 4;
+  const uint32_t vo_xbs =
+      (static_cast<uint32_t>(min(t0 + tb / 2, a.n_tok - 1)) * static_cast<uint32_t>(a.nb) * 16 + (tb & 1) * 8) * 2;
   auto fetch = [&](int b) {
 #pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      const int p = tid + 256 * k;
-      const size_t tk = static_cast<size_t>(min(t0 + p / 32, a.n_tok - 1));
-      pf[k] = *reinterpret_cast<const u32x4*>(a.xh + tk * K + b * QK_K + (p % 32) * 8);
-    }
-    // every thread loads (threads past the d and bsums slots re-read the
-    // last slot's, unused): no branch among the loads, so the waits for them
-    // count exactly
-    const int td = min(tid, TOK - 1), tb = min(tid, 2 * TOK - 1);
-    pxd = a.xd[static_cast<size_t>(min(t0 + td, a.n_tok - 1)) * a.nb + b];
-    pbs = *reinterpret_cast<const u32x4*>(a.xbs + (static_cast<size_t>(min(t0 + tb / 2, a.n_tok - 1)) * a.nb + b) * 16 +
-                                          (tb & 1) * 8);
+    for (int k = 0; k < PPT; ++k)
+      pf[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rxh, vo_pf[k], b * QK_K * 2, 0));
+    pxd = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rxd, vo_xd, b * 4, 0));
+    pbs = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rxbs, vo_xbs, b * 32, 0));
   };
   // sB keeps each token's 256 codes as 32 quads of 8 halves, quad 8g + m =
   // elements 64g + 4m .. +3 and 64g + 32 + 4m .. +3 (the B operand of lane
@@ -253,30 +268,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
     u32x4 q[WT == 0 ? 2 : 6];
     uint32_t dr[4];
   };
+  const __amdgpu_buffer_rsrc_t rw0 = gemm_rsrc(a.w.p0), rw1 = gemm_rsrc(a.w.p1), rw2 = gemm_rsrc(a.w.p2),
+                               rw3 = gemm_rsrc(a.w.p3);
+  const uint32_t rows16 = static_cast<uint32_t>(a.rows) * 16;
+  uint32_t vo_dr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    vo_dr[i] = static_cast<uint32_t>(min(r0 + 4 * g + i, a.rows - 1)) * (WT == 0 ? 16u : 2u);
+  const uint32_t vo_ra = static_cast<uint32_t>(ra) * 16;
   auto load_w = [&](WRaw& w, int b) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const size_t r = static_cast<size_t>(min(r0 + 4 * g + i, a.rows - 1));
-      if constexpr (WT == 0)
-        w.dr[i] = *reinterpret_cast<const uint32_t*>(a.w.p1 + (static_cast<size_t>(b) * rows + r) * 16);
-      else
-        w.dr[i] = *reinterpret_cast<const uint16_t*>(a.w.p3 + (static_cast<size_t>(b) * rows + r) * 2);
-    }
+    const uint32_t ub = static_cast<uint32_t>(b);
     if constexpr (WT == 0) {
-      w.hdr = *reinterpret_cast<const u32x3*>(a.w.p1 + (static_cast<size_t>(b) * rows + ra) * 16 + 4);
-      const uint8_t* q = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
-      w.q[0] = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g) * rows * 16);
-      w.q[1] = *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(2 * g + 1) * rows * 16);
-    } else {
-      const int h = g >> 1;
-      w.hdr = *reinterpret_cast<const u32x4*>(a.w.p2 + (static_cast<size_t>(b) * rows + ra) * 16);
-      const uint8_t* ql = a.w.p0 + (static_cast<size_t>(b) * 8 * rows + ra) * 16;
-      const uint8_t* qh = a.w.p1 + (static_cast<size_t>(b) * 4 * rows + ra) * 16;
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) w.q[cc] = *reinterpret_cast<const u32x4*>(ql + static_cast<size_t>(4 * h + cc) * rows * 16);
+      for (int i = 0; i < 4; ++i) w.dr[i] = __builtin_amdgcn_raw_buffer_load_b32(rw1, vo_dr[i], ub * rows16, 0);
+      w.hdr = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(rw1, vo_ra + 4, ub * rows16, 0));
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        w.q[j] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw0, vo_ra + (2 * g + j) * rows16, ub * 8 * rows16, 0));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w.dr[i] = __builtin_amdgcn_raw_buffer_load_b16(rw3, vo_dr[i], ub * static_cast<uint32_t>(a.rows) * 2, 0);
+      const int h = g >> 1;
+      w.hdr = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw2, vo_ra, ub * rows16, 0));
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        w.q[cc] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw0, vo_ra + (4 * h + cc) * rows16, ub * 8 * rows16, 0));
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc)
-        w.q[4 + cc] = *reinterpret_cast<const u32x4*>(qh + static_cast<size_t>(2 * h + cc) * rows * 16);
+        w.q[4 + cc] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw1, vo_ra + (2 * h + cc) * rows16, ub * 4 * rows16, 0));
     }
   };
   // One block: the weight bytes of block b+1 (into nxt) and its activations
