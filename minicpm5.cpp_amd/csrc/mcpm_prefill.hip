@@ -356,16 +356,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       const u32x4 q0 = wc.q[0], q1 = wc.q[1];
       const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
       // two lane groups at a time: their 2*NT MFMAs are independent and
-      // issue back to back before the first chain step reads a result
+      // issue back to back before the first chain step reads a result; the
+      // next pair's B operands are read from LDS while this pair's run
+      h8 Bc[2][NT];
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        Bc[0][n] = bq(n, 0);
+        Bc[1][n] = bq(n, 1);
+      }
 #pragma unroll
       for (int m = 0; m < 8; m += 2) {
+        h8 Bn[2][NT];
+        if (m + 2 < 8) {
+#pragma unroll
+          for (int n = 0; n < NT; ++n) {
+            Bn[0][n] = bq(n, m + 2);
+            Bn[1][n] = bq(n, m + 3);
+          }
+        }
         const h8 A0 = a_operand_fma(qw[m] & 0x0f0f0f0fu, (qw[m] >> 4) & 0x0f0f0f0fu, sa, sb, ma, mb);
         const h8 A1 = a_operand_fma(qw[m + 1] & 0x0f0f0f0fu, (qw[m + 1] >> 4) & 0x0f0f0f0fu, sa, sb, ma, mb);
         f32x4 D0[NT], D1[NT];
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          D0[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, bq(n, m), zero4, 0, 0, 0);
-          D1[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, bq(n, m + 1), zero4, 0, 0, 0);
+          D0[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bc[0][n], zero4, 0, 0, 0);
+          D1[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bc[1][n], zero4, 0, 0, 0);
+        }
+        if (m + 2 < 8) {
+#pragma unroll
+          for (int n = 0; n < NT; ++n) {
+            Bc[0][n] = Bn[0][n];
+            Bc[1][n] = Bn[1][n];
+          }
         }
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
@@ -430,25 +452,53 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         AC = __builtin_bit_cast(h8, u32x4{g == 0 ? h2bits(pair) : 0u, 0u, 0u, 0u});
       };
       // S + 16*T for lane group m and token tile n: S = sc*ql*x, T = sc*qh*x - 2C
-      auto q6_mfma = [&](int m, int n, const h8& Al, const h8& Ah, const h8& AC, f32x4& S, f32x4& T) {
-        const h8 B = bq(n, m);
-        // bsums 2m, 2m+1 of the token as an fp16 pair (lanes 0..15 use them)
-        const uint32_t bsw = reinterpret_cast<const uint32_t*>(&sBs[buf][(16 * n + c16) * BSROW])[m];
-        const h8 BC = __builtin_bit_cast(h8, u32x4{g == 0 ? bsw : 0u, 0u, 0u, 0u});
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B, zero4, 0, 0, 0);
-        const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC, BC, zero4, 0, 0, 0);  // -2C
-        T = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, B, NC, 0, 0, 0);
+      // the B operand and the bsums pair of lane group m, token tile n
+      struct BOp {
+        h8 B;
+        uint32_t bsw;
       };
+      auto b_op = [&](int m, int n) {
+        // bsums 2m, 2m+1 of the token as an fp16 pair (lanes 0..15 use them)
+        return BOp{bq(n, m), reinterpret_cast<const uint32_t*>(&sBs[buf][(16 * n + c16) * BSROW])[m]};
+      };
+      auto q6_mfma = [&](const BOp& o, const h8& Al, const h8& Ah, const h8& AC, f32x4& S, f32x4& T) {
+        const h8 BC = __builtin_bit_cast(h8, u32x4{g == 0 ? o.bsw : 0u, 0u, 0u, 0u});
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, o.B, zero4, 0, 0, 0);
+        const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC, BC, zero4, 0, 0, 0);  // -2C
+        T = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, o.B, NC, 0, 0, 0);
+      };
+      // the next pair's B operands are read from LDS while this pair's run
+      BOp Oc[2][NT];
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        Oc[0][n] = b_op(0, n);
+        Oc[1][n] = b_op(1, n);
+      }
 #pragma unroll
       for (int m = 0; m < 8; m += 2) {
+        BOp On[2][NT];
+        if (m + 2 < 8) {
+#pragma unroll
+          for (int n = 0; n < NT; ++n) {
+            On[0][n] = b_op(m + 2, n);
+            On[1][n] = b_op(m + 3, n);
+          }
+        }
         h8 Al0, Ah0, AC0, Al1, Ah1, AC1;
         q6_ops(m, Al0, Ah0, AC0);
         q6_ops(m + 1, Al1, Ah1, AC1);
         f32x4 S0[NT], T0[NT], S1[NT], T1[NT];
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          q6_mfma(m, n, Al0, Ah0, AC0, S0[n], T0[n]);
-          q6_mfma(m + 1, n, Al1, Ah1, AC1, S1[n], T1[n]);
+          q6_mfma(Oc[0][n], Al0, Ah0, AC0, S0[n], T0[n]);
+          q6_mfma(Oc[1][n], Al1, Ah1, AC1, S1[n], T1[n]);
+        }
+        if (m + 2 < 8) {
+#pragma unroll
+          for (int n = 0; n < NT; ++n) {
+            Oc[0][n] = On[0][n];
+            Oc[1][n] = On[1][n];
+          }
         }
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
