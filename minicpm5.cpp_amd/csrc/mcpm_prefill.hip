@@ -128,16 +128,12 @@ __device__ __forceinline__ h2 byte_pair_h(uint32_t t, uint32_t sel, h2 off) {
 constexpr uint32_t SEL01 = 0x04010400u, SEL23 = 0x04030402u;
 
 // Eight halves of lane m's A operand: the low (j < 4) and high (j >= 4)
-// K-halves, each four byte values (< 1024) of ta / tb minus off, times sa / sb.
-__device__ __forceinline__ h8 a_operand(uint32_t ta, uint32_t tb, h2 sa, h2 sb, h2 off) {
-  const u32x4 r{h2bits(byte_pair_h(ta, SEL01, off) * sa), h2bits(byte_pair_h(ta, SEL23, off) * sa),
-                h2bits(byte_pair_h(tb, SEL01, off) * sb), h2bits(byte_pair_h(tb, SEL23, off) * sb)};
-  return __builtin_bit_cast(h8, r);
-}
-
-// The same with non-negative scales below 64: (1024 + byte) * s - 1024 * s in
-// one packed fma (ma = -1024 * sa, exact in fp16 for sa <= 63), whose single
-// rounding meets the exact product byte * s (<= 945 for Q4_K).
+// K-halves, each four bytes of ta / tb times sa / sb, as (1024 + byte) * s +
+// m in one packed fma with m = -1024 * s, whose single rounding meets the
+// exact product byte * s.  Q4_K: s = sc <= 63 (m exact in fp16, byte * s <=
+// 945).  Q6_K: s = sc / 64 for signed sc (m = -16 * sc, |byte * sc| <= 1920,
+// so byte * sc / 64 is exact in fp16); its MFMA sums come out divided by 64,
+// exactly, and the chain's scale carries the 64 back.
 __device__ __forceinline__ h2 byte_pair_fma(uint32_t t, uint32_t sel, h2 s, h2 ms) {
   return __builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t, sel)), s, ms);
 }
@@ -335,7 +331,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
     for (int n = 0; n < NT; ++n) {
       xdv[n] = sXd[buf][16 * n + c16];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ds[n][i] = xdv[n] * dw[i];
+      for (int i = 0; i < 4; ++i) ds[n][i] = WT == 0 ? xdv[n] * dw[i] : (xdv[n] * dw[i]) * 64.0f;
     }
     // the B operand of lane group m for token tile n is quad 8g + m of the
     // token's row (at slot (8g + m) ^ sw(g))
@@ -416,9 +412,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       // scales 4g .. 4g+3 (signed bytes) = dword g of the 16 scales
       const uint32_t scw = g == 0 ? scr.x : g == 1 ? scr.y : g == 2 ? scr.z : scr.w;
       const uint32_t scall[4] = {scr.x, scr.y, scr.z, scr.w};
-      h2 sc[4];  // scales 4g .. 4g+3 of this lane's row, as fp16 pairs
+      // scales 4g .. 4g+3 of this lane's row as fp16 pairs sc/64 and -16*sc
+      h2 sc[4], msc[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) sc[k] = splat_h(__builtin_amdgcn_sbfe(static_cast<int>(scw), 8 * k, 8));
+      for (int k = 0; k < 4; ++k) {
+        const int v = __builtin_amdgcn_sbfe(static_cast<int>(scw), 8 * k, 8);
+        const _Float16 h = static_cast<_Float16>(static_cast<float>(v) * 0.015625f);
+        sc[k] = h2{h, h};
+        msc[k] = splat_h(-16 * v);
+      }
       uint32_t lw[16], hw[8];
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {
@@ -439,19 +441,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       // one lane group's operands; two lane groups' MFMAs are issued before
       // either chain reads a result
       auto q6_ops = [&](int m, h8& Al, h8& Ah, h8& AC) {
-        const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)];
-        Al = a_operand((lw[m] >> nib) & 0x0f0f0f0fu, (lw[8 + m] >> nib) & 0x0f0f0f0fu, sa, sb, off1024);
-        Ah = a_operand((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, off1024);
+        const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)], ma = msc[m >> 2], mb = msc[2 + (m >> 2)];
+        Al = a_operand_fma((lw[m] >> nib) & 0x0f0f0f0fu, (lw[8 + m] >> nib) & 0x0f0f0f0fu, sa, sb, ma, mb);
+        Ah = a_operand_fma((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, ma, mb);
         // the offset operand: K entries 0, 1 (lanes 0..15, halves 0, 1) are
-        // -2*sc[2m], -2*sc[2m+1] of this lane's row, the rest zero
+        // -2*sc[2m]/64, -2*sc[2m+1]/64 of this lane's row, the rest zero
         const uint32_t w2 = scall[m >> 1];
         const int lo = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1), 8);
         const int hi = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1) + 8, 8);
-        const h2 pair{static_cast<_Float16>(static_cast<float>(-2 * lo)),
-                      static_cast<_Float16>(static_cast<float>(-2 * hi))};
+        const h2 pair{static_cast<_Float16>(static_cast<float>(lo) * -0.03125f),
+                      static_cast<_Float16>(static_cast<float>(hi) * -0.03125f)};
         AC = __builtin_bit_cast(h8, u32x4{g == 0 ? h2bits(pair) : 0u, 0u, 0u, 0u});
       };
       // S + 16*T for lane group m and token tile n: S = sc*ql*x, T = sc*qh*x - 2C
+      // (each divided by 64, exactly)
       // the B operand and the bsums pair of lane group m, token tile n
       struct BOp {
         h8 B;
