@@ -249,6 +249,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   }
   const h2 off1024{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
   const f32x4 zero4{0.0f, 0.0f, 0.0f, 0.0f};
+  // Q6_K, per lane (K-half g: code fields at bit 4*(g&1) of each byte, and
+  // the high bits' second field 2 above): field masks and the constants of
+  // the scale builds (f = 2^-p for a field at bit p)
+  struct Q6Consts {
+    uint32_t ml, ma0, ma1;
+    h2 sl1, sl2, ol1, ol2, sa1, sa2, oa1, oa2, c1, c2;
+  };
+  const Q6Consts q6c = [&] {
+    const bool odd = (g & 1) != 0;
+    const float fl = odd ? 0.0625f : 1.0f, fa = odd ? 0.015625f : 0.25f;
+    auto hs = [](float v) {
+      const _Float16 h = static_cast<_Float16>(v);
+      return h2{h, h};
+    };
+    return Q6Consts{odd ? 0xf0f0f0f0u : 0x0f0f0f0fu, odd ? 0x30303030u : 0x03030303u, odd ? 0xc0c0c0c0u : 0x0c0c0c0cu,
+                    hs(fl * 0.015625f), hs(-18.0f * fl), hs(-16.0f * fl), hs(18432.0f * fl),
+                    hs(fa * 0.015625f), hs(-18.0f * fa), hs(-16.0f * fa), hs(18432.0f * fa),
+                    hs(-0.03125f), hs(36.0f)};
+  }();
 
   // The weight bytes a block's A operands and row scales are built from,
   // loaded one block ahead like the activations (loaded in their own block,
@@ -407,19 +426,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         for (int i = 0; i < 4; ++i) accm[n][i] = __builtin_fmaf(-(xdv[n] * dmw[i]), DM[i], accm[n][i]);
       }
     } else {
-      const int nib = 4 * (g & 1);
+      // The 16 scales as unsigned bytes u = sc + 128; fp16 (1024 + u) from a
+      // byte permute, then one packed fma gives sc*f/64 = (1024 + u)*f/64 -
+      // 18*f or -16*sc*f = (1024 + u)*(-16*f) + 18432*f, exactly (f a power of
+      // two).  The lane's code fields are masked in place (not shifted): a
+      // field at bit p of its byte reads as code*2^p, and its scale carries
+      // f = 2^-p, so every A entry is still code*sc/64.
       const u32x4 scr = wc.hdr;
-      // scales 4g .. 4g+3 (signed bytes) = dword g of the 16 scales
-      const uint32_t scw = g == 0 ? scr.x : g == 1 ? scr.y : g == 2 ? scr.z : scr.w;
-      const uint32_t scall[4] = {scr.x, scr.y, scr.z, scr.w};
-      // scales 4g .. 4g+3 of this lane's row as fp16 pairs sc/64 and -16*sc
-      h2 sc[4], msc[4];
+      const uint32_t su[4] = {scr.x ^ 0x80808080u, scr.y ^ 0x80808080u, scr.z ^ 0x80808080u, scr.w ^ 0x80808080u};
+      const uint32_t scw = g == 0 ? su[0] : g == 1 ? su[1] : g == 2 ? su[2] : su[3];  // scales 4g .. 4g+3
+      h2 sL[4], oL[4], sA[2], oA[2];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int v = __builtin_amdgcn_sbfe(static_cast<int>(scw), 8 * k, 8);
-        const _Float16 h = static_cast<_Float16>(static_cast<float>(v) * 0.015625f);
-        sc[k] = h2{h, h};
-        msc[k] = splat_h(-16 * v);
+        const h2 hb = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, scw, 0x04000400u | (k << 16) | k));
+        sL[k] = __builtin_elementwise_fma(hb, q6c.sl1, q6c.sl2);
+        oL[k] = __builtin_elementwise_fma(hb, q6c.ol1, q6c.ol2);
+        if (k >= 2) {
+          sA[k - 2] = __builtin_elementwise_fma(hb, q6c.sa1, q6c.sa2);
+          oA[k - 2] = __builtin_elementwise_fma(hb, q6c.oa1, q6c.oa2);
+        }
       }
       uint32_t lw[16], hw[8];
 #pragma unroll
@@ -441,16 +466,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       // one lane group's operands; two lane groups' MFMAs are issued before
       // either chain reads a result
       auto q6_ops = [&](int m, h8& Al, h8& Ah, h8& AC) {
-        const h2 sa = sc[m >> 2], sb = sc[2 + (m >> 2)], ma = msc[m >> 2], mb = msc[2 + (m >> 2)];
-        Al = a_operand_fma((lw[m] >> nib) & 0x0f0f0f0fu, (lw[8 + m] >> nib) & 0x0f0f0f0fu, sa, sb, ma, mb);
-        Ah = a_operand_fma((hw[m] >> nib) & 0x03030303u, (hw[m] >> (nib + 2)) & 0x03030303u, sa, sb, ma, mb);
+        const int ka = m >> 2, kb = 2 + (m >> 2);
+        Al = a_operand_fma(lw[m] & q6c.ml, lw[8 + m] & q6c.ml, sL[ka], sL[kb], oL[ka], oL[kb]);
+        Ah = a_operand_fma(hw[m] & q6c.ma0, hw[m] & q6c.ma1, sL[ka], sA[kb - 2], oL[ka], oA[kb - 2]);
         // the offset operand: K entries 0, 1 (lanes 0..15, halves 0, 1) are
-        // -2*sc[2m]/64, -2*sc[2m+1]/64 of this lane's row, the rest zero
-        const uint32_t w2 = scall[m >> 1];
-        const int lo = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1), 8);
-        const int hi = __builtin_amdgcn_sbfe(static_cast<int>(w2), 16 * (m & 1) + 8, 8);
-        const h2 pair{static_cast<_Float16>(static_cast<float>(lo) * -0.03125f),
-                      static_cast<_Float16>(static_cast<float>(hi) * -0.03125f)};
+        // -2*sc[2m]/64, -2*sc[2m+1]/64 of this lane's row (-sc/32 = (1024 +
+        // u)*(-1/32) + 36), the rest zero
+        const uint32_t sel = 0x04000400u | ((2 * (m & 1) + 1) << 16) | (2 * (m & 1));
+        const h2 hp = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, su[m >> 1], sel));
+        const h2 pair = __builtin_elementwise_fma(hp, q6c.c1, q6c.c2);
         AC = __builtin_bit_cast(h8, u32x4{g == 0 ? h2bits(pair) : 0u, 0u, 0u, 0u});
       };
       // S + 16*T for lane group m and token tile n: S = sc*ql*x, T = sc*qh*x - 2C
