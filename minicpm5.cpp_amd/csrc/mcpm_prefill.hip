@@ -248,6 +248,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
     }
   }
   const h2 off1024{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  const h2 q4c16{static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+  const h2 q4cm64{static_cast<_Float16>(-64.0f), static_cast<_Float16>(-64.0f)};
+  const h2 q4cm1024{static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
   const f32x4 zero4{0.0f, 0.0f, 0.0f, 0.0f};
   // Q6_K, per lane (K-half g: code fields at bit 4*(g&1) of each byte, and
   // the high bits' second field 2 above): field masks and the constants of
@@ -363,11 +366,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
       const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
       const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+      // sc[2g] (low nibbles) and sc[2g+1]/16 (high nibbles, read in place as
+      // 16*code), from fp16 (1024 + sc) by byte permute; the offsets -1024*s
+      // (exact: sc <= 63)
       const uint32_t sw = g < 2 ? sc_lo : sc_hi;
-      const int sh = 16 * (g & 1);
-      const int ia = static_cast<int>((sw >> sh) & 0xffu), ib = static_cast<int>((sw >> (sh + 8)) & 0xffu);
-      const h2 sa = splat_h(ia), sb = splat_h(ib);                  // sc[2g], sc[2g+1]
-      const h2 ma = splat_h(-1024 * ia), mb = splat_h(-1024 * ib);  // exact: sc <= 63
+      const uint32_t bs = 2 * (g & 1);
+      const h2 ha = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, sw, 0x04000400u | (bs << 16) | bs));
+      const h2 hb = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, sw, 0x04000400u | ((bs + 1) << 16) | (bs + 1)));
+      const h2 sa = ha - off1024, sb = __builtin_elementwise_fma(hb, q4c16, q4cm64);
+      const h2 ma = sa * q4cm1024, mb = sb * q4cm1024;
       const u32x4 q0 = wc.q[0], q1 = wc.q[1];
       const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
       // two lane groups at a time: their 2*NT MFMAs are independent and
@@ -389,8 +396,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
             Bn[1][n] = bq(n, m + 3);
           }
         }
-        const h8 A0 = a_operand_fma(qw[m] & 0x0f0f0f0fu, (qw[m] >> 4) & 0x0f0f0f0fu, sa, sb, ma, mb);
-        const h8 A1 = a_operand_fma(qw[m + 1] & 0x0f0f0f0fu, (qw[m + 1] >> 4) & 0x0f0f0f0fu, sa, sb, ma, mb);
+        const h8 A0 = a_operand_fma(qw[m] & 0x0f0f0f0fu, qw[m] & 0xf0f0f0f0u, sa, sb, ma, mb);
+        const h8 A1 = a_operand_fma(qw[m + 1] & 0x0f0f0f0fu, qw[m + 1] & 0xf0f0f0f0u, sa, sb, ma, mb);
         f32x4 D0[NT], D1[NT];
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
