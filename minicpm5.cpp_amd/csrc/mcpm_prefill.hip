@@ -101,6 +101,89 @@ __global__ void __launch_bounds__(256) k_quant_batch(const float* __restrict__ x
   }
 }
 
+// k_quant_batch for up to 4*MAXB blocks per token, with every global load
+// issued at the start: wave w holds blocks w, w+4, ... (lane l: values 4l ..
+// 4l+3 of each, with their gamma or u), RMSNorm's strided partials are read
+// back from an LDS copy of the row (thread t: x[t], x[t+256], ... in order,
+// as block_rms_scale sums them), and each block is quantized from registers.
+// Same operations and outputs as k_quant_batch.
+template <int MAXB>
+__global__ void __launch_bounds__(256) k_quant_batch_r(const float* __restrict__ x, const float* __restrict__ u,
+                                                       int ld_x, const float* __restrict__ gamma, float eps, int dim,
+                                                       int n_valid, int mode, _Float16* __restrict__ xh,
+                                                       float* __restrict__ xd, _Float16* __restrict__ xbs) {
+  __shared__ float red[260];
+  __shared__ __attribute__((aligned(16))) float sx[4 * MAXB * QK_K];
+  const int t = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float* xt = x + static_cast<size_t>(t) * ld_x;
+  const float* ut = u ? u + static_cast<size_t>(t) * ld_x : nullptr;
+  const bool norm = (mode == PRO_NORM_AWAY || mode == PRO_NORM_EVEN);
+  const bool swiglu = mode == QB_SWIGLU;
+  const bool away = (mode == PRO_QUANT_AWAY || mode == PRO_NORM_AWAY || swiglu);
+  const int nb = dim / QK_K;
+  // x (or g), and gamma (or u); blocks past nb re-read the last, and SwiGLU
+  // values at or past n_valid (a multiple of 4, checked by the launch) read
+  // the last valid four, all unused
+  f32x4 xv[MAXB], wv[MAXB];
+#pragma unroll
+  for (int j = 0; j < MAXB; ++j) {
+    int i = min(wave + 4 * j, nb - 1) * QK_K + 4 * lane;
+    if (swiglu) i = min(i, n_valid - 4);
+    xv[j] = *reinterpret_cast<const f32x4*>(xt + i);
+    if (norm) wv[j] = *reinterpret_cast<const f32x4*>(gamma + i);
+    if (swiglu) wv[j] = *reinterpret_cast<const f32x4*>(ut + i);
+  }
+  float rms = 1.0f;
+  if (norm) {
+#pragma unroll
+    for (int j = 0; j < MAXB; ++j)
+      if (wave + 4 * j < nb) *reinterpret_cast<f32x4*>(&sx[(wave + 4 * j) * QK_K + 4 * lane]) = xv[j];
+    __syncthreads();
+    float p = 0.0f;
+    for (int k = 0; k < nb; ++k) {
+      const float v = sx[k * QK_K + tid];
+      p = p + v * v;
+    }
+    rms = block_rms_1sync(p, dim, eps, red);
+  }
+#pragma unroll
+  for (int j = 0; j < MAXB; ++j) {
+    const int b = wave + 4 * j;
+    if (b >= nb) break;
+    float v[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+    const float w4[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (swiglu) {
+        const int i = b * QK_K + 4 * lane + k;
+        float h = 0.0f;
+        if (i < n_valid) {
+          const float g = v[k];
+          const float silu = g / (1.0f + exp_f32(-g));
+          h = silu * w4[k];
+        }
+        v[k] = h;
+      } else if (norm) {
+        v[k] = (v[k] * rms) * w4[k];
+      }
+    }
+    uint32_t packed;
+    float d;
+    int gsum;
+    quant_block_wave(v, away, packed, d, gsum);
+    _Float16* o = xh + static_cast<size_t>(t) * dim + b * QK_K + 4 * lane;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 hv;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      hv[k] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((packed >> (8 * k)) & 0xffu)));
+    *reinterpret_cast<h4*>(o) = hv;
+    if ((lane & 3) == 0) xbs[(static_cast<size_t>(t) * nb + b) * 16 + (lane >> 2)] = static_cast<_Float16>(gsum);
+    if (lane == 0) xd[static_cast<size_t>(t) * nb + b] = d;
+  }
+}
+
 // ------------------------------------------------------------------ GEMM ----
 struct GemmArgs {
   WView w;
@@ -501,45 +584,50 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC, BC, zero4, 0, 0, 0);  // -2C
         T = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, o.B, NC, 0, 0, 0);
       };
-      // the next pair's B operands are read from LDS while this pair's run
-      BOp Oc[2][NT];
+      // Lane groups in steps of LG: pairs with one token tile (their six
+      // MFMAs independent), one at a time with two (registers: two tiles'
+      // accumulators, sums and B operands).  The next step's B operands are
+      // read from LDS while this step's MFMAs run.
+      constexpr int LG = NT >= 2 ? 1 : 2;
+      BOp Oc[LG][NT];
 #pragma unroll
-      for (int n = 0; n < NT; ++n) {
-        Oc[0][n] = b_op(0, n);
-        Oc[1][n] = b_op(1, n);
+      for (int j = 0; j < LG; ++j) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) Oc[j][n] = b_op(j, n);
       }
 #pragma unroll
-      for (int m = 0; m < 8; m += 2) {
-        BOp On[2][NT];
-        if (m + 2 < 8) {
+      for (int m = 0; m < 8; m += LG) {
+        BOp On[LG][NT];
+        if (m + LG < 8) {
 #pragma unroll
-          for (int n = 0; n < NT; ++n) {
-            On[0][n] = b_op(m + 2, n);
-            On[1][n] = b_op(m + 3, n);
+          for (int j = 0; j < LG; ++j) {
+#pragma unroll
+            for (int n = 0; n < NT; ++n) On[j][n] = b_op(m + LG + j, n);
           }
         }
-        h8 Al0, Ah0, AC0, Al1, Ah1, AC1;
-        q6_ops(m, Al0, Ah0, AC0);
-        q6_ops(m + 1, Al1, Ah1, AC1);
-        f32x4 S0[NT], T0[NT], S1[NT], T1[NT];
+        h8 Al[LG], Ah[LG], AC[LG];
+#pragma unroll
+        for (int j = 0; j < LG; ++j) q6_ops(m + j, Al[j], Ah[j], AC[j]);
+        f32x4 S[LG][NT], T[LG][NT];
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          q6_mfma(Oc[0][n], Al0, Ah0, AC0, S0[n], T0[n]);
-          q6_mfma(Oc[1][n], Al1, Ah1, AC1, S1[n], T1[n]);
-        }
-        if (m + 2 < 8) {
 #pragma unroll
-          for (int n = 0; n < NT; ++n) {
-            Oc[0][n] = On[0][n];
-            Oc[1][n] = On[1][n];
+          for (int j = 0; j < LG; ++j) q6_mfma(Oc[j][n], Al[j], Ah[j], AC[j], S[j][n], T[j][n]);
+        }
+        if (m + LG < 8) {
+#pragma unroll
+          for (int j = 0; j < LG; ++j) {
+#pragma unroll
+            for (int n = 0; n < NT; ++n) Oc[j][n] = On[j][n];
           }
         }
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            acc[n][m][i] = __builtin_fmaf(ds[n][i], __builtin_fmaf(16.0f, T0[n][i], S0[n][i]), acc[n][m][i]);
-            acc[n][m + 1][i] = __builtin_fmaf(ds[n][i], __builtin_fmaf(16.0f, T1[n][i], S1[n][i]), acc[n][m + 1][i]);
+#pragma unroll
+            for (int j = 0; j < LG; ++j)
+              acc[n][m + j][i] = __builtin_fmaf(ds[n][i], __builtin_fmaf(16.0f, T[j][n][i], S[j][n][i]), acc[n][m + j][i]);
           }
         }
       }
@@ -666,8 +754,18 @@ hipError_t launch_embed_batch(const WView& w, const int* tokens, int n_tok, int 
 hipError_t launch_quant_batch(const float* x, const float* u, int ld_x, const float* gamma, float eps, int dim,
                               int n_valid, int mode, int n_tok, QuantBatch q, hipStream_t s) {
   if (dim % QK_K) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_quant_batch, dim3(n_tok), dim3(256), 0, s, x, u, ld_x, gamma, eps, dim, n_valid, mode,
-                     q.xh, q.xd, q.xbs);
+  // rows of up to 24 blocks load everything up front (k_quant_batch_r)
+  const int nb = dim / QK_K;
+  const bool up_front = ld_x % 4 == 0 && (mode != QB_SWIGLU || (n_valid >= 4 && n_valid % 4 == 0 && n_valid <= ld_x));
+  if (up_front && nb <= 12)
+    hipLaunchKernelGGL(k_quant_batch_r<3>, dim3(n_tok), dim3(256), 0, s, x, u, ld_x, gamma, eps, dim, n_valid, mode,
+                       q.xh, q.xd, q.xbs);
+  else if (up_front && nb <= 24)
+    hipLaunchKernelGGL(k_quant_batch_r<6>, dim3(n_tok), dim3(256), 0, s, x, u, ld_x, gamma, eps, dim, n_valid, mode,
+                       q.xh, q.xd, q.xbs);
+  else
+    hipLaunchKernelGGL(k_quant_batch, dim3(n_tok), dim3(256), 0, s, x, u, ld_x, gamma, eps, dim, n_valid, mode,
+                       q.xh, q.xd, q.xbs);
   return hipGetLastError();
 }
 
