@@ -715,19 +715,40 @@ __global__ void __launch_bounds__(256) k_quant_batch_attn(const float* __restric
     const int h = i0 / hd, d0 = i0 - h * hd;
     const float2* mz = part_mz + t * tok_stride_mz + static_cast<size_t>(h) * max_chunks;
     const float* o = part_o + t * tok_stride_o + static_cast<size_t>(h) * max_chunks * hd + d0;
+    // the chunks' partials in batches of CB whose loads are issued together
+    // (indices past the last chunk re-read it: the max is unchanged, and the
+    // combine skips them)
+    constexpr int CB = 8;
     float m = mz[0].x;
-    for (int c = 1; c < nch; ++c) m = fmaxf(m, mz[c].x);
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+      float mv[CB];
+#pragma unroll
+      for (int k = 0; k < CB; ++k) mv[k] = mz[min(c0 + k, nch - 1)].x;
+#pragma unroll
+      for (int k = 0; k < CB; ++k) m = fmaxf(m, mv[k]);
+    }
     float Z = 0.0f;
     float O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c = 0; c < nch; ++c) {
-      const float2 zc = mz[c];
-      const f32x4 oc = *reinterpret_cast<const f32x4*>(o + static_cast<size_t>(c) * hd);
-      const float f = exp_f32(zc.x - m);
-      Z = __builtin_fmaf(zc.y, f, Z);
-      O[0] = __builtin_fmaf(oc.x, f, O[0]);
-      O[1] = __builtin_fmaf(oc.y, f, O[1]);
-      O[2] = __builtin_fmaf(oc.z, f, O[2]);
-      O[3] = __builtin_fmaf(oc.w, f, O[3]);
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+      float2 zc[CB];
+      f32x4 oc[CB];
+#pragma unroll
+      for (int k = 0; k < CB; ++k) {
+        const int c = min(c0 + k, nch - 1);
+        zc[k] = mz[c];
+        oc[k] = *reinterpret_cast<const f32x4*>(o + static_cast<size_t>(c) * hd);
+      }
+#pragma unroll
+      for (int k = 0; k < CB; ++k) {
+        if (c0 + k < nch) {
+          const float f = exp_f32(zc[k].x - m);
+          Z = __builtin_fmaf(zc[k].y, f, Z);
+          O[0] = __builtin_fmaf(oc[k].x, f, O[0]);
+          O[1] = __builtin_fmaf(oc[k].y, f, O[1]);
+          O[2] = __builtin_fmaf(oc[k].z, f, O[2]);
+          O[3] = __builtin_fmaf(oc[k].w, f, O[3]);
+        }
+      }
     }
     float v[4];
 #pragma unroll
