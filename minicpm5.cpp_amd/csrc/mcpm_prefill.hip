@@ -244,11 +244,16 @@ template <int WT, int NT, int OCC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) k_gemm_q8k(const GemmArgs a) {
   constexpr int TOK = 16 * NT;        // tokens of the work group's tile
   constexpr int BROW = QK_K + 8;      // halves per token row of sB (padded: rows 132 dwords apart)
-  constexpr int BSROW = 24;           // halves per token of sBs (16 used; rows 12 dwords apart)
+  // halves per token of sBs.  Q4_K: the 16 bsums (rows 12 dwords apart).
+  // Q6_K: eight 16-byte records, record m = (bsums 2m, 2m+1 as an fp16
+  // pair, then zeros): lane group m's offset B operand read whole; a zero
+  // row after the tokens serves the lanes whose K entries are all zero.
+  constexpr int BSROW = WT == 0 ? 24 : 64;
+  constexpr int BSZERO = WT == 0 ? 0 : 64;
   constexpr int PPT = TOK * 32 / 256; // 16-byte pieces of a block's codes per thread
   __shared__ __attribute__((aligned(16))) _Float16 sB[2][TOK * BROW];
   __shared__ float sXd[2][TOK];
-  __shared__ __attribute__((aligned(16))) _Float16 sBs[2][TOK * BSROW];
+  __shared__ __attribute__((aligned(16))) _Float16 sBs[2][TOK * BSROW + BSZERO];
   const int tid = threadIdx.x, wave = tid >> 6;
   const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int n_rt = (a.rows + 15) >> 4;
@@ -314,8 +319,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       *reinterpret_cast<uint2*>(row + ((8 * gq + mq + 1) ^ sw) * 8) = uint2{pf[k].z, pf[k].w};
     }
     if (tid < TOK) sXd[buf][tid] = pxd;
-    if (tid < 2 * TOK) *reinterpret_cast<u32x4*>(&sBs[buf][(tid / 2) * BSROW + (tid & 1) * 8]) = pbs;
+    if (tid < 2 * TOK) {
+      if constexpr (WT == 0) {
+        *reinterpret_cast<u32x4*>(&sBs[buf][(tid / 2) * BSROW + (tid & 1) * 8]) = pbs;
+      } else {
+        const uint32_t pw[4] = {pbs.x, pbs.y, pbs.z, pbs.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<uint32_t*>(&sBs[buf][(tid / 2) * BSROW + (4 * (tid & 1) + j) * 8]) = pw[j];
+      }
+    }
   };
+  if constexpr (WT == 1) {
+    // the records' zero dwords and the zero row, written once (the stash
+    // writes only the pairs)
+    for (int i = tid; i < 2 * (TOK * BSROW + BSZERO) / 8; i += 256)
+      reinterpret_cast<u32x4*>(&sBs[0][0])[i] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+  }
   fetch(0);
   stash(0);
   __syncthreads();
@@ -555,33 +576,36 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       }
       // one lane group's operands; two lane groups' MFMAs are issued before
       // either chain reads a result
-      auto q6_ops = [&](int m, h8& Al, h8& Ah, h8& AC) {
+      auto q6_ops = [&](int m, h8& Al, h8& Ah, uint32_t& AC) {
         const int ka = m >> 2, kb = 2 + (m >> 2);
         Al = a_operand_fma(lw[m] & q6c.ml, lw[8 + m] & q6c.ml, sL[ka], sL[kb], oL[ka], oL[kb]);
         Ah = a_operand_fma(hw[m] & q6c.ma0, hw[m] & q6c.ma1, sL[ka], sA[kb - 2], oL[ka], oA[kb - 2]);
-        // the offset operand: K entries 0, 1 (lanes 0..15, halves 0, 1) are
-        // -2*sc[2m]/64, -2*sc[2m+1]/64 of this lane's row (-sc/32 = (1024 +
-        // u)*(-1/32) + 36), the rest zero
+        // the offset operand's first K pair: -2*sc[2m]/64, -2*sc[2m+1]/64 of
+        // this lane's row (-sc/32 = (1024 + u)*(-1/32) + 36)
         const uint32_t sel = 0x04000400u | ((2 * (m & 1) + 1) << 16) | (2 * (m & 1));
         const h2 hp = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, su[m >> 1], sel));
-        const h2 pair = __builtin_elementwise_fma(hp, q6c.c1, q6c.c2);
-        AC = __builtin_bit_cast(h8, u32x4{g == 0 ? h2bits(pair) : 0u, 0u, 0u, 0u});
+        AC = h2bits(__builtin_elementwise_fma(hp, q6c.c1, q6c.c2));
       };
       // S + 16*T for lane group m and token tile n: S = sc*ql*x, T = sc*qh*x - 2C
       // (each divided by 64, exactly)
       // the B operand and the bsums pair of lane group m, token tile n
       struct BOp {
         h8 B;
-        uint32_t bsw;
+        h8 BC;  // record m of the token (lanes 0..15), the zero row (the others)
       };
       auto b_op = [&](int m, int n) {
-        // bsums 2m, 2m+1 of the token as an fp16 pair (lanes 0..15 use them)
-        return BOp{bq(n, m), reinterpret_cast<const uint32_t*>(&sBs[buf][(16 * n + c16) * BSROW])[m]};
+        const int row = g == 0 ? (16 * n + c16) * BSROW : TOK * BSROW;
+        return BOp{bq(n, m), *reinterpret_cast<const h8*>(&sBs[buf][row + m * 8])};
       };
-      auto q6_mfma = [&](const BOp& o, const h8& Al, const h8& Ah, const h8& AC, f32x4& S, f32x4& T) {
-        const h8 BC = __builtin_bit_cast(h8, u32x4{g == 0 ? o.bsw : 0u, 0u, 0u, 0u});
+      // The offset operand is Al with its first dword replaced by the pair
+      // (formed after the S MFMAs have read Al): its other K entries meet
+      // zeros of BC, and lanes 16..63 read an all-zero BC, so NC is the
+      // offset alone.
+      auto q6_mfma = [&](const BOp& o, const h8& Al, const h8& Ah, uint32_t AC, f32x4& S, f32x4& T) {
         S = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, o.B, zero4, 0, 0, 0);
-        const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(AC, BC, zero4, 0, 0, 0);  // -2C
+        const u32x4 al = __builtin_bit_cast(u32x4, Al);
+        const h8 A2 = __builtin_bit_cast(h8, u32x4{AC, al.y, al.z, al.w});
+        const f32x4 NC = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, o.BC, zero4, 0, 0, 0);  // -2C
         T = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, o.B, NC, 0, 0, 0);
       };
       // Lane groups in steps of LG: pairs with one token tile (their six
@@ -605,7 +629,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
             for (int n = 0; n < NT; ++n) On[j][n] = b_op(m + LG + j, n);
           }
         }
-        h8 Al[LG], Ah[LG], AC[LG];
+        h8 Al[LG], Ah[LG];
+        uint32_t AC[LG];
 #pragma unroll
         for (int j = 0; j < LG; ++j) q6_ops(m + j, Al[j], Ah[j], AC[j]);
         f32x4 S[LG][NT], T[LG][NT];
