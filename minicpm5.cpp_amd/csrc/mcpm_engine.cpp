@@ -543,8 +543,14 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
     float* vc = e->vc + static_cast<size_t>(l) * e->max_seq * kvd;
     const int nbd = c.dim / QK_K;
     MCPM_HIP(launch_quant_batch(b.x, nullptr, c.dim, L.attn_norm, c.eps, c.dim, c.dim, PRO_NORM_AWAY, n, qb, s));
-    MCPM_HIP(launch_gemm_q8k(view_of(L.wq), qd, nbd, n, qb, b.qkv, nqkv, false, s));
-    MCPM_HIP(launch_gemm_q8k(view_of(L.wk), kvd, nbd, n, qb, b.qkv + qd, nqkv, false, s));
+    // q and k in one launch when they share a type (q's rows a multiple of 64)
+    const WView wq = view_of(L.wq), wk = view_of(L.wk), wg = view_of(L.wg), wu = view_of(L.wu);
+    if (wq.type == wk.type && qd % 64 == 0) {
+      MCPM_HIP(launch_gemm_q8k(wq, qd, nbd, n, qb, b.qkv, nqkv, false, s, &wk, kvd, b.qkv + qd));
+    } else {
+      MCPM_HIP(launch_gemm_q8k(wq, qd, nbd, n, qb, b.qkv, nqkv, false, s));
+      MCPM_HIP(launch_gemm_q8k(wk, kvd, nbd, n, qb, b.qkv + qd, nqkv, false, s));
+    }
     MCPM_HIP(launch_gemm_q8k(view_of(L.wv), kvd, nbd, n, qb, b.qkv + qd + kvd, nqkv, false, s));
     MCPM_HIP(launch_rope_kv_batch(b.qkv, n, qd, kvd, c.head_dim, e->rope, pos0, b.q, kc, vc, s));
     if (l == c.n_layers - 1) break;  // nothing after the last K/V rows reaches the cache
@@ -553,8 +559,12 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
     MCPM_HIP(launch_quant_batch_attn(part, tok_o, tok_mz, pos0, n, c.n_heads, c.head_dim, e->max_chunks, qb, s));
     MCPM_HIP(launch_gemm_q8k(view_of(L.wo), c.dim, qd / QK_K, n, qb, b.x, c.dim, true, s));
     MCPM_HIP(launch_quant_batch(b.x, nullptr, c.dim, L.ffn_norm, c.eps, c.dim, c.dim, PRO_NORM_AWAY, n, qb, s));
-    MCPM_HIP(launch_gemm_q8k(view_of(L.wg), c.ffn, nbd, n, qb, b.g, c.ffn, false, s));
-    MCPM_HIP(launch_gemm_q8k(view_of(L.wu), c.ffn, nbd, n, qb, b.u, c.ffn, false, s));
+    if (wg.type == wu.type && c.ffn % 64 == 0) {
+      MCPM_HIP(launch_gemm_q8k(wg, c.ffn, nbd, n, qb, b.g, c.ffn, false, s, &wu, c.ffn, b.u));
+    } else {
+      MCPM_HIP(launch_gemm_q8k(wg, c.ffn, nbd, n, qb, b.g, c.ffn, false, s));
+      MCPM_HIP(launch_gemm_q8k(wu, c.ffn, nbd, n, qb, b.u, c.ffn, false, s));
+    }
     MCPM_HIP(launch_quant_batch_swiglu(b.g, b.u, c.ffn, c.ffn, c.ffn_pad, n, qb, s));
     MCPM_HIP(launch_gemm_q8k(view_of(L.wd), c.dim, c.ffn_pad / QK_K, n, qb, b.x, c.dim, true, s));
   }

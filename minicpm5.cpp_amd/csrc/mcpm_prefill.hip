@@ -28,6 +28,7 @@
 //  * Q4_K's min sum (sum over sub-blocks of mn * pair-sum of bsums) is one
 //    more MFMA: A = mn[k/2] for k < 16, B = bsums[k].
 // Attention per token is the decode kernel at that token's position.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <type_traits>
@@ -194,6 +195,12 @@ struct GemmArgs {
   float* out;           // out[t*ld_out + r]
   int ld_out;
   int add;              // 1: out += v (residual), 0: out = v
+  // an optional second matrix of the same type and blocks per row on the
+  // same activations (rows2 > 0, rows a multiple of 64): the launch's rows
+  // rows .. rows+rows2-1 are its rows, written to out2 (same ld_out)
+  WView w2;
+  int rows2;
+  float* out2;
 };
 
 __device__ __forceinline__ uint32_t h2bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -256,7 +263,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   __shared__ __attribute__((aligned(16))) _Float16 sBs[2][TOK * BSROW + BSZERO];
   const int tid = threadIdx.x, wave = tid >> 6;
   const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
-  const int n_rt = (a.rows + 15) >> 4;
+  const int n_rt = (a.rows + a.rows2 + 15) >> 4;
   const int n_rg = (n_rt + 3) >> 2;
   // XCD-aware tiles: work group b runs on XCD b % 8, which takes the row
   // groups rg = xcd + 8j only, for every token tile, so each XCD's L2 keeps
@@ -266,9 +273,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   const int cmax = (n_rg + 7) >> 3;
   const int rg = xcd + 8 * (loc % cmax), tg = loc / cmax;
   if (rg >= n_rg) return;  // uniform in the work group, before any barrier
-  const int r0 = (4 * rg + wave) * 16, t0 = tg * TOK;
-  const bool live = r0 < a.rows;  // uniform in the wave: a wave past the rows only stages
-  const int ra = min(r0 + c16, a.rows - 1);  // A operand row of this lane
+  // the work group's matrix (its 64 rows lie in one: the first has a
+  // multiple of 64 rows)
+  const bool second = a.rows2 > 0 && 64 * rg >= a.rows;
+  const WView W = second ? a.w2 : a.w;
+  const int rows = second ? a.rows2 : a.rows;
+  float* const out = second ? a.out2 : a.out;
+  const int r0 = (4 * rg + wave) * 16 - (second ? a.rows : 0), t0 = tg * TOK;
+  const bool live = r0 < rows;  // uniform in the wave: a wave past the rows only stages
+  const int ra = min(r0 + c16, rows - 1);  // A operand row of this lane
   const int K = a.nb * QK_K;
 
   // staging of block b: piece p = tid + 256k is 16 bytes (p % 32) of token
@@ -390,13 +403,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
     u32x4 q[WT == 0 ? 2 : 6];
     uint32_t dr[4];
   };
-  const __amdgpu_buffer_rsrc_t rw0 = gemm_rsrc(a.w.p0), rw1 = gemm_rsrc(a.w.p1), rw2 = gemm_rsrc(a.w.p2),
-                               rw3 = gemm_rsrc(a.w.p3);
-  const uint32_t rows16 = static_cast<uint32_t>(a.rows) * 16;
+  const __amdgpu_buffer_rsrc_t rw0 = gemm_rsrc(W.p0), rw1 = gemm_rsrc(W.p1), rw2 = gemm_rsrc(W.p2),
+                               rw3 = gemm_rsrc(W.p3);
+  const uint32_t rows16 = static_cast<uint32_t>(rows) * 16;
   uint32_t vo_dr[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    vo_dr[i] = static_cast<uint32_t>(min(r0 + 4 * g + i, a.rows - 1)) * (WT == 0 ? 16u : 2u);
+    vo_dr[i] = static_cast<uint32_t>(min(r0 + 4 * g + i, rows - 1)) * (WT == 0 ? 16u : 2u);
   const uint32_t vo_ra = static_cast<uint32_t>(ra) * 16;
   auto load_w = [&](WRaw& w, int b) {
     const uint32_t ub = static_cast<uint32_t>(b);
@@ -411,7 +424,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        w.dr[i] = __builtin_amdgcn_raw_buffer_load_b16(rw3, vo_dr[i], ub * static_cast<uint32_t>(a.rows) * 2, 0);
+        w.dr[i] = __builtin_amdgcn_raw_buffer_load_b16(rw3, vo_dr[i], ub * static_cast<uint32_t>(rows) * 2, 0);
       const int h = g >> 1;
       w.hdr = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw2, vo_ra, ub * rows16, 0));
 #pragma unroll
@@ -682,8 +695,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
       float v = ((acc[n][0][i] + acc[n][4][i]) + (acc[n][2][i] + acc[n][6][i])) +
                 ((acc[n][1][i] + acc[n][5][i]) + (acc[n][3][i] + acc[n][7][i]));
       if constexpr (WT == 0) v = v + accm[n][i];
-      if (r < a.rows && t < a.n_tok) {
-        float* o = a.out + static_cast<size_t>(t) * a.ld_out + r;
+      if (r < rows && t < a.n_tok) {
+        float* o = out + static_cast<size_t>(t) * a.ld_out + r;
         *o = a.add ? *o + v : v;
       }
     }
@@ -821,9 +834,12 @@ hipError_t launch_quant_batch_swiglu(const float* g, const float* u, int ld, int
 }
 
 hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const QuantBatch& q, float* out, int ld_out,
-                           bool add, hipStream_t s) {
+                           bool add, hipStream_t s, const WView* w2, int rows2, float* out2) {
   if (w.type != MCPM_TYPE_Q4_K && w.type != MCPM_TYPE_Q6_K) return hipErrorInvalidValue;
-  GemmArgs a{w, rows, nb, n_tok, q.xh, q.xd, q.xbs, out, ld_out, add ? 1 : 0};
+  if (rows2 > 0 && (!w2 || !out2 || w2->type != w.type || rows % 64)) return hipErrorInvalidValue;
+  GemmArgs a{w, rows, nb, n_tok, q.xh, q.xd, q.xbs, out, ld_out, add ? 1 : 0, rows2 > 0 ? *w2 : WView{},
+             std::max(rows2, 0), out2};
+  rows += std::max(rows2, 0);
   // token tiles per wave and waves per SIMD (MCPM_PREFILL_NT=1|2|4 and
   // MCPM_PREFILL_OCC=1|2 override, tuning aids; "a,b" sets Q4_K a, Q6_K b)
   struct Pair {
