@@ -40,7 +40,7 @@ struct TimedPair {
 struct PrefillBufs {
   int cap = 0, max_chunks = 0;
   int* tokens = nullptr;
-  float *x = nullptr, *qkv = nullptr, *q = nullptr, *g = nullptr, *u = nullptr, *part = nullptr;
+  float *x = nullptr, *q = nullptr, *g = nullptr, *u = nullptr, *part = nullptr;
   _Float16 *xh = nullptr, *xbs = nullptr;
   float* xd = nullptr;
 };
@@ -124,7 +124,7 @@ void drop_graph(mcpm_engine* e) {
 }
 
 void free_prefill(PrefillBufs& b) {
-  for (void* p : {static_cast<void*>(b.tokens), static_cast<void*>(b.x), static_cast<void*>(b.qkv),
+  for (void* p : {static_cast<void*>(b.tokens), static_cast<void*>(b.x),
                   static_cast<void*>(b.q), static_cast<void*>(b.g),
                   static_cast<void*>(b.u), static_cast<void*>(b.part), static_cast<void*>(b.xh),
                   static_cast<void*>(b.xbs), static_cast<void*>(b.xd)})
@@ -501,12 +501,11 @@ int ensure_prefill(mcpm_engine* e, int cap) {
   if (cap <= b.cap && b.max_chunks == e->max_chunks) return MCPM_OK;
   free_prefill(b);
   const mcpm_model_config& c = e->cfg;
-  const size_t qd = static_cast<size_t>(c.n_heads) * c.head_dim, kvd = static_cast<size_t>(c.n_kv_heads) * c.head_dim;
+  const size_t qd = static_cast<size_t>(c.n_heads) * c.head_dim;
   const size_t kmax = std::max<size_t>({static_cast<size_t>(c.dim), qd, static_cast<size_t>(c.ffn_pad)});
   const size_t n = static_cast<size_t>(cap);
   int rc = alloc_dev(reinterpret_cast<void**>(&b.tokens), n * sizeof(int));
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.x), n * c.dim * 4);
-  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.qkv), n * (qd + 2 * kvd) * 4);
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.q), n * qd * 4);
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.g), n * c.ffn * 4);
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&b.u), n * c.ffn * 4);
@@ -530,7 +529,7 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
   const mcpm_model_config& c = e->cfg;
   hipStream_t s = e->ctx->stream;
   PrefillBufs& b = e->pf;
-  const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim, nqkv = qd + 2 * kvd;
+  const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
   const QuantBatch qb{b.xh, b.xd, b.xbs};
   MCPM_HIP(hipMemcpyAsync(b.tokens, tokens, n * sizeof(int), hipMemcpyHostToDevice, s));
   MCPM_HIP(launch_embed_batch(view_of(e->embd), b.tokens, n, c.dim, b.x, s));
@@ -543,16 +542,20 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
     float* vc = e->vc + static_cast<size_t>(l) * e->max_seq * kvd;
     const int nbd = c.dim / QK_K;
     MCPM_HIP(launch_quant_batch(b.x, nullptr, c.dim, L.attn_norm, c.eps, c.dim, c.dim, PRO_NORM_AWAY, n, qb, s));
-    // q and k in one launch when they share a type (q's rows a multiple of 64)
+    // q rotated into b.q and k rotated into the cache rows by the GEMM's
+    // RoPE epilogue, in one launch when q and k share a type (q's rows a
+    // multiple of 64); v straight into the cache rows
     const WView wq = view_of(L.wq), wk = view_of(L.wk), wg = view_of(L.wg), wu = view_of(L.wu);
+    const GemmRope rp{e->rope, c.head_dim, pos0};
+    float* krows = kc + static_cast<size_t>(pos0) * kvd;
+    float* vrows = vc + static_cast<size_t>(pos0) * kvd;
     if (wq.type == wk.type && qd % 64 == 0) {
-      MCPM_HIP(launch_gemm_q8k(wq, qd, nbd, n, qb, b.qkv, nqkv, false, s, &wk, kvd, b.qkv + qd));
+      MCPM_HIP(launch_gemm_q8k(wq, qd, nbd, n, qb, b.q, qd, false, s, &wk, kvd, krows, kvd, &rp));
     } else {
-      MCPM_HIP(launch_gemm_q8k(wq, qd, nbd, n, qb, b.qkv, nqkv, false, s));
-      MCPM_HIP(launch_gemm_q8k(wk, kvd, nbd, n, qb, b.qkv + qd, nqkv, false, s));
+      MCPM_HIP(launch_gemm_q8k(wq, qd, nbd, n, qb, b.q, qd, false, s, nullptr, 0, nullptr, 0, &rp));
+      MCPM_HIP(launch_gemm_q8k(wk, kvd, nbd, n, qb, krows, kvd, false, s, nullptr, 0, nullptr, 0, &rp));
     }
-    MCPM_HIP(launch_gemm_q8k(view_of(L.wv), kvd, nbd, n, qb, b.qkv + qd + kvd, nqkv, false, s));
-    MCPM_HIP(launch_rope_kv_batch(b.qkv, n, qd, kvd, c.head_dim, e->rope, pos0, b.q, kc, vc, s));
+    MCPM_HIP(launch_gemm_q8k(view_of(L.wv), kvd, nbd, n, qb, vrows, kvd, false, s));
     if (l == c.n_layers - 1) break;  // nothing after the last K/V rows reaches the cache
     MCPM_HIP(launch_attention_batch(b.q, kc, vc, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part, tok_o,
                                     tok_mz, pos0, n, s));
@@ -560,7 +563,7 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
     MCPM_HIP(launch_gemm_q8k(view_of(L.wo), c.dim, qd / QK_K, n, qb, b.x, c.dim, true, s));
     MCPM_HIP(launch_quant_batch(b.x, nullptr, c.dim, L.ffn_norm, c.eps, c.dim, c.dim, PRO_NORM_AWAY, n, qb, s));
     if (wg.type == wu.type && c.ffn % 64 == 0) {
-      MCPM_HIP(launch_gemm_q8k(wg, c.ffn, nbd, n, qb, b.g, c.ffn, false, s, &wu, c.ffn, b.u));
+      MCPM_HIP(launch_gemm_q8k(wg, c.ffn, nbd, n, qb, b.g, c.ffn, false, s, &wu, c.ffn, b.u, c.ffn));
     } else {
       MCPM_HIP(launch_gemm_q8k(wg, c.ffn, nbd, n, qb, b.g, c.ffn, false, s));
       MCPM_HIP(launch_gemm_q8k(wu, c.ffn, nbd, n, qb, b.u, c.ffn, false, s));

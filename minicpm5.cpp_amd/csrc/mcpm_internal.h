@@ -316,12 +316,17 @@ hipError_t launch_quant_batch(const float* x, const float* u, int ld_x, const fl
                               int n_valid, int mode, int n_tok, QuantBatch q, hipStream_t s);
 hipError_t launch_quant_batch_swiglu(const float* g, const float* u, int ld, int n_valid, int dim, int n_tok,
                                      QuantBatch q, hipStream_t s);
-// w2 / rows2 / out2: a second matrix of w's type on the same activations in
-// the same launch (rows % 64 == 0), rows written to out2 with ld_out.
+// RoPE applied to a GEMM's row pairs before they are stored: the (cos, sin)
+// table (head_dim/2 pairs per position), token t at position pos0 + t.
+struct GemmRope {
+  const float2* table;
+  int head_dim, pos0;
+};
+// w2 / rows2 / out2 / ld_out2: a second matrix of w's type on the same
+// activations in the same launch (rows % 64 == 0).
 hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const QuantBatch& q, float* out, int ld_out,
-                           bool add, hipStream_t s, const WView* w2 = nullptr, int rows2 = 0, float* out2 = nullptr);
-hipError_t launch_rope_kv_batch(const float* qkv, int n_tok, int qd, int kvd, int head_dim, const float2* rope,
-                                int pos0, float* q_out, float* kc, float* vc, hipStream_t s);
+                           bool add, hipStream_t s, const WView* w2 = nullptr, int rows2 = 0, float* out2 = nullptr,
+                           int ld_out2 = 0, const GemmRope* rope = nullptr);
 hipError_t launch_attention_batch(const float* q, const float* kc, const float* vc, int n_heads, int n_kv_heads,
                                   int head_dim, int max_chunks, const AttnPart& part, size_t tok_o, size_t tok_mz,
                                   int pos0, int n_tok, hipStream_t s);

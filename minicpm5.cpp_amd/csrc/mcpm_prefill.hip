@@ -197,10 +197,16 @@ struct GemmArgs {
   int add;              // 1: out += v (residual), 0: out = v
   // an optional second matrix of the same type and blocks per row on the
   // same activations (rows2 > 0, rows a multiple of 64): the launch's rows
-  // rows .. rows+rows2-1 are its rows, written to out2 (same ld_out)
+  // rows .. rows+rows2-1 are its rows, written to out2 (row stride ld_out2)
   WView w2;
   int rows2;
   float* out2;
+  int ld_out2;
+  // rope != nullptr: every row pair (2i, 2i+1) of a matrix is rotated as
+  // apply_rope does before it is stored (head_dim rope_hd, token t at
+  // position pos0 + t, table rows of rope_hd/2 (cos, sin) pairs)
+  const float2* rope;
+  int rope_hd, pos0;
 };
 
 __device__ __forceinline__ uint32_t h2bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -279,6 +285,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   const WView W = second ? a.w2 : a.w;
   const int rows = second ? a.rows2 : a.rows;
   float* const out = second ? a.out2 : a.out;
+  const int ld_out = second ? a.ld_out2 : a.ld_out;
   const int r0 = (4 * rg + wave) * 16 - (second ? a.rows : 0), t0 = tg * TOK;
   const bool live = r0 < rows;  // uniform in the wave: a wave past the rows only stages
   const int ra = min(r0 + c16, rows - 1);  // A operand row of this lane
@@ -689,45 +696,34 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int t = t0 + 16 * n + c16;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = ((acc[n][0][i] + acc[n][4][i]) + (acc[n][2][i] + acc[n][6][i])) +
+             ((acc[n][1][i] + acc[n][5][i]) + (acc[n][3][i] + acc[n][7][i]));
+      if constexpr (WT == 0) v[i] = v[i] + accm[n][i];
+    }
+    if (a.rope) {
+      // rows 4g+i of the lane: pairs (0, 1) and (2, 3), apply_rope's
+      // products and sums (src/ops/ops.cpp:502-516)
+      const size_t pos = static_cast<size_t>(a.pos0 + min(t, a.n_tok - 1));
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const int d = (r0 + 4 * g + i) % a.rope_hd;
+        const float2 cs = a.rope[pos * (a.rope_hd / 2) + (d >> 1)];
+        const float e = v[i], o = v[i + 1];
+        v[i] = e * cs.x - o * cs.y;
+        v[i + 1] = e * cs.y + o * cs.x;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = r0 + 4 * g + i;
-      float v = ((acc[n][0][i] + acc[n][4][i]) + (acc[n][2][i] + acc[n][6][i])) +
-                ((acc[n][1][i] + acc[n][5][i]) + (acc[n][3][i] + acc[n][7][i]));
-      if constexpr (WT == 0) v = v + accm[n][i];
       if (r < rows && t < a.n_tok) {
-        float* o = out + static_cast<size_t>(t) * a.ld_out + r;
-        *o = a.add ? *o + v : v;
+        float* o = out + static_cast<size_t>(t) * ld_out + r;
+        *o = a.add ? *o + v[i] : v[i];
       }
     }
-  }
-}
-
-// ---------------------------------------------------------- RoPE and KV ----
-// qkv[t] = (q | k | v) rows of token t (position pos0 + t): q rotated into
-// q_out[t], k rotated and v copied into the KV cache rows (decode's QKV
-// epilogue, src/ops/ops.cpp:502-516).
-__global__ void k_rope_kv_batch(const float* __restrict__ qkv, int qd, int kvd, int head_dim,
-                                const float2* __restrict__ rope, int pos0, float* __restrict__ q_out,
-                                float* __restrict__ kc, float* __restrict__ vc) {
-  const int t = blockIdx.y;
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  const int n = qd + 2 * kvd;
-  if (r >= n) return;
-  const int pos = pos0 + t;
-  const float* src = qkv + static_cast<size_t>(t) * n;
-  const float v = src[r];
-  if (r < qd + kvd) {
-    const int i = (r < qd ? r : r - qd) % head_dim;
-    const float partner = src[r ^ 1];
-    const float2 cs = rope[static_cast<size_t>(pos) * (head_dim / 2) + (i >> 1)];
-    float o;
-    if ((i & 1) == 0) o = v * cs.x - partner * cs.y;
-    else o = partner * cs.y + v * cs.x;
-    if (r < qd) q_out[static_cast<size_t>(t) * qd + r] = o;
-    else kc[static_cast<size_t>(pos) * kvd + (r - qd)] = o;
-  } else {
-    vc[static_cast<size_t>(pos) * kvd + (r - qd - kvd)] = v;
   }
 }
 
@@ -834,11 +830,18 @@ hipError_t launch_quant_batch_swiglu(const float* g, const float* u, int ld, int
 }
 
 hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const QuantBatch& q, float* out, int ld_out,
-                           bool add, hipStream_t s, const WView* w2, int rows2, float* out2) {
+                           bool add, hipStream_t s, const WView* w2, int rows2, float* out2, int ld_out2,
+                           const GemmRope* rope) {
   if (w.type != MCPM_TYPE_Q4_K && w.type != MCPM_TYPE_Q6_K) return hipErrorInvalidValue;
   if (rows2 > 0 && (!w2 || !out2 || w2->type != w.type || rows % 64)) return hipErrorInvalidValue;
+  // a rotated pair (rows 2i, 2i+1) stays in one head and one lane: head_dim
+  // even, every matrix's rows a multiple of it
+  if (rope && (!rope->table || rope->head_dim <= 0 || rope->head_dim % 2 || rows % rope->head_dim ||
+               (rows2 > 0 && rows2 % rope->head_dim)))
+    return hipErrorInvalidValue;
   GemmArgs a{w, rows, nb, n_tok, q.xh, q.xd, q.xbs, out, ld_out, add ? 1 : 0, rows2 > 0 ? *w2 : WView{},
-             std::max(rows2, 0), out2};
+             std::max(rows2, 0), out2, ld_out2, rope ? rope->table : nullptr, rope ? rope->head_dim : 0,
+             rope ? rope->pos0 : 0};
   rows += std::max(rows2, 0);
   // token tiles per wave and waves per SIMD (MCPM_PREFILL_NT=1|2|4 and
   // MCPM_PREFILL_OCC=1|2 override, tuning aids; "a,b" sets Q4_K a, Q6_K b)
@@ -872,14 +875,6 @@ hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const Qu
   }
   MCPM_GEMM(1, 1) MCPM_GEMM(1, 2) MCPM_GEMM(2, 1) MCPM_GEMM(2, 2) MCPM_GEMM(4, 1) MCPM_GEMM(4, 2)
 #undef MCPM_GEMM
-  return hipGetLastError();
-}
-
-hipError_t launch_rope_kv_batch(const float* qkv, int n_tok, int qd, int kvd, int head_dim, const float2* rope,
-                                int pos0, float* q_out, float* kc, float* vc, hipStream_t s) {
-  const int n = qd + 2 * kvd;
-  hipLaunchKernelGGL(k_rope_kv_batch, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, qkv, qd, kvd, head_dim, rope,
-                     pos0, q_out, kc, vc);
   return hipGetLastError();
 }
 
