@@ -563,12 +563,14 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
     MCPM_HIP(launch_gemm_q8k(view_of(L.wo), c.dim, qd / QK_K, n, qb, b.x, c.dim, true, s));
     MCPM_HIP(launch_quant_batch(b.x, nullptr, c.dim, L.ffn_norm, c.eps, c.dim, c.dim, PRO_NORM_AWAY, n, qb, s));
     if (wg.type == wu.type && c.ffn % 64 == 0) {
-      MCPM_HIP(launch_gemm_q8k(wg, c.ffn, nbd, n, qb, b.g, c.ffn, false, s, &wu, c.ffn, b.u, c.ffn));
+      // gate and up in one launch, h = silu(gate)*up written by its epilogue
+      MCPM_HIP(launch_gemm_q8k(wg, c.ffn, nbd, n, qb, b.g, c.ffn, false, s, &wu, c.ffn, nullptr, 0, nullptr, true));
+      MCPM_HIP(launch_quant_batch(b.g, nullptr, c.ffn, nullptr, 0.0f, c.ffn_pad, c.ffn, PRO_QUANT_AWAY, n, qb, s));
     } else {
       MCPM_HIP(launch_gemm_q8k(wg, c.ffn, nbd, n, qb, b.g, c.ffn, false, s));
       MCPM_HIP(launch_gemm_q8k(wu, c.ffn, nbd, n, qb, b.u, c.ffn, false, s));
+      MCPM_HIP(launch_quant_batch_swiglu(b.g, b.u, c.ffn, c.ffn, c.ffn_pad, n, qb, s));
     }
-    MCPM_HIP(launch_quant_batch_swiglu(b.g, b.u, c.ffn, c.ffn, c.ffn_pad, n, qb, s));
     MCPM_HIP(launch_gemm_q8k(view_of(L.wd), c.dim, c.ffn_pad / QK_K, n, qb, b.x, c.dim, true, s));
   }
   return MCPM_OK;

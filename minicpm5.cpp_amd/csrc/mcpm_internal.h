@@ -326,7 +326,7 @@ struct GemmRope {
 // activations in the same launch (rows % 64 == 0).
 hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const QuantBatch& q, float* out, int ld_out,
                            bool add, hipStream_t s, const WView* w2 = nullptr, int rows2 = 0, float* out2 = nullptr,
-                           int ld_out2 = 0, const GemmRope* rope = nullptr);
+                           int ld_out2 = 0, const GemmRope* rope = nullptr, bool swiglu = false);
 hipError_t launch_attention_batch(const float* q, const float* kc, const float* vc, int n_heads, int n_kv_heads,
                                   int head_dim, int max_chunks, const AttnPart& part, size_t tok_o, size_t tok_mz,
                                   int pos0, int n_tok, hipStream_t s);

@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(256) k_quant_batch(const float* __restrict__ x
         }
         v[k] = h;
       } else {
-        v[k] = xt[i];
+        v[k] = i < n_valid ? xt[i] : 0.0f;
         if (norm) v[k] = (v[k] * rms) * gamma[i];
       }
     }
@@ -123,14 +123,13 @@ __global__ void __launch_bounds__(256) k_quant_batch_r(const float* __restrict__
   const bool swiglu = mode == QB_SWIGLU;
   const bool away = (mode == PRO_QUANT_AWAY || mode == PRO_NORM_AWAY || swiglu);
   const int nb = dim / QK_K;
-  // x (or g), and gamma (or u); blocks past nb re-read the last, and SwiGLU
-  // values at or past n_valid (a multiple of 4, checked by the launch) read
-  // the last valid four, all unused
+  // x (or g), and gamma (or u); blocks past nb re-read the last, and values
+  // at or past n_valid (a multiple of 4, checked by the launch; they
+  // quantize as 0) read the last valid four, unused
   f32x4 xv[MAXB], wv[MAXB];
 #pragma unroll
   for (int j = 0; j < MAXB; ++j) {
-    int i = min(wave + 4 * j, nb - 1) * QK_K + 4 * lane;
-    if (swiglu) i = min(i, n_valid - 4);
+    const int i = min(min(wave + 4 * j, nb - 1) * QK_K + 4 * lane, n_valid - 4);
     xv[j] = *reinterpret_cast<const f32x4*>(xt + i);
     if (norm) wv[j] = *reinterpret_cast<const f32x4*>(gamma + i);
     if (swiglu) wv[j] = *reinterpret_cast<const f32x4*>(ut + i);
@@ -165,8 +164,9 @@ __global__ void __launch_bounds__(256) k_quant_batch_r(const float* __restrict__
           h = silu * w4[k];
         }
         v[k] = h;
-      } else if (norm) {
-        v[k] = (v[k] * rms) * w4[k];
+      } else {
+        if (norm) v[k] = (v[k] * rms) * w4[k];
+        if (b * QK_K + 4 * lane + k >= n_valid) v[k] = 0.0f;
       }
     }
     uint32_t packed;
@@ -207,6 +207,10 @@ struct GemmArgs {
   // position pos0 + t, table rows of rope_hd/2 (cos, sin) pairs)
   const float2* rope;
   int rope_hd, pos0;
+  // swiglu: the two matrices are gate and up (rows2 == rows, rows % 32 ==
+  // 0); a work group takes 32 rows of each (waves 0, 1: gate; 2, 3: up) and
+  // writes h = silu(gate)*up (decode's gate/up epilogue) to out
+  int swiglu;
 };
 
 __device__ __forceinline__ uint32_t h2bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -281,12 +285,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   if (rg >= n_rg) return;  // uniform in the work group, before any barrier
   // the work group's matrix (its 64 rows lie in one: the first has a
   // multiple of 64 rows)
-  const bool second = a.rows2 > 0 && 64 * rg >= a.rows;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const bool second = a.swiglu ? wv >= 2 : a.rows2 > 0 && 64 * rg >= a.rows;
   const WView W = second ? a.w2 : a.w;
   const int rows = second ? a.rows2 : a.rows;
   float* const out = second ? a.out2 : a.out;
   const int ld_out = second ? a.ld_out2 : a.ld_out;
-  const int r0 = (4 * rg + wave) * 16 - (second ? a.rows : 0), t0 = tg * TOK;
+  const int r0 = a.swiglu ? 32 * rg + 16 * (wv & 1) : (4 * rg + wave) * 16 - (second ? a.rows : 0), t0 = tg * TOK;
   const bool live = r0 < rows;  // uniform in the wave: a wave past the rows only stages
   const int ra = min(r0 + c16, rows - 1);  // A operand row of this lane
   const int K = a.nb * QK_K;
@@ -693,16 +698,43 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   }
   if (b < a.nb) block(b, w0, w1);
 
+  float vs[NT][4];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      vs[n][i] = ((acc[n][0][i] + acc[n][4][i]) + (acc[n][2][i] + acc[n][6][i])) +
+                 ((acc[n][1][i] + acc[n][5][i]) + (acc[n][3][i] + acc[n][7][i]));
+      if constexpr (WT == 0) vs[n][i] = vs[n][i] + accm[n][i];
+    }
+  }
+  if (a.swiglu) {
+    // the up waves hand their values to the gate waves of the same rows and
+    // tokens through LDS (sB is free: every read of it passed the last
+    // block's barrier)
+    float* xs = reinterpret_cast<float*>(&sB[0][0]);
+    if (second) {
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xs[(((wv & 1) * NT + n) * 4 + i) * 64 + lane] = vs[n][i];
+      }
+    }
+    __syncthreads();
+    if (second) return;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float gv = vs[n][i], uv = xs[(((wv & 1) * NT + n) * 4 + i) * 64 + lane];
+        vs[n][i] = (gv / (1.0f + exp_f32(-gv))) * uv;
+      }
+    }
+  }
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int t = t0 + 16 * n + c16;
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = ((acc[n][0][i] + acc[n][4][i]) + (acc[n][2][i] + acc[n][6][i])) +
-             ((acc[n][1][i] + acc[n][5][i]) + (acc[n][3][i] + acc[n][7][i]));
-      if constexpr (WT == 0) v[i] = v[i] + accm[n][i];
-    }
+    float v[4] = {vs[n][0], vs[n][1], vs[n][2], vs[n][3]};
     if (a.rope) {
       // rows 4g+i of the lane: pairs (0, 1) and (2, 3), apply_rope's
       // products and sums (src/ops/ops.cpp:502-516)
@@ -811,7 +843,8 @@ hipError_t launch_quant_batch(const float* x, const float* u, int ld_x, const fl
   if (dim % QK_K) return hipErrorInvalidValue;
   // rows of up to 24 blocks load everything up front (k_quant_batch_r)
   const int nb = dim / QK_K;
-  const bool up_front = ld_x % 4 == 0 && (mode != QB_SWIGLU || (n_valid >= 4 && n_valid % 4 == 0 && n_valid <= ld_x));
+  if (n_valid < 1 || n_valid > dim || n_valid > ld_x) return hipErrorInvalidValue;
+  const bool up_front = ld_x % 4 == 0 && n_valid % 4 == 0;
   if (up_front && nb <= 12)
     hipLaunchKernelGGL(k_quant_batch_r<3>, dim3(n_tok), dim3(256), 0, s, x, u, ld_x, gamma, eps, dim, n_valid, mode,
                        q.xh, q.xd, q.xbs);
@@ -831,9 +864,10 @@ hipError_t launch_quant_batch_swiglu(const float* g, const float* u, int ld, int
 
 hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const QuantBatch& q, float* out, int ld_out,
                            bool add, hipStream_t s, const WView* w2, int rows2, float* out2, int ld_out2,
-                           const GemmRope* rope) {
+                           const GemmRope* rope, bool swiglu) {
   if (w.type != MCPM_TYPE_Q4_K && w.type != MCPM_TYPE_Q6_K) return hipErrorInvalidValue;
-  if (rows2 > 0 && (!w2 || !out2 || w2->type != w.type || rows % 64)) return hipErrorInvalidValue;
+  if (rows2 > 0 && (!w2 || w2->type != w.type || rows % 64 || (!swiglu && !out2))) return hipErrorInvalidValue;
+  if (swiglu && (rows2 != rows || rows % 32 || rope || add)) return hipErrorInvalidValue;
   // a rotated pair (rows 2i, 2i+1) stays in one head and one lane: head_dim
   // even, every matrix's rows a multiple of it
   if (rope && (!rope->table || rope->head_dim <= 0 || rope->head_dim % 2 || rows % rope->head_dim ||
@@ -841,7 +875,7 @@ hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const Qu
     return hipErrorInvalidValue;
   GemmArgs a{w, rows, nb, n_tok, q.xh, q.xd, q.xbs, out, ld_out, add ? 1 : 0, rows2 > 0 ? *w2 : WView{},
              std::max(rows2, 0), out2, ld_out2, rope ? rope->table : nullptr, rope ? rope->head_dim : 0,
-             rope ? rope->pos0 : 0};
+             rope ? rope->pos0 : 0, swiglu ? 1 : 0};
   rows += std::max(rows2, 0);
   // token tiles per wave and waves per SIMD (MCPM_PREFILL_NT=1|2|4 and
   // MCPM_PREFILL_OCC=1|2 override, tuning aids; "a,b" sets Q4_K a, Q6_K b)
