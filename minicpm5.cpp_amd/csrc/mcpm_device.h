@@ -54,6 +54,14 @@ __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
 }
 
+// LDS stores of the wave before this point are seen by its loads after it
+// (other lanes' stores included).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Maximum over the 16 lanes of the row, on every lane of the row.
 __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_f<DPP_XOR1>(v));

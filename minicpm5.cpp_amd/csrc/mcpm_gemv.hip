@@ -48,12 +48,6 @@ __device__ __forceinline__ T pick(int reg, T a, T b, T c) {
 }
 #define MCPM_PICK(reg, A, B, C, f) pick((reg), (A).f, (B).f, (C).f)
 
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // ------------------------------------------------------------- LDS plan ----
 // Dynamic LDS in dwords, by blocks per row nb:
 //   xs   [nb][68]  Q8_K quants of block b (64 dwords, native order) + pad

@@ -140,7 +140,7 @@ hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc
 // value read from LDS serves NT tokens.  Token k's queries at sQ + k*QSZ, its
 // softmax terms at sE + k*ESZ, its (m_c, z_c) at mz[k*ATTN_MAX_GROUP + hh], its
 // outputs in o[k].
-template <int HDM, int OPT, int NT>
+template <int HDM, int OPT, int NT, bool WL>
 __device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* sV, const float* sQ, float* sE,
                                                   float2* mz, int c, const int (&Tk)[NT], int group, int hd, int gh,
                                                   float scale, float (&o)[NT][OPT]) {
@@ -187,7 +187,10 @@ __device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* 
       if (lane == 0) mz[k * ATTN_MAX_GROUP + hh] = make_float2(mc, z);
     }
   }
-  __syncthreads();
+  // WL (head_dim 64): the weighted sums of head hh run on the wave that
+  // formed its softmax terms, so a wave-level ordering suffices
+  if constexpr (WL) wave_sync();
+  else __syncthreads();
   // positions 0..nt_k-1 for token k: the first nt_lo for every token, then
   // the later ones for the tokens that have them
   int nt[NT];
@@ -284,7 +287,11 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
 // tile stages past a token's context take no part in that token's sums.
 constexpr int ATTN_TOK = 4;
 
-template <int HDM>
+// WL (head_dim 64): every LDS value a wave reads in the token loop (its
+// heads' queries, softmax terms and (m_c, z_c)) was written by the same wave,
+// so the loop orders them within the wave and only the staged K/V rows wait
+// for a work-group barrier.
+template <int HDM, bool WL>
 __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict__ q, const float* __restrict__ kc,
                                                         const float* __restrict__ vc, int n_heads, int n_kv_heads,
                                                         int hd, int max_chunks, float* __restrict__ part_o,
@@ -334,8 +341,13 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
     *reinterpret_cast<f32x4*>(&sK[j * KS + c4 * 4]) = R.k[u];
     *reinterpret_cast<f32x4*>(&sV[j * HDM + c4 * 4]) = R.v[u];
   }
+  if constexpr (WL) __syncthreads();  // the staged rows
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int z = zlo; z < zhi; z += NT) {
-    __syncthreads();  // the previous tokens' readers of sQ, sE and sMZ are done
+    // the previous tokens' readers of sQ, sE and sMZ are done (and, first, the
+    // staged rows are in)
+    if constexpr (WL) wave_sync();
+    else __syncthreads();
 #pragma unroll
     for (int k = 0; k < NT; ++k) {
 #pragma unroll
@@ -345,12 +357,13 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
       }
     }
     if (z + NT < zhi) load_q(z + NT, qv);
-    __syncthreads();
+    if constexpr (WL) wave_sync();
+    else __syncthreads();
     int Tk[NT];
 #pragma unroll
     for (int k = 0; k < NT; ++k) Tk[k] = pos0 + min(z + k, zhi - 1) + 1;
     float o[NT][OPT];
-    attn_tokens_chunk<HDM, OPT, NT>(sK, sV, sQ, sE, sMZ, c, Tk, group, hd, gh, scale, o);
+    attn_tokens_chunk<HDM, OPT, NT, WL>(sK, sV, sQ, sE, sMZ, c, Tk, group, hd, gh, scale, o);
 #pragma unroll
     for (int k = 0; k < NT; ++k) {
       if (z + k < zhi) {
@@ -363,9 +376,16 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
             po[(static_cast<size_t>(kvh * group + hh) * max_chunks + c) * hd + i] = o[k][u];
           }
         }
-        if (tid < group)
+        if constexpr (WL) {
+          // lane 0 of the wave that wrote them: heads wave, wave + 4
+          for (int hh = wave; hh < group; hh += 4)
+            if (lane == 0)
+              part_mz[static_cast<size_t>(z + k) * tok_mz + static_cast<size_t>(kvh * group + hh) * max_chunks + c] =
+                  sMZ[k * ATTN_MAX_GROUP + hh];
+        } else if (tid < group) {
           part_mz[static_cast<size_t>(z + k) * tok_mz + static_cast<size_t>(kvh * group + tid) * max_chunks + c] =
               sMZ[k * ATTN_MAX_GROUP + tid];
+        }
       }
     }
   }
@@ -426,11 +446,14 @@ hipError_t launch_attention_batch(const float* q, const float* kc, const float* 
   const int tt = tt_env >= 1 && tt_env <= 256 ? tt_env : 16;
   const dim3 grid(n_kv_heads, (pos0 + n_tok - 1) / ATTN_CHUNK + 1, (n_tok + tt - 1) / tt);
   const size_t tok_q = static_cast<size_t>(n_heads) * head_dim;
-  if (head_dim <= 64)
-    hipLaunchKernelGGL(k_attention_tile<64>, grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
+  if (head_dim == 64)
+    hipLaunchKernelGGL((k_attention_tile<64, true>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
+                       max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
+  else if (head_dim < 64)
+    hipLaunchKernelGGL((k_attention_tile<64, false>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
                        max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
   else
-    hipLaunchKernelGGL(k_attention_tile<128>, grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
+    hipLaunchKernelGGL((k_attention_tile<128, false>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
                        max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
   return hipGetLastError();
 }
