@@ -748,12 +748,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
         v[i + 1] = e * cs.y + o * cs.x;
       }
     }
+    // the lane's four rows are consecutive: one 16-byte access where all
+    // four exist and the address is aligned, else one by one
+    const int r4 = r0 + 4 * g;
+    float* o = out + static_cast<size_t>(min(t, a.n_tok - 1)) * ld_out + r4;
+    if (t < a.n_tok) {
+      if (r4 + 3 < rows && (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
+        f32x4 w{v[0], v[1], v[2], v[3]};
+        if (a.add) {
+          const f32x4 p = *reinterpret_cast<const f32x4*>(o);
+          w = f32x4{p.x + v[0], p.y + v[1], p.z + v[2], p.w + v[3]};
+        }
+        *reinterpret_cast<f32x4*>(o) = w;
+      } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = r0 + 4 * g + i;
-      if (r < rows && t < a.n_tok) {
-        float* o = out + static_cast<size_t>(t) * ld_out + r;
-        *o = a.add ? *o + v[i] : v[i];
+        for (int i = 0; i < 4; ++i)
+          if (r4 + i < rows) o[i] = a.add ? o[i] + v[i] : v[i];
       }
     }
   }
