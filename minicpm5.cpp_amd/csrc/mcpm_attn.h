@@ -92,7 +92,7 @@ __device__ __forceinline__ void attn_load_chunk(AttnRegs<NV>& R, const float* __
 // (wave <-> head, lane <-> position) into sE and mz[hh] = (m_c, z_c), a
 // barrier, then the weighted V sums, thread (head, dim) oi = tid + 256u into
 // o[u].  Positions at or past T take no part.
-template <int HDM, int OPT>
+template <int HDM, int OPT, bool WL = false>
 __device__ __forceinline__ void attn_token_chunk(const float* sK, const float* sV, const float* sQ, float* sE,
                                                  float2* mz, int c, int T, int group, int hd, int gh, float scale,
                                                  float (&o)[OPT]) {
@@ -119,7 +119,10 @@ __device__ __forceinline__ void attn_token_chunk(const float* sK, const float* s
     sE[hh * ATTN_CHUNK + lane] = e;
     if (lane == 0) mz[hh] = make_float2(mc, z);
   }
-  __syncthreads();
+  // WL (head_dim 64): head hh's weighted sums run on the wave that formed
+  // its softmax terms, so a wave-level ordering suffices
+  if constexpr (WL) wave_sync();
+  else __syncthreads();
   const int nt = min(ATTN_CHUNK, T - c * ATTN_CHUNK);
 #pragma unroll
   for (int u = 0; u < OPT; ++u) {
@@ -174,7 +177,7 @@ struct AttnLds {
 // written by other work groups of the same launch and are read through the
 // coherence point.  pre: the split's first chunk is already in R
 // (attn_load_chunk by the caller).
-template <int HDM, bool COH>
+template <int HDM, bool COH, bool WL = false>
 __device__ __forceinline__ void attn_split(const float* __restrict__ q, const float* __restrict__ kc,
                                            const float* __restrict__ vc, int T, int kvh, int split, int n_heads,
                                            int n_kv_heads, int hd, int max_chunks, float* __restrict__ part_o,
@@ -240,7 +243,7 @@ __device__ __forceinline__ void attn_split(const float* __restrict__ q, const fl
       if (cc + 1 < n) attn_load_chunk<NV>(R, kc, vc, c + 1, T, kvd, head_off, r4, nf4);
       __syncthreads();
       float o[OPT];
-      attn_token_chunk<HDM, OPT>(sK, sV, sQ, sE, sMZ + cc * ATTN_MAX_GROUP, c, T, group, hd, gh, scale, o);
+      attn_token_chunk<HDM, OPT, WL>(sK, sV, sQ, sE, sMZ + cc * ATTN_MAX_GROUP, c, T, group, hd, gh, scale, o);
 #pragma unroll
       for (int u = 0; u < OPT; ++u) oc[u][cc] = o[u];
     }
@@ -258,7 +261,15 @@ __device__ __forceinline__ void attn_split(const float* __restrict__ q, const fl
         if (cc < n) ph[static_cast<size_t>(cc) * hd] = oc[u][cc];
     }
   }
-  if (tid < ATTN_CPW * ATTN_MAX_GROUP) {
+  if constexpr (WL) {
+    // (m_c, z_c) stored by lane 0 of the wave that wrote them (heads wave,
+    // wave + 4)
+    if ((tid & 63) == 0) {
+      for (int hh = tid >> 6; hh < group; hh += 4)
+        for (int cc = 0; cc < n; ++cc)
+          part_mz[static_cast<size_t>(kvh * group + hh) * max_chunks + c0 + cc] = sMZ[cc * ATTN_MAX_GROUP + hh];
+    }
+  } else if (tid < ATTN_CPW * ATTN_MAX_GROUP) {
     const int cc = tid / ATTN_MAX_GROUP, hh = tid % ATTN_MAX_GROUP;
     if (cc < n && hh < group) part_mz[static_cast<size_t>(kvh * group + hh) * max_chunks + c0 + cc] = sMZ[cc * ATTN_MAX_GROUP + hh];
   }

@@ -255,7 +255,7 @@ __device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* 
   }
 }
 
-template <int HDM>
+template <int HDM, bool WL>
 __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, const int* __restrict__ state,
                                                    int n_heads, int n_kv_heads, int hd, int max_chunks,
@@ -274,7 +274,7 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
     T = state[1] + 1;
   }
   AttnRegs<HDM / 16> R;
-  attn_split<HDM, false>(q, kc, vc, T, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), n_heads,
+  attn_split<HDM, false, WL>(q, kc, vc, T, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), n_heads,
                          n_kv_heads, hd, max_chunks, part_o, part_mz, AttnLds<HDM>(lds), R, false);
 }
 
@@ -421,10 +421,11 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, co
     return hipErrorInvalidValue;
   const dim3 grid(n_kv_heads, attn_max_splits(1, max_chunks));
   if (head_dim <= 64)
-    launch_kernel(k_attention<64>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
+    launch_kernel(head_dim == 64 ? k_attention<64, true> : k_attention<64, false>, grid, dim3(256), 0, s, q, kc, vc,
+                  state, n_heads, n_kv_heads, head_dim,
                   max_chunks, part.o, part.mz, -1, size_t{0}, size_t{0}, size_t{0});
   else
-    launch_kernel(k_attention<128>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
+    launch_kernel(k_attention<128, false>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
                   max_chunks, part.o, part.mz, -1, size_t{0}, size_t{0}, size_t{0});
   return hipGetLastError();
 }
