@@ -275,14 +275,26 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8
   const int lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int n_rt = (a.rows + a.rows2 + 15) >> 4;
   const int n_rg = (n_rt + 3) >> 2;
-  // XCD-aware tiles: work group b runs on XCD b % 8, which takes the row
-  // groups rg = xcd + 8j only, for every token tile, so each XCD's L2 keeps
-  // one eighth of the matrix for the whole launch.  Work groups past the row
-  // groups of their XCD have nothing to do.
+  // XCD-aware tiles: work group b runs on XCD b % 8.  Of n_rg = 8q + r row
+  // groups, XCD x takes rg = x + 8j (j < q) for every token tile (token
+  // tiles outer, so the tile's activations serve its q row groups from one
+  // L2), and then an equal share of the r remaining row groups' (row group,
+  // token tile) items, so every XCD has the same work; each XCD's L2 keeps
+  // about one eighth of the matrix for the whole launch.
   const int xcd = static_cast<int>(blockIdx.x) & 7, loc = static_cast<int>(blockIdx.x) >> 3;
-  const int cmax = (n_rg + 7) >> 3;
-  const int rg = xcd + 8 * (loc % cmax), tg = loc / cmax;
-  if (rg >= n_rg) return;  // uniform in the work group, before any barrier
+  const int n_tg = (a.n_tok + TOK - 1) / TOK;
+  const int rq = n_rg >> 3, rr = n_rg & 7;
+  const int share = (rr * n_tg + 7) >> 3;
+  int rg, tg;
+  if (loc < rq * n_tg) {
+    rg = xcd + 8 * (loc % rq);
+    tg = loc / rq;
+  } else {
+    const int li = xcd * share + (loc - rq * n_tg);
+    if (li >= rr * n_tg) return;  // uniform in the work group, before any barrier
+    rg = 8 * rq + li / n_tg;
+    tg = li % n_tg;
+  }
   // the work group's matrix (its 64 rows lie in one: the first has a
   // multiple of 64 rows)
   const int wv = __builtin_amdgcn_readfirstlane(wave);
@@ -908,10 +920,10 @@ hipError_t launch_gemm_q8k(const WView& w, int rows, int nb, int n_tok, const Qu
   // four MFMA operand sets need the room.
   const int NT = nt_e == 1 || nt_e == 2 || nt_e == 4 ? nt_e : (q4 ? 2 : 1);
   const int OCC = occ_e == 1 ? 1 : 2;
-  // one work group per 64 rows (four 16-row tiles) x 16*NT tokens
-  // 8 XCDs x (row groups per XCD) x token tiles (see k_gemm_q8k)
-  const int n_groups = 8 * (((rows + 63) / 64 + 7) / 8) * ((n_tok + 16 * NT - 1) / (16 * NT));
-  const dim3 grid(n_groups);
+  // one work group per 64 rows (four 16-row tiles) x 16*NT tokens: per XCD,
+  // q row groups x token tiles and a share of the other r (see k_gemm_q8k)
+  const int n_rg = (rows + 63) / 64, n_tg = (n_tok + 16 * NT - 1) / (16 * NT);
+  const dim3 grid(8 * ((n_rg / 8) * n_tg + ((n_rg % 8) * n_tg + 7) / 8));
 #define MCPM_GEMM(N, O) \
   if (NT == N && OCC == O) { \
     if (q4) launch_kernel(k_gemm_q8k<0, N, O>, grid, dim3(256), 0, s, a); \
