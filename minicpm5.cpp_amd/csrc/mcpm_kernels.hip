@@ -140,13 +140,19 @@ hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc
 // value read from LDS serves NT tokens.  Token k's queries at sQ + k*QSZ, its
 // softmax terms at sE + k*ESZ, its (m_c, z_c) at mz[k*ATTN_MAX_GROUP + hh], its
 // outputs in o[k].
-template <int HDM, int OPT, int NT, bool WL>
+// GM: the most query heads per kv head that sQ and sE hold.  SWZ: K rows
+// unpadded, 64 floats apart, float4 c4 of row j at (c4 ^ (j % 16)) (distinct
+// banks across 16 rows read together, as the padding gives).  (m_c, z_c) go
+// to put_mz(k, hh, value) from lane 0 of the head's wave.
+template <int HDM, int OPT, int NT, bool WL, int GM, bool SWZ, class PutMZ>
 __device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* sV, const float* sQ, float* sE,
-                                                  float2* mz, int c, const int (&Tk)[NT], int group, int hd, int gh,
+                                                  PutMZ put_mz, int c, const int (&Tk)[NT], int group, int hd, int gh,
                                                   float scale, float (&o)[NT][OPT]) {
-  constexpr int KS = HDM + 4;
-  constexpr int QSZ = ATTN_MAX_GROUP * HDM, ESZ = ATTN_MAX_GROUP * ATTN_CHUNK;
+  constexpr int KS = SWZ ? HDM : HDM + 4;
+  constexpr int QSZ = GM * HDM, ESZ = GM * ATTN_CHUNK;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // float offset of dimension i (a multiple of 4) in this lane's K row
+  auto kof = [&](int i) { return SWZ ? (((i >> 2) ^ (lane & 15)) << 2) : i; };
   for (int hh = wave; hh < group; hh += 4) {
     const float* kt = &sK[lane * KS];
     const float* qh = sQ + hh * HDM;
@@ -155,13 +161,13 @@ __device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* 
     for (int k = 0; k < NT; ++k) dot[k] = 0.0f;
     // the next 4 dimensions' K and q are read while this step's fmas run
     // (the last step reads itself again)
-    f32x4 kc4 = *reinterpret_cast<const f32x4*>(kt), qc4[NT];
+    f32x4 kc4 = *reinterpret_cast<const f32x4*>(kt + kof(0)), qc4[NT];
 #pragma unroll
     for (int k = 0; k < NT; ++k) qc4[k] = *reinterpret_cast<const f32x4*>(qh + k * QSZ);
 #pragma unroll 2
     for (int i = 0; i < hd; i += 4) {
       const int in = min(i + 4, hd - 4);
-      const f32x4 kn4 = *reinterpret_cast<const f32x4*>(kt + in);
+      const f32x4 kn4 = *reinterpret_cast<const f32x4*>(kt + kof(in));
       f32x4 qn4[NT];
 #pragma unroll
       for (int k = 0; k < NT; ++k) qn4[k] = *reinterpret_cast<const f32x4*>(qh + k * QSZ + in);
@@ -184,7 +190,7 @@ __device__ __forceinline__ void attn_tokens_chunk(const float* sK, const float* 
       const float e = present ? exp_f32(sv - mc) : 0.0f;
       const float z = wave_tree_sum_fast(e);
       sE[k * ESZ + hh * ATTN_CHUNK + lane] = e;
-      if (lane == 0) mz[k * ATTN_MAX_GROUP + hh] = make_float2(mc, z);
+      if (lane == 0) put_mz(k, hh, make_float2(mc, z));
     }
   }
   // WL (head_dim 64): the weighted sums of head hh run on the wave that
@@ -291,23 +297,29 @@ constexpr int ATTN_TOK = 4;
 // heads' queries, softmax terms and (m_c, z_c)) was written by the same wave,
 // so the loop orders them within the wave and only the staged K/V rows wait
 // for a work-group barrier.
-template <int HDM, bool WL>
+template <int HDM, bool WL, int GM>
 __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict__ q, const float* __restrict__ kc,
                                                         const float* __restrict__ vc, int n_heads, int n_kv_heads,
                                                         int hd, int max_chunks, float* __restrict__ part_o,
                                                         float2* __restrict__ part_mz, int pos0, int n_tok, int tt,
                                                         size_t tok_q, size_t tok_o, size_t tok_mz) {
+  // GM 4 (head_dim 64, at most 4 query heads per kv head): sQ and sE for 4
+  // heads, K rows unpadded and swizzled, (m_c, z_c) stored straight from
+  // the wave: 40 KB of LDS, four work groups per CU where the padded layout
+  // for 8 heads (50 KB) fits three
+  constexpr bool SWZ = GM == 4;
   constexpr int NV = HDM / 16;
-  constexpr int OPT = ATTN_MAX_GROUP * HDM / 256;
-  constexpr int NQ = ATTN_MAX_GROUP * HDM / 256;
-  constexpr int KS = HDM + 4;
+  constexpr int OPT = GM * HDM / 256;
+  constexpr int NQ = GM * HDM / 256;
+  constexpr int KS = SWZ ? HDM : HDM + 4;
   constexpr int NT = ATTN_TOK;
-  constexpr int QSZ = ATTN_MAX_GROUP * HDM, ESZ = ATTN_MAX_GROUP * ATTN_CHUNK;
+  constexpr int QSZ = GM * HDM, ESZ = GM * ATTN_CHUNK;
+  static_assert(!SWZ || (WL && HDM == 64), "the compact layout is for head_dim 64");
   __shared__ __attribute__((aligned(16))) float sK[ATTN_CHUNK * KS];
   __shared__ __attribute__((aligned(16))) float sV[ATTN_CHUNK * HDM];
   __shared__ __attribute__((aligned(16))) float sQ[NT * QSZ];
   __shared__ __attribute__((aligned(16))) float sE[NT * ESZ];
-  __shared__ float2 sMZ[NT * ATTN_MAX_GROUP];
+  __shared__ float2 sMZ[SWZ ? 1 : NT * ATTN_MAX_GROUP];
   const int tid = threadIdx.x;
   const int kvh = blockIdx.x, c = blockIdx.y;
   const int z0 = static_cast<int>(blockIdx.z) * tt;
@@ -338,7 +350,7 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
   for (int u = 0; u < NV; ++u) {
     const int f = min(tid + 256 * u, nf4 - 1);
     const int j = f / r4, c4 = f - j * r4;
-    *reinterpret_cast<f32x4*>(&sK[j * KS + c4 * 4]) = R.k[u];
+    *reinterpret_cast<f32x4*>(&sK[j * KS + (SWZ ? (c4 ^ (j & 15)) : c4) * 4]) = R.k[u];
     *reinterpret_cast<f32x4*>(&sV[j * HDM + c4 * 4]) = R.v[u];
   }
   if constexpr (WL) __syncthreads();  // the staged rows
@@ -363,7 +375,15 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
 #pragma unroll
     for (int k = 0; k < NT; ++k) Tk[k] = pos0 + min(z + k, zhi - 1) + 1;
     float o[NT][OPT];
-    attn_tokens_chunk<HDM, OPT, NT, WL>(sK, sV, sQ, sE, sMZ, c, Tk, group, hd, gh, scale, o);
+    auto put_mz = [&](int k, int hh, float2 v) {
+      if constexpr (SWZ) {
+        if (z + k < zhi)
+          part_mz[static_cast<size_t>(z + k) * tok_mz + static_cast<size_t>(kvh * group + hh) * max_chunks + c] = v;
+      } else {
+        sMZ[k * ATTN_MAX_GROUP + hh] = v;
+      }
+    };
+    attn_tokens_chunk<HDM, OPT, NT, WL, GM, SWZ>(sK, sV, sQ, sE, put_mz, c, Tk, group, hd, gh, scale, o);
 #pragma unroll
     for (int k = 0; k < NT; ++k) {
       if (z + k < zhi) {
@@ -376,7 +396,9 @@ __global__ void __launch_bounds__(256) k_attention_tile(const float* __restrict_
             po[(static_cast<size_t>(kvh * group + hh) * max_chunks + c) * hd + i] = o[k][u];
           }
         }
-        if constexpr (WL) {
+        if constexpr (SWZ) {
+          // stored by put_mz
+        } else if constexpr (WL) {
           // lane 0 of the wave that wrote them: heads wave, wave + 4
           for (int hh = wave; hh < group; hh += 4)
             if (lane == 0)
@@ -447,14 +469,17 @@ hipError_t launch_attention_batch(const float* q, const float* kc, const float* 
   const int tt = tt_env >= 1 && tt_env <= 256 ? tt_env : 16;
   const dim3 grid(n_kv_heads, (pos0 + n_tok - 1) / ATTN_CHUNK + 1, (n_tok + tt - 1) / tt);
   const size_t tok_q = static_cast<size_t>(n_heads) * head_dim;
-  if (head_dim == 64)
-    hipLaunchKernelGGL((k_attention_tile<64, true>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
+  if (head_dim == 64 && n_heads / n_kv_heads <= 4)
+    hipLaunchKernelGGL((k_attention_tile<64, true, 4>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads,
+                       head_dim, max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL((k_attention_tile<64, true, 8>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
                        max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
   else if (head_dim < 64)
-    hipLaunchKernelGGL((k_attention_tile<64, false>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
+    hipLaunchKernelGGL((k_attention_tile<64, false, 8>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
                        max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
   else
-    hipLaunchKernelGGL((k_attention_tile<128, false>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
+    hipLaunchKernelGGL((k_attention_tile<128, false, 8>), grid, dim3(256), 0, s, q, kc, vc, n_heads, n_kv_heads, head_dim,
                        max_chunks, part.o, part.mz, pos0, n_tok, tt, tok_q, tok_o, tok_mz);
   return hipGetLastError();
 }
