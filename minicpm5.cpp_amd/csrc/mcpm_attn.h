@@ -70,13 +70,15 @@ struct AttnRegs {
 // leave a stale line in this XCD's L2, which later loads of the launch,
 // coherent ones included, could then hit; attn_reload_last_row fills those
 // slots once the writers are done.
+// tid: the thread's index in its group of 256 (the work group's by default).
 template <int NV, bool SKIP_LAST = false>
 __device__ __forceinline__ void attn_load_chunk(AttnRegs<NV>& R, const float* __restrict__ kc,
                                                 const float* __restrict__ vc, int c, int T, int kvd,
-                                                size_t head_off, int r4, int nf4) {
+                                                size_t head_off, int r4, int nf4,
+                                                int tid = static_cast<int>(threadIdx.x)) {
 #pragma unroll
   for (int u = 0; u < NV; ++u) {
-    const int f = min(static_cast<int>(threadIdx.x) + 256 * u, nf4 - 1);
+    const int f = min(tid + 256 * u, nf4 - 1);
     const int j = f / r4, c4 = f - j * r4;
     const int t = min(c * ATTN_CHUNK + j, T - 1);
     const size_t o = static_cast<size_t>(t) * kvd + head_off + c4 * 4;
@@ -91,13 +93,15 @@ __device__ __forceinline__ void attn_load_chunk(AttnRegs<NV>& R, const float* __
 // rows in sV, the token's group of queries in sQ): scores and softmax terms
 // (wave <-> head, lane <-> position) into sE and mz[hh] = (m_c, z_c), a
 // barrier, then the weighted V sums, thread (head, dim) oi = tid + 256u into
-// o[u].  Positions at or past T take no part.
+// o[u].  Positions at or past T take no part.  tid: the thread's index in its
+// group of 256 (the work group's by default); with WL (a wave-level ordering
+// between the two phases) several groups may run chunks side by side.
 template <int HDM, int OPT, bool WL = false>
 __device__ __forceinline__ void attn_token_chunk(const float* sK, const float* sV, const float* sQ, float* sE,
                                                  float2* mz, int c, int T, int group, int hd, int gh, float scale,
-                                                 float (&o)[OPT]) {
+                                                 float (&o)[OPT], int tid = static_cast<int>(threadIdx.x)) {
   constexpr int KS = HDM + 4;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = tid >> 6;
   for (int hh = wave; hh < group; hh += 4) {
     const float* qh = &sQ[hh * HDM];
     const float* kt = &sK[lane * KS];
@@ -172,17 +176,17 @@ struct AttnLds {
       : sK(base), sV(base + K), sQ(base + K + V), sE(base + K + V + Q), sMZ(reinterpret_cast<float2*>(base + K + V + Q + E)) {}
 };
 
-// Split `split` of kv head kvh at context T: its chunks' partials (the work
-// of one k_attention work group).  COH: q and the K and V rows at T-1 were
-// written by other work groups of the same launch and are read through the
-// coherence point.  pre: the split's first chunk is already in R
-// (attn_load_chunk by the caller).
-template <int HDM, bool COH, bool WL = false>
-__device__ __forceinline__ void attn_split(const float* __restrict__ q, const float* __restrict__ kc,
-                                           const float* __restrict__ vc, int T, int kvh, int split, int n_heads,
-                                           int n_kv_heads, int hd, int max_chunks, float* __restrict__ part_o,
-                                           float2* __restrict__ part_mz, const AttnLds<HDM>& S,
-                                           AttnRegs<HDM / 16>& R, bool pre) {
+// Chunks c0 .. c0+n-1 (n <= ATTN_CPW) of kv head kvh at context T: o_c of
+// thread (head, dim) oi = tid + 256u into oc[u][cc], (m_c, z_c) of head hh
+// into S.sMZ[cc*ATTN_MAX_GROUP + hh] (written by lane 0 of wave hh % 4).
+// COH: q and the K and V rows at T-1 were written by other work groups of the
+// same launch and are read through the coherence point.  pre: chunk c0 is
+// already in R (attn_load_chunk by the caller).
+template <int HDM, bool COH, bool WL>
+__device__ __forceinline__ void attn_chunks(const float* __restrict__ q, const float* __restrict__ kc,
+                                            const float* __restrict__ vc, int T, int kvh, int c0, int n, int group,
+                                            int hd, int kvd, const AttnLds<HDM>& S, AttnRegs<HDM / 16>& R, bool pre,
+                                            float (&oc)[ATTN_MAX_GROUP * HDM / 256][ATTN_CPW]) {
   constexpr int NV = HDM / 16;                      // float4 of a chunk's K (or V) per thread, at most
   constexpr int OPT = ATTN_MAX_GROUP * HDM / 256;   // outputs per thread, at most
   constexpr int NQ = ATTN_MAX_GROUP * HDM / 256;    // query values per thread, at most
@@ -194,12 +198,6 @@ __device__ __forceinline__ void attn_split(const float* __restrict__ q, const fl
   float2* sMZ = S.sMZ;
   const int tid = threadIdx.x;
   const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
-  const int cps = attn_chunks_per_split(nch);
-  const int nsplit = attn_splits(nch);
-  if (split >= nsplit) return;
-  const int c0 = split * cps, n = min(cps, nch - c0);
-  const int group = n_heads / n_kv_heads;
-  const int kvd = n_kv_heads * hd;
   const int r4 = hd / 4;              // float4 per K/V row
   const int nf4 = ATTN_CHUNK * r4;    // float4 per chunk
   const int gh = group * hd;          // outputs of the work group
@@ -223,7 +221,6 @@ __device__ __forceinline__ void attn_split(const float* __restrict__ q, const fl
     }
   }
 
-  float oc[OPT][ATTN_CPW];
 #pragma clang loop unroll(full)
   for (int cc = 0; cc < ATTN_CPW; ++cc) {
     if (cc < n) {
@@ -248,6 +245,29 @@ __device__ __forceinline__ void attn_split(const float* __restrict__ q, const fl
       for (int u = 0; u < OPT; ++u) oc[u][cc] = o[u];
     }
   }
+}
+
+// Split `split` of kv head kvh at context T: its chunks' partials (the work
+// of one k_attention work group).  COH and pre as for attn_chunks.
+template <int HDM, bool COH, bool WL = false>
+__device__ __forceinline__ void attn_split(const float* __restrict__ q, const float* __restrict__ kc,
+                                           const float* __restrict__ vc, int T, int kvh, int split, int n_heads,
+                                           int n_kv_heads, int hd, int max_chunks, float* __restrict__ part_o,
+                                           float2* __restrict__ part_mz, const AttnLds<HDM>& S,
+                                           AttnRegs<HDM / 16>& R, bool pre) {
+  constexpr int OPT = ATTN_MAX_GROUP * HDM / 256;   // outputs per thread, at most
+  const int tid = threadIdx.x;
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  const int cps = attn_chunks_per_split(nch);
+  const int nsplit = attn_splits(nch);
+  if (split >= nsplit) return;
+  const int c0 = split * cps, n = min(cps, nch - c0);
+  const int group = n_heads / n_kv_heads;
+  const int gh = group * hd;          // outputs of the work group
+  float2* sMZ = S.sMZ;
+
+  float oc[OPT][ATTN_CPW];
+  attn_chunks<HDM, COH, WL>(q, kc, vc, T, kvh, c0, n, group, hd, n_kv_heads * hd, S, R, pre, oc);
 
   // this split's chunks to the partials
 #pragma unroll

@@ -80,9 +80,18 @@ struct mcpm_engine {
   float2* rope = nullptr;
   float* attn_part = nullptr;
   bool attn_fused = false;  // the O-projection's prologue combines the attention partials
+  // contexts of at most ATTN_Q8K_MAX_CHUNKS chunks: one attention work group
+  // per kv head leaves the O projection's input as Q8_K blocks (att_q8); a
+  // launch at a longer context sets attn_err
+  bool attn_q8k = false;
+  int attn_q8k_chunks = ATTN_Q8K_CHUNKS;  // up to this many chunks (MCPM_ATTN_Q8K=n: n)
+  BlockQ8K* att_q8 = nullptr;
+  unsigned* attn_err = nullptr;
   // graph
   bool use_graph = true;
-  hipGraphExec_t graph[2] = {nullptr, nullptr};  // greedy (argmax at the end), sampled
+  // [greedy (argmax at the end), sampled][longer contexts, contexts the
+  // per-kv-head attention covers]
+  hipGraphExec_t graph[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
   // timing
   int timing_class = -1;
   std::vector<TimedPair> events;
@@ -117,10 +126,11 @@ int alloc_dev(void** p, size_t bytes) {
 }
 
 void drop_graph(mcpm_engine* e) {
-  for (hipGraphExec_t& g : e->graph) {
-    if (g) (void)hipGraphExecDestroy(g);
-    g = nullptr;
-  }
+  for (auto& mode : e->graph)
+    for (hipGraphExec_t& g : mode) {
+      if (g) (void)hipGraphExecDestroy(g);
+      g = nullptr;
+    }
 }
 
 void free_prefill(PrefillBufs& b) {
@@ -152,7 +162,8 @@ void free_engine(mcpm_engine* e) {
                   static_cast<void*>(e->h), static_cast<void*>(e->logits), static_cast<void*>(e->argmax_part),
                   static_cast<void*>(e->st), static_cast<void*>(e->out_tokens), static_cast<void*>(e->kc),
                   static_cast<void*>(e->vc), static_cast<void*>(e->rope), static_cast<void*>(e->attn_part),
-                  e->d_sample, static_cast<void*>(e->gsync), static_cast<void*>(e->d_draws)})
+                  e->d_sample, static_cast<void*>(e->gsync), static_cast<void*>(e->d_draws),
+                  static_cast<void*>(e->att_q8), static_cast<void*>(e->attn_err)})
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
   free_prefill(e->pf);
@@ -268,6 +279,13 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
   }
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->st), sizeof(StepState));
   if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->gsync), GRID_SYNC_WORDS * sizeof(unsigned));
+  if (!rc && e->attn_fused && attn_q8k_fits(c.n_heads, c.n_kv_heads, c.head_dim)) {
+    const char* v = std::getenv("MCPM_ATTN_Q8K");
+    e->attn_q8k = !v || std::atoi(v) != 0;
+    if (v && std::atoi(v) > 0) e->attn_q8k_chunks = std::min(std::atoi(v), ATTN_Q8K_MAX_CHUNKS);
+    if (e->attn_q8k) rc = alloc_dev(reinterpret_cast<void**>(&e->att_q8), (qd / QK_K) * sizeof(BlockQ8K));
+    if (!rc && e->attn_q8k) rc = alloc_dev(reinterpret_cast<void**>(&e->attn_err), sizeof(unsigned));
+  }
   if (rc) {
     free_engine(e);
     return rc;
@@ -332,6 +350,14 @@ hipError_t timed(mcpm_engine* e, int kc, F&& launch) {
 // (spin limit) left its error word set; report it and reset the barrier
 // state for the next launches.
 int check_grid_sync(mcpm_engine* e) {
+  if (e->attn_q8k) {
+    unsigned aerr = 0;
+    MCPM_HIP(hipMemcpy(&aerr, e->attn_err, sizeof aerr, hipMemcpyDeviceToHost));
+    if (aerr) {
+      MCPM_HIP(hipMemset(e->attn_err, 0, sizeof(unsigned)));
+      return fail(MCPM_ERR_HIP, "the per-kv-head attention ran past its context limit; results of the call are invalid");
+    }
+  }
   if (!e->fused_ffn && !e->fused_attn) return MCPM_OK;
   unsigned err = 0;
   MCPM_HIP(hipMemcpy(&err, e->gsync + 8 * 64 + 64, sizeof err, hipMemcpyDeviceToHost));
@@ -340,13 +366,15 @@ int check_grid_sync(mcpm_engine* e) {
   return fail(MCPM_ERR_HIP, "a fused kernel's grid barrier timed out; results of the call are invalid");
 }
 
-// All kernels of one token, reading token and pos from e->st.
-int enqueue_token(mcpm_engine* e) {
+// All kernels of one token, reading token and pos from e->st.  short_ctx:
+// the context (pos + 1) has at most ATTN_Q8K_MAX_CHUNKS chunks.
+int enqueue_token(mcpm_engine* e, bool short_ctx) {
   const mcpm_model_config& c = e->cfg;
   hipStream_t s = e->ctx->stream;
   const int n_cu = e->ctx->n_cu;
   const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
   const int* st = reinterpret_cast<const int*>(e->st);
+  const bool q8k = short_ctx && e->attn_q8k && !e->fused_attn;
   MCPM_HIP(launch_embedding(view_of(e->embd), st, c.dim, e->x, s));
   for (int l = 0; l < c.n_layers; ++l) {
     const Layer& L = e->L[l];
@@ -380,11 +408,24 @@ int enqueue_token(mcpm_engine* e) {
       if (fe == hipErrorNotSupported) {
         MCPM_HIP(timed(e, MCPM_KC_QKV, [&] { return launch_gemv(a, PRO_NORM_AWAY, EPI_QKV, n_cu, s); }));
         MCPM_HIP(timed(e, MCPM_KC_ATTN, [&] {
+          if (q8k)
+            return launch_attention_q8k(e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->att_q8,
+                                        e->attn_err, s);
           return launch_attention(e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part, s);
         }));
       }
     }
-    {
+    if (q8k) {
+      // the attention output is already the O projection's Q8_K input
+      GemvArgs a{};
+      a.reg[0] = GemvRegion{view_of(L.wo), nullptr, 0, c.dim};
+      a.nreg = 1;
+      a.total_rows = c.dim;
+      a.nb = qd / QK_K;
+      a.resid = e->x;
+      a.xq = e->att_q8;
+      MCPM_HIP(timed(e, MCPM_KC_OPROJ, [&] { return launch_gemv(a, PRO_Q8K, EPI_RESID, n_cu, s); }));
+    } else {
       // the attention output is combined from its chunk partials in this
       // GEMV's prologue where the shape allows, else by its own kernel
       GemvArgs a{};
@@ -457,16 +498,19 @@ int enqueue_token(mcpm_engine* e) {
   return MCPM_OK;
 }
 
-int run_token(mcpm_engine* e) {
+// One token at position pos (the position the step state holds when the
+// token's kernels run): the graph for its context length.
+int run_token(mcpm_engine* e, int pos) {
+  const bool short_ctx = pos / ATTN_CHUNK + 1 <= e->attn_q8k_chunks;
   // Events recorded inside a captured graph cannot be read back with
   // hipEventElapsedTime, so a timed kernel class runs the same launches eagerly.
-  if (!e->use_graph || e->timing_class >= 0) return enqueue_token(e);
-  hipGraphExec_t& graph = e->graph[e->sample_mode ? 1 : 0];
+  if (!e->use_graph || e->timing_class >= 0) return enqueue_token(e, short_ctx);
+  hipGraphExec_t& graph = e->graph[e->sample_mode ? 1 : 0][short_ctx && e->attn_q8k ? 1 : 0];
   if (!graph) {
     hipStream_t s = e->ctx->stream;
     MCPM_HIP(hipStreamSynchronize(s));
     MCPM_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    const int rc = enqueue_token(e);
+    const int rc = enqueue_token(e, short_ctx);
     hipGraph_t g = nullptr;
     const hipError_t ce = hipStreamEndCapture(s, &g);
     if (rc) {
@@ -696,7 +740,7 @@ int mcpm_engine_forward(mcpm_engine* e, int token, int pos, int max_seq_len, flo
   if (rc) return rc;
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
   rc = queue_state(e, 0, token, pos, 0);
-  if (!rc) rc = run_token(e);
+  if (!rc) rc = run_token(e, pos);
   if (rc) return rc;
   e->gen_count = 0;
   if (logits)
@@ -719,9 +763,11 @@ static int set_sample_mode(mcpm_engine* e, bool on) {
 }
 
 static void set_sampling(mcpm_engine* e, float temperature, float top_p) {
-  if (e->graph[1] && (e->smp_T != temperature || e->smp_P != top_p)) {
-    (void)hipGraphExecDestroy(e->graph[1]);
-    e->graph[1] = nullptr;
+  if (e->smp_T != temperature || e->smp_P != top_p) {
+    for (hipGraphExec_t& g : e->graph[1]) {
+      if (g) (void)hipGraphExecDestroy(g);
+      g = nullptr;
+    }
   }
   e->smp_T = temperature;
   e->smp_P = top_p;
@@ -802,11 +848,12 @@ static int generate_at(mcpm_engine* e, const int* toks, int n, int pos0, int n_g
   if (!rc && first) rc = mcpm_engine_prefill(e, toks, first, pos0);
   for (int i = first; i < n && !rc; ++i) {
     rc = queue_state(e, i, toks[i], pos0 + i, 0);
-    if (!rc) rc = run_token(e);
+    if (!rc) rc = run_token(e, pos0 + i);
   }
   if (!rc && sampled) rc = sample_step(e);
+  // generated token i runs at position pos0 + n - 1 + i
   for (int i = 1; i < n_gen && !rc; ++i) {
-    rc = run_token(e);
+    rc = run_token(e, pos0 + n - 1 + i);
     if (!rc && sampled) rc = sample_step(e);
   }
   const int rc2 = set_sample_mode(e, false);
@@ -847,7 +894,7 @@ int mcpm_engine_decode_steps(mcpm_engine* e, int n_steps) {
     MCPM_HIP(hipMemcpy(e->st, &st, sizeof(st), hipMemcpyHostToDevice));
   }
   for (int i = 0; i < n_steps; ++i) {
-    const int rc = run_token(e);
+    const int rc = run_token(e, e->next_pos + i);
     if (rc) return rc;
   }
   e->gen_count += n_steps;
@@ -879,7 +926,7 @@ int mcpm_engine_decode_sampled(mcpm_engine* e, int n_steps, float temperature, f
   set_sampling(e, temperature, top_p);
   rc = upload_draws(e, seed, e->gen_count, n_steps);
   for (int i = 0; i < n_steps && !rc; ++i) {
-    rc = run_token(e);
+    rc = run_token(e, e->next_pos + i);
     if (!rc) rc = sample_step(e);
   }
   const int rc2 = set_sample_mode(e, false);

@@ -1288,6 +1288,7 @@ hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, 
 #define MCPM_PE(PP, EE) \
   if (prologue == PP && epilogue == EE) return launch_pe<PP, EE>(b, sh, n_cu, s);
   MCPM_PE(PRO_Q8K, EPI_STORE)
+  MCPM_PE(PRO_Q8K, EPI_RESID)
   MCPM_PE(PRO_QUANT_EVEN, EPI_STORE)
   MCPM_PE(PRO_QUANT_EVEN, EPI_RESID)
   MCPM_PE(PRO_ATTN_EVEN, EPI_RESID)

@@ -300,6 +300,18 @@ hipError_t launch_kv_append(const float* k, const float* v, float* kc, float* vc
                             hipStream_t s);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, const int* state, int n_heads,
                             int n_kv_heads, int head_dim, int max_chunks, const AttnPart& part, hipStream_t s);
+// Decode attention for contexts of at most ATTN_Q8K_MAX_CHUNKS chunks (512
+// positions), head_dim 64, one work group per kv head, its output combined and quantized ties-even into Q8_K blocks
+// (for the O projection); shapes whose query group covers whole blocks.
+// A longer context sets *err and writes nothing.
+constexpr int ATTN_Q8K_MAX_CHUNKS = 8;
+constexpr int ATTN_Q8K_CHUNKS = 2;  // the decode engine's default limit
+inline bool attn_q8k_fits(int n_heads, int n_kv_heads, int head_dim) {
+  return n_kv_heads > 0 && head_dim == 64 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8 &&
+         (n_heads / n_kv_heads * head_dim) % 256 == 0;
+}
+hipError_t launch_attention_q8k(const float* q, const float* kc, const float* vc, const int* state, int n_heads,
+                                int n_kv_heads, int head_dim, BlockQ8K* out, unsigned* err, hipStream_t s);
 hipError_t launch_attn_combine(const AttnPart& part, const int* state, int n_heads, int head_dim, int max_chunks,
                                float* out, hipStream_t s);
 

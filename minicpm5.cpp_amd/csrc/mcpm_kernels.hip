@@ -284,6 +284,150 @@ __global__ void __launch_bounds__(256) k_attention(const float* __restrict__ q, 
                          n_kv_heads, hd, max_chunks, part_o, part_mz, AttnLds<HDM>(lds), R, false);
 }
 
+static_assert(ATTN_Q8K_MAX_CHUNKS == ATTN_CPW, "one work group holds every chunk's o_c in registers");
+
+// Decode, contexts of at most ATTN_CPW chunks, head_dim 64: one work group of
+// four 256-thread groups per kv head.  Group g runs chunks g and g + 4 (the
+// splits' arithmetic, attn_token_chunk on its own staged K and V rows; the
+// query rows are shared), the groups' waves sharing each SIMD; then the work
+// group combines the chunks with the consumers' arithmetic (m = max m_c;
+// f_c = exp(m_c - m); Z = fma(z_c, f_c, Z); O = fma(o_c, f_c, O); O / Z) and
+// quantizes its heads' outputs ties-even into Q8_K blocks (the group's
+// gh = group*64 values are gh/256 whole blocks: block kvh*gh/256 + r), so
+// the O projection reads them as they are.  A longer context sets *err and
+// writes nothing.
+constexpr int AQ_GROUPS = 4;
+struct AttnQ8kLds {
+  static constexpr int K = ATTN_CHUNK * 68, V = ATTN_CHUNK * 64, E = ATTN_MAX_GROUP * ATTN_CHUNK;
+  static constexpr int PER = K + V + E;                        // floats per group
+  static constexpr int Q = ATTN_MAX_GROUP * 64;
+  static constexpr int MZ = ATTN_CPW * ATTN_MAX_GROUP;        // float2
+  static constexpr size_t bytes = (AQ_GROUPS * PER + Q) * sizeof(float) + MZ * sizeof(float2);
+};
+
+__global__ void __launch_bounds__(256 * AQ_GROUPS) k_attention_q8k(const float* __restrict__ q,
+                                                                   const float* __restrict__ kc,
+                                                                   const float* __restrict__ vc,
+                                                                   const int* __restrict__ state, int n_heads,
+                                                                   int n_kv_heads, BlockQ8K* __restrict__ out,
+                                                                   unsigned* __restrict__ err) {
+  constexpr int HDM = 64, NV = HDM / 16, OPT = ATTN_MAX_GROUP * HDM / 256, KS = HDM + 4;
+  using L = AttnQ8kLds;
+  __shared__ __attribute__((aligned(16))) float lds[L::bytes / sizeof(float)];
+  const int T = state[1] + 1;
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  if (nch > ATTN_CPW) {  // uniform: before any barrier
+    if (blockIdx.x == 0 && threadIdx.x == 0) *err = 1u;
+    return;
+  }
+  const int tid = threadIdx.x, g = tid >> 8, t = tid & 255, kvh = blockIdx.x;
+  const int hd = HDM, group = n_heads / n_kv_heads, gh = group * hd, kvd = n_kv_heads * hd;
+  const int r4 = hd / 4, nf4 = ATTN_CHUNK * r4;
+  const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+  const size_t head_off = static_cast<size_t>(kvh) * hd;
+  float* sK = lds + g * L::PER;
+  float* sV = sK + L::K;
+  float* sE = sV + L::V;
+  float* sQ = lds + AQ_GROUPS * L::PER;
+  float2* sMZ = reinterpret_cast<float2*>(sQ + L::Q);
+  // the queries first (loads complete in order, so their wait leaves the K
+  // and V loads in flight); group 0 stores them
+  const float* qg = q + static_cast<size_t>(kvh) * gh;
+  float qv[OPT];
+#pragma unroll
+  for (int u = 0; u < OPT; ++u) qv[u] = qg[min(t + 256 * u, gh - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  AttnRegs<NV> R;
+  attn_load_chunk<NV>(R, kc, vc, min(g, nch - 1), T, kvd, head_off, r4, nf4, t);
+  if (g == 0) {
+#pragma unroll
+    for (int u = 0; u < OPT; ++u) {
+      const int i = min(t + 256 * u, gh - 1);  // threads past the queries store query gh-1 again
+      sQ[(i / hd) * HDM + i % hd] = qv[u];
+    }
+  }
+  const int rounds = (nch + AQ_GROUPS - 1) / AQ_GROUPS;  // 1 or 2
+  float oc[2][OPT];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if (r < rounds) {  // uniform
+      // chunk c of group g (c >= nch: the group stages a copy of the last
+      // chunk and computes nothing)
+      const int c = g + AQ_GROUPS * r;
+      __syncthreads();  // readers of the previous chunk are done
+#pragma unroll
+      for (int u = 0; u < NV; ++u) {
+        const int f = min(t + 256 * u, nf4 - 1);
+        const int j = f / r4, c4 = f - j * r4;
+        *reinterpret_cast<f32x4*>(&sK[j * KS + c4 * 4]) = R.k[u];
+        *reinterpret_cast<f32x4*>(&sV[j * HDM + c4 * 4]) = R.v[u];
+      }
+      if (r + 1 < rounds) attn_load_chunk<NV>(R, kc, vc, min(c + AQ_GROUPS, nch - 1), T, kvd, head_off, r4, nf4, t);
+      __syncthreads();
+      // uniform in the group; a group past the context only keeps the barriers
+      if (c < nch)
+        attn_token_chunk<HDM, OPT, true>(sK, sV, sQ, sE, sMZ + c * ATTN_MAX_GROUP, c, T, group, hd, gh, scale, oc[r], t);
+    }
+  }
+  // every chunk's o_c into the staging area (each group's own K rows: its
+  // readers are done after the barrier), o_c of chunk c at sO[c*gh + oi]
+  __syncthreads();
+  float* sO = lds;  // ATTN_CPW * 512 floats at most: within group 0's K and V rows
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = g + AQ_GROUPS * r;
+    if (r < rounds && c < nch) {
+#pragma unroll
+      for (int u = 0; u < OPT; ++u) {
+        const int oi = t + 256 * u;
+        if (oi < gh) sO[c * gh + oi] = oc[r][u];
+      }
+    }
+  }
+  __syncthreads();
+  float* sX = lds + 2 * L::PER;  // group 2's area: gh floats
+  if (tid < gh) {
+    const int oi = tid, hh = oi / hd;
+    float m = sMZ[hh].x;
+    for (int cc = 1; cc < nch; ++cc) m = fmaxf(m, sMZ[cc * ATTN_MAX_GROUP + hh].x);
+    float Z = 0.0f, O = 0.0f;
+    for (int cc = 0; cc < nch; ++cc) {
+      const float2 mz = sMZ[cc * ATTN_MAX_GROUP + hh];
+      const float f = exp_f32(mz.x - m);
+      Z = __builtin_fmaf(mz.y, f, Z);
+      O = __builtin_fmaf(sO[cc * gh + oi], f, O);
+    }
+    sX[oi] = O / Z;
+  }
+  __syncthreads();
+  // block r of the group on row r (16 lanes) of wave 0, lane j holding
+  // values 16j .. 16j+15: the GEMV prologue's quantization
+  const int row = tid >> 4, j = tid & 15;
+  if (tid < 64 && 256 * row < gh) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 x4 = *reinterpret_cast<const f32x4*>(&sX[256 * row + 16 * j + 4 * i]);
+      v[4 * i] = x4.x;
+      v[4 * i + 1] = x4.y;
+      v[4 * i + 2] = x4.z;
+      v[4 * i + 3] = x4.w;
+    }
+    u32x4 packed;
+    float d;
+    int gsum;
+    quant_block_row16(v, false, packed, d, gsum);
+    BlockQ8K* blk = out + kvh * (gh / QK_K) + row;
+    uint32_t* qs = reinterpret_cast<uint32_t*>(blk->qs) + 4 * j;  // 4-byte aligned
+    qs[0] = packed.x;
+    qs[1] = packed.y;
+    qs[2] = packed.z;
+    qs[3] = packed.w;
+    blk->bsums[j] = static_cast<int16_t>(gsum);
+    if (j == 0) blk->d = d;
+  }
+}
+
 // Prefill: chunk blockIdx.y of kv head blockIdx.x for the tile of tt
 // consecutive tokens from blockIdx.z * tt (token z at position pos0 + z,
 // its own q and partials).  The chunk's K and V rows are staged once; the
@@ -449,6 +593,14 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, co
   else
     launch_kernel(k_attention<128, false>, grid, dim3(256), 0, s, q, kc, vc, state, n_heads, n_kv_heads, head_dim,
                   max_chunks, part.o, part.mz, -1, size_t{0}, size_t{0}, size_t{0});
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_q8k(const float* q, const float* kc, const float* vc, const int* state, int n_heads,
+                                int n_kv_heads, int head_dim, BlockQ8K* out, unsigned* err, hipStream_t s) {
+  if (!attn_q8k_fits(n_heads, n_kv_heads, head_dim)) return hipErrorInvalidValue;
+  launch_kernel(k_attention_q8k, dim3(n_kv_heads), dim3(256 * AQ_GROUPS), 0, s, q, kc, vc, state, n_heads, n_kv_heads,
+                out, err);
   return hipGetLastError();
 }
 

@@ -278,6 +278,56 @@ def test_long_context_greedy_matches_oracle(ctx, n_prompt):
     assert got == want
 
 
+def test_per_head_attention_matches_oracle(ctx, monkeypatch):
+    """Short contexts run one attention work group per kv head that combines
+    its chunks and hands the O projection Q8_K blocks; longer ones run the
+    splits and the O projection's combine.  With the per-head path allowed up
+    to its limit (MCPM_ATTN_Q8K=8: 8 chunks, two rounds of its four chunk
+    groups), logits bit-identical to the oracle at every position 0..519
+    (both paths, and the switch between their graphs at 512); greedy tokens
+    across 512 and across the default switch (128) equal to the oracle's and
+    to the split path's alone (MCPM_ATTN_Q8K=0)."""
+    cfg = mcpm.make_config(2, 1024, 16, 4, 64, 2048, 1000)
+    img = mcpm.synth_gguf(cfg, seed=515, mix=0)
+    rng = np.random.default_rng(23)
+    toks = [int(t) for t in rng.integers(0, 1000, 520)]
+    om = O.OracleModel(img)
+    om.init_kv(600)
+    want = np.empty(1000, np.float32)
+    monkeypatch.setenv("MCPM_ATTN_Q8K", "8")
+    eng = mcpm.Engine(ctx, image=img)
+    try:
+        eng.init_kv_cache(600)
+        announce("per-kv-head attention: forward at positions 0..519")
+        for pos, t in enumerate(toks):
+            got, _ = eng.forward(t, pos)
+            om.forward(t, pos, want)
+            assert_bits(got, want)
+    finally:
+        eng.free()
+    om.close()
+    om = O.OracleModel(img)
+    want_long = list(om.generate_greedy(toks[:490], 30))
+    om.close()
+    om = O.OracleModel(img)
+    want_short = list(om.generate_greedy(toks[:100], 40))
+    om.close()
+    for mode in ("8", None, "0"):
+        if mode is None:
+            monkeypatch.delenv("MCPM_ATTN_Q8K", raising=False)
+        else:
+            monkeypatch.setenv("MCPM_ATTN_Q8K", mode)
+        announce(f"per-kv-head attention: greedy, MCPM_ATTN_Q8K={mode}")
+        eng = mcpm.Engine(ctx, image=img)
+        try:
+            eng.init_kv_cache(600)
+            eng.set_prefill(False)
+            assert list(eng.generate_greedy(toks[:490], 30)) == want_long
+            assert list(eng.generate_greedy(toks[:100], 40)) == want_short
+        finally:
+            eng.free()
+
+
 @pytest.mark.parametrize("prefill", [True, False])
 def test_generate_at_reuses_cached_rows(ctx, prefill):
     """mcpm_engine_generate_{greedy,sampled}_at: a second turn that keeps the
