@@ -330,20 +330,14 @@ __global__ void __launch_bounds__(256 * AQ_GROUPS) k_attention_q8k(const float* 
   float* sE = sV + L::V;
   float* sQ = lds + AQ_GROUPS * L::PER;
   float2* sMZ = reinterpret_cast<float2*>(sQ + L::Q);
-  // the queries first (loads complete in order, so their wait leaves the K
-  // and V loads in flight); group 0 stores them
-  const float* qg = q + static_cast<size_t>(kvh) * gh;
-  float qv[OPT];
-#pragma unroll
-  for (int u = 0; u < OPT; ++u) qv[u] = qg[min(t + 256 * u, gh - 1)];
-  __builtin_amdgcn_sched_barrier(0);
   AttnRegs<NV> R;
   attn_load_chunk<NV>(R, kc, vc, min(g, nch - 1), T, kvd, head_off, r4, nf4, t);
-  if (g == 0) {
+  if (g == 0) {  // group 0 stages the queries for every group
+    const float* qg = q + static_cast<size_t>(kvh) * gh;
 #pragma unroll
     for (int u = 0; u < OPT; ++u) {
       const int i = min(t + 256 * u, gh - 1);  // threads past the queries store query gh-1 again
-      sQ[(i / hd) * HDM + i % hd] = qv[u];
+      sQ[(i / hd) * HDM + i % hd] = qg[i];
     }
   }
   const int rounds = (nch + AQ_GROUPS - 1) / AQ_GROUPS;  // 1 or 2
