@@ -331,7 +331,7 @@ __global__ void __launch_bounds__(256 * AQ_GROUPS) k_attention_q8k(const float* 
   float* sQ = lds + AQ_GROUPS * L::PER;
   float2* sMZ = reinterpret_cast<float2*>(sQ + L::Q);
   AttnRegs<NV> R;
-  attn_load_chunk<NV>(R, kc, vc, min(g, nch - 1), T, kvd, head_off, r4, nf4, t);
+  if (g < nch) attn_load_chunk<NV>(R, kc, vc, g, T, kvd, head_off, r4, nf4, t);  // uniform in the group
   if (g == 0) {  // group 0 stages the queries for every group
     const float* qg = q + static_cast<size_t>(kvh) * gh;
 #pragma unroll
@@ -345,20 +345,22 @@ __global__ void __launch_bounds__(256 * AQ_GROUPS) k_attention_q8k(const float* 
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     if (r < rounds) {  // uniform
-      // chunk c of group g (c >= nch: the group stages a copy of the last
-      // chunk and computes nothing)
+      // chunk c of group g; a group past the context (c >= nch, uniform in
+      // the group) loads, stages and computes nothing and only keeps the
+      // barriers
       const int c = g + AQ_GROUPS * r;
       __syncthreads();  // readers of the previous chunk are done
+      if (c < nch) {
 #pragma unroll
-      for (int u = 0; u < NV; ++u) {
-        const int f = min(t + 256 * u, nf4 - 1);
-        const int j = f / r4, c4 = f - j * r4;
-        *reinterpret_cast<f32x4*>(&sK[j * KS + c4 * 4]) = R.k[u];
-        *reinterpret_cast<f32x4*>(&sV[j * HDM + c4 * 4]) = R.v[u];
+        for (int u = 0; u < NV; ++u) {
+          const int f = min(t + 256 * u, nf4 - 1);
+          const int j = f / r4, c4 = f - j * r4;
+          *reinterpret_cast<f32x4*>(&sK[j * KS + c4 * 4]) = R.k[u];
+          *reinterpret_cast<f32x4*>(&sV[j * HDM + c4 * 4]) = R.v[u];
+        }
+        if (c + AQ_GROUPS < nch) attn_load_chunk<NV>(R, kc, vc, c + AQ_GROUPS, T, kvd, head_off, r4, nf4, t);
       }
-      if (r + 1 < rounds) attn_load_chunk<NV>(R, kc, vc, min(c + AQ_GROUPS, nch - 1), T, kvd, head_off, r4, nf4, t);
       __syncthreads();
-      // uniform in the group; a group past the context only keeps the barriers
       if (c < nch)
         attn_token_chunk<HDM, OPT, true>(sK, sV, sQ, sE, sMZ + c * ATTN_MAX_GROUP, c, T, group, hd, gh, scale, oc[r], t);
     }
