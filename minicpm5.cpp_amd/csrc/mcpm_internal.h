@@ -305,7 +305,7 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, co
 // (for the O projection); shapes whose query group covers whole blocks.
 // A longer context sets *err and writes nothing.
 constexpr int ATTN_Q8K_MAX_CHUNKS = 8;
-constexpr int ATTN_Q8K_CHUNKS = 2;  // the decode engine's default limit
+constexpr int ATTN_Q8K_CHUNKS = 3;  // the decode engine's default limit
 inline bool attn_q8k_fits(int n_heads, int n_kv_heads, int head_dim) {
   return n_kv_heads > 0 && head_dim == 64 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8 &&
          (n_heads / n_kv_heads * head_dim) % 256 == 0;

@@ -285,7 +285,7 @@ def test_per_head_attention_matches_oracle(ctx, monkeypatch):
     to its limit (MCPM_ATTN_Q8K=8: 8 chunks, two rounds of its four chunk
     groups), logits bit-identical to the oracle at every position 0..519
     (both paths, and the switch between their graphs at 512); greedy tokens
-    across 512 and across the default switch (128) equal to the oracle's and
+    across 512 and across the default switch (192) equal to the oracle's and
     to the split path's alone (MCPM_ATTN_Q8K=0)."""
     cfg = mcpm.make_config(2, 1024, 16, 4, 64, 2048, 1000)
     img = mcpm.synth_gguf(cfg, seed=515, mix=0)
@@ -310,7 +310,7 @@ def test_per_head_attention_matches_oracle(ctx, monkeypatch):
     want_long = list(om.generate_greedy(toks[:490], 30))
     om.close()
     om = O.OracleModel(img)
-    want_short = list(om.generate_greedy(toks[:100], 40))
+    want_short = list(om.generate_greedy(toks[:170], 40))
     om.close()
     for mode in ("8", None, "0"):
         if mode is None:
@@ -323,7 +323,7 @@ def test_per_head_attention_matches_oracle(ctx, monkeypatch):
             eng.init_kv_cache(600)
             eng.set_prefill(False)
             assert list(eng.generate_greedy(toks[:490], 30)) == want_long
-            assert list(eng.generate_greedy(toks[:100], 40)) == want_short
+            assert list(eng.generate_greedy(toks[:170], 40)) == want_short
         finally:
             eng.free()
 
