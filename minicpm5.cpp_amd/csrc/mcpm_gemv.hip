@@ -1140,6 +1140,12 @@ Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
         return Shape{true, s, -kb, GEMV_TILE_WAVES, true};
     }
   }
+  // the O projection (a residual epilogue after a ties-even or given Q8_K
+  // input): work-group items of 16 rows (2.4B shape, 256-token decode: 9.4
+  // -> 8.9 us per launch at contexts past 192, 696 -> 704 tok/s; 8, 12, 14,
+  // 20, 24 and 32 rows and the one-wave items of 3-8 rows were slower)
+  if (epilogue == EPI_RESID && prologue != PRO_QUANT_AWAY && grp_ok && 16 * nb <= 256 && items_for(a, 16) <= n_cu)
+    return Shape{true, 16, 1, GEMV_TILE_WAVES, true};
   const int cap = 4 * n_cu;
   const int row_items = items_for(a, 64);
   if (row_items >= cap) return Shape{false, 64, nb, waves_for(row_items, n_cu)};
