@@ -1156,7 +1156,12 @@ Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
       if (best.S == 0 || (S % 4 == 0 && best.S % 4 != 0)) best.S = S;
     }
     if (best.S) {
-      const int sg = std::min(64, 256 / nb);
+      // work-group items: the fewest rows per item that still give at most
+      // one item per CU (the down projection of the 2.4B shape: 9 rows, 256
+      // items, 8.7 -> 8.25 us per launch against the most rows one step
+      // holds, 11; decode 702.9 -> 711.5 tok/s)
+      int sg = std::min(64, 256 / nb);
+      while (grp_ok && sg > 1 && items_for(a, sg - 1) <= n_cu) --sg;  // grp_ok: not paired (no S/2)
       if (kb >= 2 && grp_ok && sg >= 1 && items_for(a, sg) <= n_cu) return Shape{true, sg, 1, GEMV_TILE_WAVES, true};
       return best;
     }
