@@ -258,6 +258,16 @@ int mcpm_sample_logits(const float *logits, int n, float temperature, float top_
 /* 1: replay each token as one captured hipGraph (default); 0: eager launches. */
 int mcpm_engine_set_graph(mcpm_engine *e, int enable);
 
+/* 1 (MCPM_PERSIST=1 in the environment at load sets it; default 0): where
+ * the model's shape and the KV capacity fit (8 kv heads of 64, 4 query heads
+ * per kv head, a CU count that is a multiple of 8, at most 2 attention chunks
+ * of 64 positions per CU), every layer of a token runs in one persistent
+ * launch, the per-token loop of MiniCPM5Engine::forward (src/model.cpp:171-226)
+ * as one kernel; 0: five launches per layer.  Results are the same. */
+int mcpm_engine_set_persistent(mcpm_engine *e, int enable);
+/* 1 when the next token runs its layers in one launch. */
+int mcpm_engine_uses_persistent(const mcpm_engine *e);
+
 /* Processes tokens[0..n) at positions pos0.. through every layer together
  * (MFMA GEMMs), leaving the KV cache exactly as n calls of
  * mcpm_engine_forward would; produces no logits.  Replaces the reference's
@@ -278,7 +288,8 @@ int mcpm_engine_read_kv(mcpm_engine *e, int layer, int pos0, int n, float *k, fl
 #define MCPM_KC_GATE_UP 3
 #define MCPM_KC_DOWN 4
 #define MCPM_KC_LM_HEAD 5
-#define MCPM_KC_COUNT 6
+#define MCPM_KC_LAYERS 6 /* the persistent launch of every layer */
+#define MCPM_KC_COUNT 7
 /* When enabled, HIP events bracket every launch of `kernel_class` on the
  * engine stream (inside the captured graph too); mcpm_engine_kernel_time
  * returns the summed milliseconds and launch count since the last reset. */

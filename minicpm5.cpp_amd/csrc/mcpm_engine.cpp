@@ -1,7 +1,9 @@
 // mcpm_engine.cpp -- the decode engine: GGUF load into HBM, KV cache, the
 // per-token kernel sequence (captured as one hipGraph) and the decode loops.
 //
-// One token (src/model.cpp:142-242), five fused kernels per layer:
+// One token (src/model.cpp:142-242): where the shape fits, every layer in
+// one persistent launch (mcpm_persist.hip); otherwise five fused kernels per
+// layer:
 //   qkv    RMSNorm+Q8_K (lround) prologue, Q/K/V GEMV, RoPE + KV append epilogue
 //   attn   split softmax over 64-position chunks, last wave combines
 //   oproj  Q8_K (ties-even) prologue, O GEMV, residual add epilogue
@@ -21,6 +23,7 @@
 
 #include "gguf.h"
 #include "mcpm_host.h"
+#include "mcpm_persist.h"
 
 using namespace mcpm;
 
@@ -115,13 +118,32 @@ struct mcpm_engine {
   bool fused_ffn = false;
   bool fused_attn = false;  // QKV and attention in one launch (launch_qkv_attn)
   unsigned* gsync = nullptr;  // GRID_SYNC_WORDS words
+  // every layer of a token in one persistent launch, where the shape fits:
+  // the plan for the current KV cache, each work group's weight slabs, the
+  // hand-off records, launch count and error word, and the launch's
+  // arguments in device memory
+  bool pd_want = false;  // MCPM_PERSIST=1 or mcpm_engine_set_persistent(1) turn it on
+  bool pd_ready = false;
+  PdShape pd{};
+  PdLayer* d_pd_layers = nullptr;
+  uint8_t* pd_slab = nullptr;
+  int pd_slab_stride = 0;  // layout the slab was built for
+  uint64_t* pd_rec = nullptr;
+  unsigned* pd_sync = nullptr;  // [0] launch count, [64] error word
+  float* pd_norms = nullptr;    // [L][2][dim] RMSNorm gains
+  PdArgs pd_args{};
 };
 
 namespace {
 
+// The context's stream is non-blocking: it does not wait for the null stream,
+// where hipMemset and hipMemcpy run.  Every fill or copy that work on the
+// context's stream reads is therefore complete before the call that made it
+// returns (or runs on the context's stream itself).
 int alloc_dev(void** p, size_t bytes) {
   MCPM_HIP(hipMalloc(p, bytes ? bytes : 4));
   MCPM_HIP(hipMemset(*p, 0, bytes ? bytes : 4));
+  MCPM_HIP(hipStreamSynchronize(nullptr));
   return MCPM_OK;
 }
 
@@ -163,7 +185,9 @@ void free_engine(mcpm_engine* e) {
                   static_cast<void*>(e->st), static_cast<void*>(e->out_tokens), static_cast<void*>(e->kc),
                   static_cast<void*>(e->vc), static_cast<void*>(e->rope), static_cast<void*>(e->attn_part),
                   e->d_sample, static_cast<void*>(e->gsync), static_cast<void*>(e->d_draws),
-                  static_cast<void*>(e->att_q8), static_cast<void*>(e->attn_err)})
+                  static_cast<void*>(e->att_q8), static_cast<void*>(e->attn_err), static_cast<void*>(e->d_pd_layers),
+                  static_cast<void*>(e->pd_slab), static_cast<void*>(e->pd_rec), static_cast<void*>(e->pd_sync),
+                  static_cast<void*>(e->pd_norms)})
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
   free_prefill(e->pf);
@@ -295,6 +319,8 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
     e->fused_ffn = f && std::atoi(f) != 0;
     const char* a = std::getenv("MCPM_FUSED_ATTN");
     e->fused_attn = a && std::atoi(a) != 0;
+    const char* pv = std::getenv("MCPM_PERSIST");
+    e->pd_want = pv && std::atoi(pv) != 0;
   }
   *out = e;
   return MCPM_OK;
@@ -350,19 +376,39 @@ hipError_t timed(mcpm_engine* e, int kc, F&& launch) {
 // (spin limit) left its error word set; report it and reset the barrier
 // state for the next launches.
 int check_grid_sync(mcpm_engine* e) {
+  hipStream_t s = e->ctx->stream;
   if (e->attn_q8k) {
     unsigned aerr = 0;
-    MCPM_HIP(hipMemcpy(&aerr, e->attn_err, sizeof aerr, hipMemcpyDeviceToHost));
+    MCPM_HIP(hipMemcpyAsync(&aerr, e->attn_err, sizeof aerr, hipMemcpyDeviceToHost, s));
+    MCPM_HIP(hipStreamSynchronize(s));
     if (aerr) {
-      MCPM_HIP(hipMemset(e->attn_err, 0, sizeof(unsigned)));
+      MCPM_HIP(hipMemsetAsync(e->attn_err, 0, sizeof(unsigned), s));
+      MCPM_HIP(hipStreamSynchronize(s));
       return fail(MCPM_ERR_HIP, "the per-kv-head attention ran past its context limit; results of the call are invalid");
+    }
+  }
+  if (e->pd_ready) {
+    unsigned perr = 0;
+    MCPM_HIP(hipMemcpyAsync(&perr, e->pd_sync + 64, sizeof perr, hipMemcpyDeviceToHost, s));
+    MCPM_HIP(hipStreamSynchronize(s));
+    if (perr) {
+      // records of the abandoned launch may carry tags a later launch would
+      // take: clear them and restart the launch count
+      const unsigned init[1] = {1u};
+      MCPM_HIP(hipMemsetAsync(e->pd_rec, 0, pd_records(e->pd) * sizeof(uint64_t), s));
+      MCPM_HIP(hipMemsetAsync(e->pd_sync, 0, 128 * sizeof(unsigned), s));
+      MCPM_HIP(hipMemcpyAsync(e->pd_sync, init, sizeof init, hipMemcpyHostToDevice, s));
+      MCPM_HIP(hipStreamSynchronize(s));
+      return fail(MCPM_ERR_HIP, "the persistent decode launch gave up waiting (spin limit); results of the call are invalid");
     }
   }
   if (!e->fused_ffn && !e->fused_attn) return MCPM_OK;
   unsigned err = 0;
-  MCPM_HIP(hipMemcpy(&err, e->gsync + 8 * 64 + 64, sizeof err, hipMemcpyDeviceToHost));
+  MCPM_HIP(hipMemcpyAsync(&err, e->gsync + 8 * 64 + 64, sizeof err, hipMemcpyDeviceToHost, s));
+  MCPM_HIP(hipStreamSynchronize(s));
   if (!err) return MCPM_OK;
-  MCPM_HIP(hipMemset(e->gsync, 0, GRID_SYNC_WORDS * sizeof(unsigned)));
+  MCPM_HIP(hipMemsetAsync(e->gsync, 0, GRID_SYNC_WORDS * sizeof(unsigned), s));
+  MCPM_HIP(hipStreamSynchronize(s));
   return fail(MCPM_ERR_HIP, "a fused kernel's grid barrier timed out; results of the call are invalid");
 }
 
@@ -375,8 +421,12 @@ int enqueue_token(mcpm_engine* e, bool short_ctx) {
   const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
   const int* st = reinterpret_cast<const int*>(e->st);
   const bool q8k = short_ctx && e->attn_q8k && !e->fused_attn;
-  MCPM_HIP(launch_embedding(view_of(e->embd), st, c.dim, e->x, s));
-  for (int l = 0; l < c.n_layers; ++l) {
+  const bool persist = e->pd_ready && e->pd_want;
+  if (persist)
+    MCPM_HIP(timed(e, MCPM_KC_LAYERS, [&] { return launch_decode_persist(e->pd_args, s); }));
+  else
+    MCPM_HIP(launch_embedding(view_of(e->embd), st, c.dim, e->x, s));
+  for (int l = 0; l < c.n_layers && !persist; ++l) {
     const Layer& L = e->L[l];
     float* kc = e->kc + static_cast<size_t>(l) * e->max_seq * kvd;
     float* vc = e->vc + static_cast<size_t>(l) * e->max_seq * kvd;
@@ -620,6 +670,84 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
   return MCPM_OK;
 }
 
+// The persistent decode path for the current KV cache: plan, weight slabs
+// (built once per layout), hand-off records, launch count and arguments.
+// Leaves pd_ready false (the five-launch path) when the shape or the
+// context does not fit.
+int pd_setup(mcpm_engine* e) {
+  e->pd_ready = false;
+  const mcpm_model_config& c = e->cfg;
+  if (!e->kc || c.n_layers <= 0) return MCPM_OK;
+  const Layer& L0 = e->L[0];
+  PdShape s{};
+  const char* why = nullptr;
+  if (!pd_plan(c, e->ctx->n_cu, e->max_seq, L0.wq.type, L0.wk.type, L0.wv.type, L0.wo.type, L0.wd.type, s, &why))
+    return MCPM_OK;
+  if (prepare_decode_persist(s) != hipSuccess) return MCPM_OK;
+  // every layer must have the first layer's types (the slab layout's)
+  for (const Layer& l : e->L)
+    if (l.wq.type != s.sq.type || l.wk.type != s.sk.type || l.wv.type != s.sv.type || l.wo.type != s.so.type ||
+        l.wd.type != s.sd.type || l.wg.type != MCPM_TYPE_Q4_K || l.wu.type != MCPM_TYPE_Q4_K)
+      return MCPM_OK;
+  hipStream_t st = e->ctx->stream;
+  MCPM_HIP(hipStreamSynchronize(st));
+  if (!e->pd_slab || e->pd_slab_stride != s.slab_stride || e->pd.G != s.G) {
+    if (e->pd_slab) (void)hipFree(e->pd_slab);
+    if (e->d_pd_layers) (void)hipFree(e->d_pd_layers);
+    e->pd_slab = nullptr;
+    e->d_pd_layers = nullptr;
+    std::vector<PdLayer> hl(c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+      const Layer& y = e->L[l];
+      hl[l] = PdLayer{y.attn_norm, y.ffn_norm, view_of(y.wq), view_of(y.wk), view_of(y.wv), view_of(y.wo),
+                      view_of(y.wg), view_of(y.wu), view_of(y.wd)};
+    }
+    const size_t slab_bytes = static_cast<size_t>(c.n_layers) * s.G * s.slab_stride;
+    int rc = alloc_dev(reinterpret_cast<void**>(&e->d_pd_layers), hl.size() * sizeof(PdLayer));
+    if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->pd_slab), slab_bytes);
+    if (rc) return rc;
+    MCPM_HIP(hipMemcpyAsync(e->d_pd_layers, hl.data(), hl.size() * sizeof(PdLayer), hipMemcpyHostToDevice, st));
+    MCPM_HIP(launch_build_slab(s, e->d_pd_layers, e->pd_slab, st));
+    MCPM_HIP(hipStreamSynchronize(st));
+    e->pd_slab_stride = s.slab_stride;
+  }
+  if (e->pd_rec) (void)hipFree(e->pd_rec);
+  e->pd_rec = nullptr;
+  int rc = alloc_dev(reinterpret_cast<void**>(&e->pd_rec), pd_records(s) * sizeof(uint64_t));
+  if (!rc && !e->pd_sync) rc = alloc_dev(reinterpret_cast<void**>(&e->pd_sync), 128 * sizeof(unsigned));
+  if (!rc && !e->pd_norms)
+    rc = alloc_dev(reinterpret_cast<void**>(&e->pd_norms), static_cast<size_t>(c.n_layers) * 2 * c.dim * sizeof(float));
+  if (rc) return rc;
+  for (int l = 0; l < c.n_layers; ++l) {
+    float* dst = e->pd_norms + static_cast<size_t>(2 * l) * c.dim;
+    MCPM_HIP(hipMemcpyAsync(dst, e->L[l].attn_norm, c.dim * sizeof(float), hipMemcpyDeviceToDevice, st));
+    MCPM_HIP(hipMemcpyAsync(dst + c.dim, e->L[l].ffn_norm, c.dim * sizeof(float), hipMemcpyDeviceToDevice, st));
+  }
+  const unsigned init[2] = {1u, 0u};  // launch count 1: no record (all zero) carries a tag
+  MCPM_HIP(hipMemsetAsync(e->pd_sync, 0, 128 * sizeof(unsigned), st));
+  MCPM_HIP(hipMemcpyAsync(e->pd_sync, init, sizeof(unsigned), hipMemcpyHostToDevice, st));
+  MCPM_HIP(hipStreamSynchronize(st));
+  PdArgs a{};
+  a.s = s;
+  a.norms = e->pd_norms;
+  a.slab = e->pd_slab;
+  a.kc = e->kc;
+  a.vc = e->vc;
+  a.max_seq = e->max_seq;
+  a.rope = e->rope;
+  a.state = reinterpret_cast<const int*>(e->st);
+  a.embd = view_of(e->embd);
+  pd_bind_records(a, e->pd_rec);
+  a.epoch = e->pd_sync;
+  a.err = e->pd_sync + 64;
+  a.spin_limit = 1u << 18;
+  a.x_out = e->x;
+  e->pd_args = a;
+  e->pd = s;
+  e->pd_ready = true;
+  return MCPM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -712,13 +840,14 @@ int mcpm_engine_init_kv_cache(mcpm_engine* e, int max_seq_len) {
   std::vector<float2> tab(static_cast<size_t>(max_seq_len) * (c.head_dim / 2));
   for (int p = 0; p < max_seq_len; ++p) rope_row(p, c.head_dim, c.rope_base, tab.data() + static_cast<size_t>(p) * (c.head_dim / 2));
   MCPM_HIP(hipMalloc(&e->rope, tab.size() * sizeof(float2)));
-  MCPM_HIP(hipMemcpy(e->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+  MCPM_HIP(hipMemcpyAsync(e->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice, e->ctx->stream));
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
   e->max_chunks = (max_seq_len + ATTN_CHUNK - 1) / ATTN_CHUNK;
   rc = alloc_dev(reinterpret_cast<void**>(&e->attn_part),
                  static_cast<size_t>(c.n_heads) * e->max_chunks * (2 + c.head_dim) * sizeof(float));
   if (rc) return rc;
   e->max_seq = max_seq_len;
-  return MCPM_OK;
+  return pd_setup(e);
 }
 
 int mcpm_engine_set_graph(mcpm_engine* e, int enable) {
@@ -728,6 +857,16 @@ int mcpm_engine_set_graph(mcpm_engine* e, int enable) {
   drop_graph(e);
   return MCPM_OK;
 }
+
+int mcpm_engine_set_persistent(mcpm_engine* e, int enable) {
+  if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_set_persistent: null engine");
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  e->pd_want = enable != 0;
+  drop_graph(e);
+  return MCPM_OK;
+}
+
+int mcpm_engine_uses_persistent(const mcpm_engine* e) { return e && e->pd_ready && e->pd_want ? 1 : 0; }
 
 int mcpm_engine_forward(mcpm_engine* e, int token, int pos, int max_seq_len, float* logits, int* argmax) {
   if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_forward: null engine");
@@ -886,12 +1025,15 @@ int mcpm_engine_decode_steps(mcpm_engine* e, int n_steps) {
     MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
     int rc = ensure_out_tokens(e, e->gen_count + n_steps);
     if (rc) return rc;
-    MCPM_HIP(hipMemcpy(e->out_tokens, keep.data(), keep.size() * sizeof(int), hipMemcpyHostToDevice));
+    hipStream_t s = e->ctx->stream;
+    MCPM_HIP(hipMemcpyAsync(e->out_tokens, keep.data(), keep.size() * sizeof(int), hipMemcpyHostToDevice, s));
     // the state's capacity field must follow the new array
     StepState st;
-    MCPM_HIP(hipMemcpy(&st, e->st, sizeof(st), hipMemcpyDeviceToHost));
+    MCPM_HIP(hipMemcpyAsync(&st, e->st, sizeof(st), hipMemcpyDeviceToHost, s));
+    MCPM_HIP(hipStreamSynchronize(s));
     st.n_out = e->out_cap;
-    MCPM_HIP(hipMemcpy(e->st, &st, sizeof(st), hipMemcpyHostToDevice));
+    MCPM_HIP(hipMemcpyAsync(e->st, &st, sizeof(st), hipMemcpyHostToDevice, s));
+    MCPM_HIP(hipStreamSynchronize(s));
   }
   for (int i = 0; i < n_steps; ++i) {
     const int rc = run_token(e, e->next_pos + i);
@@ -987,6 +1129,16 @@ int64_t mcpm_engine_kernel_bytes(const mcpm_engine* e, int kc) {
     case MCPM_KC_ATTN:
       // K and V rows of the current context, the query and the output
       return 2 * static_cast<int64_t>(e->next_pos + 1) * kvd * 4 + 8 * qd;
+    case MCPM_KC_LAYERS: {
+      // every layer's weights and norm gains, one embedding row, and the K
+      // and V rows of the current context
+      int64_t b = static_cast<int64_t>(e->embd.bytes / c.vocab);
+      for (const Layer& y : e->L)
+        b += static_cast<int64_t>(y.wq.bytes + y.wk.bytes + y.wv.bytes + y.wo.bytes + y.wg.bytes + y.wu.bytes +
+                                  y.wd.bytes) +
+             8 * static_cast<int64_t>(c.dim);
+      return b + 2 * static_cast<int64_t>(e->next_pos + 1) * kvd * 4 * c.n_layers;
+    }
     default:
       return 0;
   }

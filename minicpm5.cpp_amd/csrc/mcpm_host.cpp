@@ -624,7 +624,7 @@ int mcpm_sample_device(mcpm_ctx* c, const float* logits, int n, float temperatur
     MCPM_HIP(hipMalloc(&c->d_sample, need));
     // the sampler's bucket masses and gather count start at zero (each call
     // leaves them so)
-    MCPM_HIP(hipMemset(c->d_sample, 0, need));
+    MCPM_HIP(hipMemsetAsync(c->d_sample, 0, need, c->stream));
     c->sample_cap = need;
   }
   MCPM_HIP(launch_sample(c->d_sample, c->sample_cap, logits, n, temperature, top_p, r, out, nullptr, nullptr,

@@ -1,0 +1,208 @@
+// mcpm_persist.h -- the decode layers of one token as one persistent launch
+// (mcpm_persist.hip): its shape plan, shared by the engine (host) and the
+// kernels.
+#pragma once
+
+#include "mcpm_internal.h"
+
+namespace mcpm {
+
+// One weight matrix's rows of a work group inside a region of its slab (and
+// of its LDS): byte offset in the region, rows allocated (the most any work
+// group has; rows past a work group's own are zero) and ggml type.  Layout,
+// nb blocks per row:
+//   Q4_K  16-byte chunk c (0..7 quants, 8 header) of (block b, row i) at
+//         ((b*9 + c)*R + i)*16
+//   Q6_K  chunk c (0..7 ql, 8..11 qh, 12 scales) at ((b*13 + c)*R + i)*16,
+//         then the fp16 d of (b, i) in the low half of dword b*R + i
+// so that consecutive lanes on consecutive rows read consecutive 16 bytes.
+struct PdSub {
+  int off, R, type;
+};
+
+__host__ __device__ inline int pd_sub_bytes(int type, int R, int nb) {
+  return type == MCPM_TYPE_Q4_K ? 144 * R * nb : 208 * R * nb + ((4 * R * nb + 15) & ~15);
+}
+
+constexpr int PD_XCDS = 8;     // work group b runs on XCD b % 8
+constexpr int PD_NBX = 16;     // largest dim / 256
+constexpr int PD_NBH = 32;     // largest ffn_pad / 256
+constexpr int PD_NBQ = 9;      // largest n_heads * head_dim / 256
+constexpr int PD_REC_BLK = 85; // records of one Q8_K block: d, 64 code dwords, 16 bsums, 4 bsum-pair words
+constexpr int PD_ATTN_LDS = ((ATTN_CHUNK * 68 + ATTN_CHUNK * 64 + 8 * 64 + 8 * ATTN_CHUNK) * 4 + 64 * 8 + 15) & ~15;
+
+struct PdShape {
+  int L, G, W;  // layers, work groups (one per CU), work groups per XCD
+  int dim, nbx, qd, nbq, kvd, hd, group, gh, nkv, ffn, ffn_pad, nbh;
+  int nq, nk;          // q rows, and k (= v) rows, of one work group
+  int nh_max, np_max;  // rows of x and FFN pairs of a work group, at most
+  float eps;
+  PdSub sq, sk, sv, so, sg, su, sd;  // sub-regions: offsets within their region
+  int reg_off[4], reg_sz[4];         // regions QKV, O, gate/up, down in a (layer, work group) slab and in LDS
+  int wd_lds;                        // LDS bytes of the down region (the attention's staging shares it)
+  int scr_off;                       // scratch region in LDS (bytes)
+  // scratch, in dwords from scr_off: Q8_K activations (codes, d, bsum
+  // pairs, bsums), the RMS tree, a union area (x staging / chain entries /
+  // attention rows and combine), row values, own x and x after O, flags
+  int s_xs, s_xd, s_xbp, s_xbs, s_red, s_u, s_vrow, s_ownx, s_ownx2, s_misc;
+  int lds_bytes;
+  int slab_stride;  // bytes per (layer, work group)
+  int max_chunks;   // attention partial records per kv head
+};
+
+// Per-layer pointers: norms and the weight planes (the slab builder's source).
+struct PdLayer {
+  const float* attn_norm;
+  const float* ffn_norm;
+  WView q, k, v, o, g, u, d;
+};
+
+// The launch's arguments (by value: pointers in kernel arguments are known to
+// address global memory, so the kernel's accesses through them are global
+// rather than flat, and none is loaded from memory).
+struct PdArgs {
+  PdShape s;
+  const float* norms;     // [L][2][dim]: attention and FFN RMSNorm gains
+  const uint8_t* slab;    // [L][G][slab_stride]
+  float* kc;              // KV cache, [L][max_seq][kvd]
+  float* vc;
+  int max_seq;
+  const float2* rope;     // [max_seq][hd/2] (cos, sin)
+  const int* state;       // token, pos
+  WView embd;
+  // hand-off records (value bits, tag), 64-bit each
+  uint64_t* rx;    // [dim]   x entering a layer
+  uint64_t* rx2;   // [dim]   x after the O projection
+  uint64_t* rh;    // [ffn]   SwiGLU output
+  uint64_t* rqkv;  // [nkv][gh + 2*hd]  q of the head group, K and V rows at pos
+  uint64_t* rpart; // [nkv][max_chunks][gh + 2*group]  chunk partials o_c, m_c, z_c
+  uint64_t* ratt;  // [nbq][PD_REC_BLK]  attention output as Q8_K blocks
+  unsigned* epoch; // launch counter (tags), advanced by each launch
+  unsigned* err;   // set when a wait passed spin_limit
+  unsigned spin_limit;
+  float* x_out;    // x after the last layer (plain stores, for the LM head)
+};
+
+// Rows of work group b.
+struct PdRows {
+  int hr0, nh;  // rows of x: O and down outputs, embedding values
+  int fp0, np;  // FFN pairs (gate row, up row)
+  int kvh, k;   // kv head (= XCD) and index within the XCD
+  int qr0, kr0; // first q row, first k (and v) row
+};
+
+__host__ __device__ inline PdRows pd_rows(const PdShape& s, int b) {
+  PdRows r;
+  r.hr0 = static_cast<int>((static_cast<int64_t>(b) * s.dim) / s.G);
+  r.nh = static_cast<int>((static_cast<int64_t>(b + 1) * s.dim) / s.G) - r.hr0;
+  r.fp0 = static_cast<int>((static_cast<int64_t>(b) * s.ffn) / s.G);
+  r.np = static_cast<int>((static_cast<int64_t>(b + 1) * s.ffn) / s.G) - r.fp0;
+  r.kvh = b % PD_XCDS;
+  r.k = b / PD_XCDS;
+  r.qr0 = r.kvh * s.gh + r.k * s.nq;
+  r.kr0 = r.kvh * s.hd + r.k * s.nk;
+  return r;
+}
+
+// Where slab byte `off` (a multiple of 16) of work group b's layer slab comes
+// from: tensor (0..6: q, k, v, o, gate, up, down; -1: padding, zeros) and
+// either one 16-byte chunk of plane `plane` at byte src[0] (n = 1) or, for
+// a Q6_K d array chunk, four fp16 d's of plane 3 at src[0..3] (n = 4;
+// src[i] < 0: zero).  rows: the tensor's rows (its plane stride).
+struct PdSrc {
+  int tensor, plane, n;
+  int64_t src[4];
+};
+
+__host__ __device__ inline PdSrc pd_slab_src(const PdShape& s, int b, int off, const int (&rows)[7]) {
+  PdSrc out{-1, 0, 0, {-1, -1, -1, -1}};
+  int r = 3;
+  while (r > 0 && off < s.reg_off[r]) --r;
+  const int o = off - s.reg_off[r];
+  const PdRows me = pd_rows(s, b);
+  PdSub sb[3];
+  int tens[3], valid[3], row0[3], nsub, nb;
+  if (r == 0) {
+    sb[0] = s.sq; sb[1] = s.sk; sb[2] = s.sv;
+    tens[0] = 0; tens[1] = 1; tens[2] = 2;
+    valid[0] = s.nq; valid[1] = s.nk; valid[2] = s.nk;
+    row0[0] = me.qr0; row0[1] = me.kr0; row0[2] = me.kr0;
+    nsub = 3;
+    nb = s.nbx;
+  } else if (r == 1) {
+    sb[0] = s.so; tens[0] = 3; valid[0] = me.nh; row0[0] = me.hr0;
+    nsub = 1;
+    nb = s.nbq;
+  } else if (r == 2) {
+    sb[0] = s.sg; sb[1] = s.su;
+    tens[0] = 4; tens[1] = 5;
+    valid[0] = me.np; valid[1] = me.np;
+    row0[0] = me.fp0; row0[1] = me.fp0;
+    nsub = 2;
+    nb = s.nbx;
+  } else {
+    sb[0] = s.sd; tens[0] = 6; valid[0] = me.nh; row0[0] = me.hr0;
+    nsub = 1;
+    nb = s.nbh;
+  }
+  for (int q = 0; q < nsub; ++q) {
+    const int so = o - sb[q].off, R = sb[q].R;
+    if (so < 0 || so >= pd_sub_bytes(sb[q].type, R, nb)) continue;
+    const int64_t nrows = rows[tens[q]];
+    const int kc = so / 16;
+    if (sb[q].type == MCPM_TYPE_Q4_K) {
+      const int row = kc % R, tt = kc / R, c = tt % 9, blk = tt / 9;
+      if (row < valid[q]) {
+        const int64_t gr = row0[q] + row;
+        out.tensor = tens[q];
+        out.n = 1;
+        out.plane = c < 8 ? 0 : 1;
+        out.src[0] = c < 8 ? ((static_cast<int64_t>(blk) * 8 + c) * nrows + gr) * 16 : (blk * nrows + gr) * 16;
+      }
+    } else if (kc < 13 * nb * R) {
+      const int row = kc % R, tt = kc / R, c = tt % 13, blk = tt / 13;
+      if (row < valid[q]) {
+        const int64_t gr = row0[q] + row;
+        out.tensor = tens[q];
+        out.n = 1;
+        out.plane = c < 8 ? 0 : c < 12 ? 1 : 2;
+        out.src[0] = c < 8    ? ((static_cast<int64_t>(blk) * 8 + c) * nrows + gr) * 16
+                     : c < 12 ? ((static_cast<int64_t>(blk) * 4 + (c - 8)) * nrows + gr) * 16
+                              : (blk * nrows + gr) * 16;
+      }
+    } else {
+      const int e0 = (kc - 13 * nb * R) * 4;
+      out.tensor = tens[q];
+      out.plane = 3;
+      out.n = 4;
+      for (int k = 0; k < 4; ++k) {
+        const int e = e0 + k;
+        if (e < nb * R) {
+          const int blk = e / R, row = e % R;
+          if (row < valid[q]) out.src[k] = (blk * nrows + row0[q] + row) * 2;
+        }
+      }
+    }
+  }
+  return out;
+}
+
+// The plan for a model on n_cu CUs with a KV cache of max_seq positions and
+// the given weight types; false (and *why) when the shape does not fit the
+// persistent kernel: n_cu a multiple of 8, 8 kv heads of 64 (head h's rows
+// and attention on XCD h), a head group of one Q8_K block (4 query heads),
+// at most two attention chunks per work group, LDS within 160 KiB.
+bool pd_plan(const mcpm_model_config& c, int n_cu, int max_seq, int tq, int tk, int tv, int to, int td,
+             PdShape& s, const char** why);
+// Copies every layer's weights into the slab layout (device gather).
+hipError_t launch_build_slab(const PdShape& s, const PdLayer* d_layers, uint8_t* slab, hipStream_t st);
+// Record buffer sizes (records) for the shape.
+size_t pd_records(const PdShape& s);
+// Points the record arrays of a at one allocation of pd_records(s) records.
+void pd_bind_records(PdArgs& a, uint64_t* base);
+// The launch's LDS attribute and the check that one work group fits a CU
+// (outside any graph capture); then the launch.
+hipError_t prepare_decode_persist(const PdShape& s);
+hipError_t launch_decode_persist(const PdArgs& a, hipStream_t st);
+
+}  // namespace mcpm

@@ -1,0 +1,1073 @@
+// mcpm_persist.hip -- every decoder layer of one token in one launch
+// (src/model.cpp:171-226, the layer loop of MiniCPM5Engine::forward).
+//
+// The per-token kernel sequence runs five launches per layer; each starts
+// by waiting for the previous launch's last wave and then for its own first
+// weights.  Here one work group per CU (b on XCD b % 8) runs all layers:
+//   E  the token's embedding values of this work group's rows of x
+//   Q  RMSNorm + Q8_K (ties away) of x; the q, k and v rows of kv head
+//      h = b % 8 (so head h's rows are computed on XCD h); RoPE; K and V
+//      rows at pos into the cache
+//   A  attention of kv head h: chunk c of 64 positions on work group
+//      (h, c mod W); work group (h, 0) combines the chunks' partials in chunk
+//      order and quantizes the head group's output ties-even (Q8_K blocks)
+//   O  O projection of this work group's rows of x, residual add
+//   G  RMSNorm + Q8_K (ties away); gate and up rows of its FFN pairs; SwiGLU
+//   D  Q8_K (ties away) of h; down projection of its rows of x; residual add
+// The arithmetic of every phase is that of the per-token kernels (lane sums
+// of src/ops/ops_avx2.cpp:153-276, the float chain over blocks, the chunked
+// softmax), so results are bit-identical to them.
+//
+// Hand-offs.  A phase's outputs go to the next phase's work groups as
+// records of (value bits, tag), stored and loaded as 64-bit atomics at agent
+// scope: a consumer spins until every record it needs carries the tag of the
+// current (launch, layer); no barrier counter and no fence.  Records are
+// reused by every layer and launch; the tag tells them apart, and no work
+// group can be more than one phase ahead of another (each phase needs every
+// work group's output of the one before), so a record is never rewritten
+// while a reader still waits for its previous value.
+//
+// Weights.  Each work group's share of a layer is a contiguous slab (built
+// once from the weight planes), in four regions: QKV, O, gate/up, down.  A
+// region is copied into LDS (direct-to-LDS loads, 1 KiB per wave
+// instruction) after its previous use, during the hand-off wait of a phase
+// before the one that reads it: O at Q, the next layer's QKV at O, gate/up
+// at O (a layer ahead, at D, on the work groups that combine attention
+// chunks), down at G.  The wait ends with every copy landed.
+//
+// Every wait is bounded: past spin_limit, or once another work group has
+// given up, the work group sets the error word and returns.
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+
+#include "mcpm_attn.h"
+#include "mcpm_device.h"
+#include "mcpm_persist.h"
+
+namespace mcpm {
+
+static_assert(PD_ATTN_LDS == static_cast<int>(AttnLds<64>::bytes), "attention staging size");
+
+namespace {
+
+typedef short pd_i16x2 __attribute__((ext_vector_type(2)));
+constexpr int CHAIN_BATCH_PD = 12;  // chain entries read per LDS round trip
+
+__device__ __forceinline__ uint64_t rec_ld(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void rec_st(uint64_t* p, uint32_t v, uint32_t tag) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void rec_stf(uint64_t* p, float v, uint32_t tag) { rec_st(p, __float_as_uint(v), tag); }
+__device__ __forceinline__ unsigned ld_u32c(const unsigned* p) {
+  return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_u32c(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int pd_dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+__device__ __forceinline__ int pd_dot2(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(pd_i16x2, a), __builtin_bit_cast(pd_i16x2, b), c, false);
+}
+__device__ __forceinline__ uint32_t pd_byte_pair(uint32_t w, int k) {
+  return __builtin_amdgcn_perm(0u, w, 0x0c000c00u | (static_cast<uint32_t>(k + 1) << 16) | static_cast<uint32_t>(k));
+}
+__device__ __forceinline__ int pd_mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+__device__ __forceinline__ uint32_t comp(const u32x4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Work-group barrier ordering LDS only: it does not wait for the waves'
+// vector memory operations, so weight copies stay in flight across it.
+__device__ __forceinline__ void pd_bar() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Any thread's v, on every thread, with one barrier: each wave's vote in one
+// of two slot sets (by call parity, it counts the work group's calls), so a
+// set is rewritten only after every thread has read it.
+__device__ __forceinline__ bool pd_any(bool v, uint32_t* slots, uint32_t& it) {
+  const bool w = __any(v);
+  uint32_t* q = slots + 4 * (it & 1u);
+  if ((threadIdx.x & 63) == 0) q[threadIdx.x >> 6] = w ? 1u : 0u;
+  pd_bar();
+  ++it;
+  return (q[0] | q[1] | q[2] | q[3]) != 0u;
+}
+
+// The work group's RMS factor 1/sqrt(sum/dim + eps) from thread t's partial
+// p (t < 256): the 256-slot tree of block_rms_1sync, with an LDS-only
+// barrier.
+__device__ __forceinline__ float pd_rms(float p, int dim, float eps, float* s_red) {
+  const int tid = static_cast<int>(threadIdx.x), lane = tid & 63;
+  s_red[tid] = p;
+  pd_bar();
+  float v = (s_red[lane] + s_red[lane + 128]) + (s_red[lane + 64] + s_red[lane + 192]);
+  v = wave_tree_sum_fast(v);
+  v = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+  return 1.0f / sqrtf(v / static_cast<float>(dim) + eps);
+}
+
+// A region of a (layer, work group) slab into LDS: 1 KiB per wave
+// instruction (global_load_lds_dwordx4: lane i's 16 bytes to M0 + 16i), the
+// 4 waves taking every fourth KiB.  bytes is a multiple of 1 KiB.  Issued as
+// assembly, so the compiler inserts no wait for it (it cannot prove that
+// later LDS accesses miss the region, and would wait for the copy at the
+// next one): the data is there once the issuing waves have waited for their
+// vector memory counter, which the hand-off wait the copy is issued before
+// does before its barrier, and the region is first read after that.
+__device__ __forceinline__ void pd_copy(const uint8_t* src, uint8_t* lds, int bytes) {
+  const int wave = static_cast<int>(threadIdx.x >> 6), lane = static_cast<int>(threadIdx.x & 63);
+  const uint32_t l0 = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(lds)));
+  for (int i = wave; i < (bytes >> 10); i += 4) {
+    const uint8_t* g = src + (static_cast<size_t>(i) << 10) + lane * 16;
+    const uint32_t m = __builtin_amdgcn_readfirstlane(l0 + (static_cast<uint32_t>(i) << 10));
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m), "v"(g) : "m0", "memory");
+  }
+}
+
+// ------------------------------------------------------------ hand-offs ---
+// Waits (the whole work group) until record idx(k) of buf carries `tag` for
+// every k < K of every thread (idx < 0: no record, value 0); values to v.
+// Ends with the thread's vector memory operations complete and a barrier.
+// false: a wait passed the spin limit or another work group gave up (the
+// error word is set).
+template <int K, class F>
+__device__ __forceinline__ bool pd_poll(const PdArgs& a, const uint64_t* buf, uint32_t tag, F idx, uint32_t (&v)[K],
+                                        uint32_t* misc, uint32_t& vit) {
+  uint64_t r[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = idx(k);
+    r[k] = i >= 0 ? rec_ld(buf + i) : (static_cast<uint64_t>(tag) << 32);
+  }
+  uint32_t spins = 0;
+  for (;;) {
+    uint32_t pend = 0;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (static_cast<uint32_t>(r[k] >> 32) != tag) pend |= 1u << k;
+    if (threadIdx.x == 0 && (++spins & 63) == 0 && (spins > a.spin_limit || ld_u32c(a.err))) {
+      misc[0] = 1;
+      st_u32c(a.err, 1u);
+    }
+    // vmcnt(0), expcnt and lgkmcnt left free: every load and copy this wave
+    // issued is complete (the builtin, so the compiler knows it)
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    const bool any = pd_any(pend != 0, misc + 4, vit);
+    if (misc[0]) return false;
+    if (!any) break;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (pend & (1u << k)) r[k] = rec_ld(buf + idx(k));
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = static_cast<uint32_t>(r[k]);
+  return true;
+}
+
+// One thread's wait for the records p[i] whose bit i is set in mask (the
+// others are not read and give 0); values to v.  false past the spin limit.
+template <int N>
+__device__ __forceinline__ bool pd_wait_m(const uint64_t* const (&p)[N], uint32_t mask, uint32_t tag, uint32_t limit,
+                                          uint32_t (&v)[N]) {
+  uint64_t r[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) r[i] = (mask >> i) & 1u ? rec_ld(p[i]) : (static_cast<uint64_t>(tag) << 32);
+  for (uint32_t s = 0;; ++s) {
+    bool done = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (static_cast<uint32_t>(r[i] >> 32) != tag) {
+        done = false;
+        r[i] = rec_ld(p[i]);
+      }
+    }
+    if (done) break;
+    if (s > limit) return false;
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = static_cast<uint32_t>(r[i]);
+  return true;
+}
+
+// ------------------------------------------------------ Q8_K activations ---
+// Block b of the scratch's Q8_K activations from a row of 16 lanes (lane j
+// holding values 16j..16j+15): codes, d, bsums and the bsum pair sums (the
+// layout the lane sums read).  Every lane of the row takes part (lane moves).
+__device__ __forceinline__ void pd_store_xblock(uint32_t* S, const PdShape& s, int b, int j, u32x4 q, float d,
+                                                int bs) {
+  const int v = bs + dpp_i<DPP_XOR1>(bs);
+  const uint32_t w = (static_cast<uint32_t>(v) & 0xffffu) | (static_cast<uint32_t>(dpp_i<DPP_XOR2>(v)) << 16);
+  *reinterpret_cast<u32x4*>(S + s.s_xs + b * 68 + 4 * j) = q;
+  S[s.s_xbs + b * 16 + j] = static_cast<uint32_t>(bs);
+  if (j == 0) S[s.s_xd + b] = __float_as_uint(d);
+  if ((j & 3) == 0) S[s.s_xbp + b * 4 + (j >> 2)] = w;
+}
+
+// -------------------------------------------------------- lane sums -------
+// Half h = p of a Q4_K (row, block): the lane sums isum[m] for m = 4p..4p+3
+// (lane m owns bytes 4m..4m+3 of every 32-byte chunk; quant dword 8j+m is
+// in chunk 2j+p), by summation by parts over the running dots as in the
+// per-token GEMV; p = 0 also forms the min sum.  Entry e: words 4p..4p+3 the
+// sums, p = 0: words 8..10 d_x*d, d_x*dmin, minsum.
+__device__ __forceinline__ void q4k_half(const uint8_t* w, int R, int blk, int row, int p, const uint32_t* xs,
+                                         const uint32_t* xbp, float xd, uint32_t* e) {
+  const u32x4* base = reinterpret_cast<const u32x4*>(w) + static_cast<size_t>(blk) * 9 * R + row;
+  const u32x4 hdr = base[8 * R];
+  u32x4 qv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) qv[j] = base[(2 * j + p) * R];
+  const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+  const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+  const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+  int sc[8], cf[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    sc[k] = static_cast<int>(__builtin_amdgcn_ubfe(sc_lo, 8 * k, 8));
+    sc[4 + k] = static_cast<int>(__builtin_amdgcn_ubfe(sc_hi, 8 * k, 8));
+  }
+#pragma unroll
+  for (int k = 0; k < 7; ++k) cf[k] = sc[k] - sc[k + 1];
+  cf[7] = sc[7];
+  int P[4], is[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const u32x4 xe = *reinterpret_cast<const u32x4*>(xs + 16 * j + 4 * p);
+    const u32x4 xo = *reinterpret_cast<const u32x4*>(xs + 16 * j + 8 + 4 * p);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t q = comp(qv[j], m);
+      P[m] = pd_dot4(q & 0x0f0f0f0fu, comp(xe, m), j == 0 ? 0 : P[m]);
+      is[m] = j == 0 ? __mul24(cf[0], P[m]) : pd_mad24(cf[2 * j], P[m], is[m]);
+      P[m] = pd_dot4((q >> 4) & 0x0f0f0f0fu, comp(xo, m), P[m]);
+      is[m] = pd_mad24(cf[2 * j + 1], P[m], is[m]);
+    }
+  }
+  *reinterpret_cast<u32x4*>(e + 4 * p) = u32x4{static_cast<uint32_t>(is[0]), static_cast<uint32_t>(is[1]),
+                                               static_cast<uint32_t>(is[2]), static_cast<uint32_t>(is[3])};
+  if (p == 0) {
+    const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+    const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+    const u32x4 bp = *reinterpret_cast<const u32x4*>(xbp);
+    int v = pd_dot2(pd_byte_pair(mn_lo, 0), bp.x, 0);
+    v = pd_dot2(pd_byte_pair(mn_lo, 2), bp.y, v);
+    v = pd_dot2(pd_byte_pair(mn_hi, 0), bp.z, v);
+    const int ms = pd_dot2(pd_byte_pair(mn_hi, 2), bp.w, v);
+    const float ds = xd * fp16_to_fp32(static_cast<uint16_t>(hdr.x & 0xffffu));
+    const float dm = xd * fp16_to_fp32(static_cast<uint16_t>(hdr.x >> 16));
+    e[8] = __float_as_uint(ds);
+    e[9] = __float_as_uint(dm);
+    e[10] = static_cast<uint32_t>(ms);
+  }
+}
+
+// Half p of a Q6_K (row, block): lane sums m = 4p..4p+3 (codes in [0, 63],
+// the -32 applied through the bsums), as the per-token GEMV: for half h of
+// the block, ql dwords 16h+m and 16h+8+m (chunks 4h+p and 4h+2+p), qh dword
+// 8h+m (chunk 8+2h+p), activations 32h+8g+m, scale 8h+2g+p.
+__device__ __forceinline__ void q6k_half(const uint8_t* w, int R, int nb, int blk, int row, int p,
+                                         const uint32_t* xs, const uint32_t* xbs, float xd, uint32_t* e) {
+  const u32x4* base = reinterpret_cast<const u32x4*>(w) + static_cast<size_t>(blk) * 13 * R + row;
+  const u32x4 scv = base[12 * R];
+  const uint32_t dword = reinterpret_cast<const uint32_t*>(w + 208 * R * nb)[blk * R + row];
+  u32x4 a0[2], a1[2], hb[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    a0[h] = base[(4 * h + p) * R];
+    a1[h] = base[(4 * h + 2 + p) * R];
+    hb[h] = base[(8 + 2 * h + p) * R];
+  }
+  // term k = 4h+g has scale sc[8h+2g+p]: byte 2(g&1)+p of scale dword
+  // 2h+(g>>1), taken with a bit offset that depends on the half p (no
+  // lookup by a runtime index); by parts as the per-token GEMV
+  int scp[8], cf[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    scp[k] = __builtin_amdgcn_sbfe(static_cast<int>(comp(scv, 2 * (k >> 2) + ((k & 3) >> 1))),
+                                   16 * (k & 1) + 8 * p, 8);
+#pragma unroll
+  for (int k = 0; k < 7; ++k) cf[k] = scp[k] - scp[k + 1];
+  cf[7] = scp[7];
+  int P[4], is[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    u32x4 xv[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) xv[g] = *reinterpret_cast<const u32x4*>(xs + 32 * h + 8 * g + 4 * p);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t av = comp(a0[h], m), bv = comp(a1[h], m), hv = comp(hb[h], m);
+      const uint32_t q0 = (av & 0x0f0f0f0fu) | ((hv << 4) & 0x30303030u);
+      const uint32_t q1 = (bv & 0x0f0f0f0fu) | ((hv << 2) & 0x30303030u);
+      const uint32_t q2 = ((av >> 4) & 0x0f0f0f0fu) | (hv & 0x30303030u);
+      const uint32_t q3 = ((bv >> 4) & 0x0f0f0f0fu) | ((hv >> 2) & 0x30303030u);
+      P[m] = pd_dot4(q0, comp(xv[0], m), h == 0 ? 0 : P[m]);
+      int v = h == 0 ? __mul24(cf[0], P[m]) : pd_mad24(cf[4], P[m], is[m]);
+      P[m] = pd_dot4(q1, comp(xv[1], m), P[m]);
+      v = pd_mad24(cf[4 * h + 1], P[m], v);
+      P[m] = pd_dot4(q2, comp(xv[2], m), P[m]);
+      v = pd_mad24(cf[4 * h + 2], P[m], v);
+      P[m] = pd_dot4(q3, comp(xv[3], m), P[m]);
+      is[m] = pd_mad24(cf[4 * h + 3], P[m], v);
+    }
+  }
+  const u32x4 b0 = *reinterpret_cast<const u32x4*>(xbs + 8 * p);
+  const u32x4 b1 = *reinterpret_cast<const u32x4*>(xbs + 8 * p + 4);
+  const int bsv[8] = {static_cast<int>(b0.x), static_cast<int>(b0.y), static_cast<int>(b0.z), static_cast<int>(b0.w),
+                      static_cast<int>(b1.x), static_cast<int>(b1.y), static_cast<int>(b1.z), static_cast<int>(b1.w)};
+  // lane m = 4p+m' takes sc[2m] and sc[2m+1]: bytes 2(m'&1) and 2(m'&1)+1 of
+  // scale dword 2p+(m'>>1)
+  const uint32_t slo = p ? scv.z : scv.x, shi = p ? scv.w : scv.y;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int w = static_cast<int>(m < 2 ? slo : shi);
+    const int sa = __builtin_amdgcn_sbfe(w, 16 * (m & 1), 8), sb = __builtin_amdgcn_sbfe(w, 16 * (m & 1) + 8, 8);
+    is[m] -= 32 * pd_mad24(bsv[2 * m], sa, __mul24(bsv[2 * m + 1], sb));
+  }
+  *reinterpret_cast<u32x4*>(e + 4 * p) = u32x4{static_cast<uint32_t>(is[0]), static_cast<uint32_t>(is[1]),
+                                               static_cast<uint32_t>(is[2]), static_cast<uint32_t>(is[3])};
+  if (p == 0) {
+    e[8] = __float_as_uint(xd * fp16_to_fp32(static_cast<uint16_t>(dword & 0xffffu)));
+    e[9] = 0u;
+    e[10] = 0u;
+  }
+}
+
+// ------------------------------------------------------------ GEMV phase ---
+// A phase's rows: up to three sub-regions of its LDS region, each with the
+// work group's valid rows, in the order of the phase's row index (chain
+// entries and row values).
+struct PdPhase {
+  const uint8_t* w;        // the region in LDS
+  int off0, off1, off2;    // sub-region offsets in the region
+  int R0, R1, R2;          // rows allocated (the LDS layout's row stride)
+  int ty0, ty1, ty2;       // weight types
+  int v0, v1, v2;          // valid rows of each sub-region
+  int nsub, nb, rtot;
+};
+
+__device__ __forceinline__ PdPhase pd_phase(const uint8_t* w, const PdSub& a, const PdSub& b, const PdSub& c, int v0,
+                                            int v1, int v2, int nsub, int nb, int rtot) {
+  return PdPhase{w, a.off, b.off, c.off, a.R, b.R, c.R, a.type, b.type, c.type, v0, v1, v2, nsub, nb, rtot};
+}
+
+// Integer work of a phase: tasks (sub-region, row, block, half), rows
+// fastest so that consecutive lanes read consecutive 16-byte chunks; each
+// task's lane sums into its chain entry, (block b, row r) at (b*rtot + r)*12.
+// The sub-regions' parameters come from a table in LDS (tab[4i..4i+3]:
+// offset, rows allocated, type, valid rows), indexed per task.
+__device__ __forceinline__ void pd_tasks(const PdShape& s, const PdPhase& ph, const uint32_t* S, const int* tab,
+                                         uint32_t* chain) {
+  const int t = static_cast<int>(threadIdx.x);
+  // halves of a row-block as tasks of their own when they fit one pass of
+  // the work group, else both halves in one task (half the per-task work of
+  // finding the row, block and sub-region)
+  const int H = (ph.v0 + ph.v1 + ph.v2) * ph.nb * 2 <= 256 ? 2 : 1;
+  const int n0 = ph.v0 * ph.nb * H, n1 = ph.nsub > 1 ? ph.v1 * ph.nb * H : 0, n2 = ph.nsub > 2 ? ph.v2 * ph.nb * H : 0;
+  // a sub-region of another weight type than the one before starts on a
+  // wave boundary, so that no wave runs both types' code
+  const int b1 = ph.ty1 != ph.ty0 ? (n0 + 63) & ~63 : n0;
+  const int b2 = ph.ty2 != ph.ty1 ? (b1 + n1 + 63) & ~63 : b1 + n1;
+  const int nt = b2 + n2;
+#pragma unroll 1
+  for (int q = t; q < nt; q += 256) {
+    const int i = q < b1 ? 0 : q < b2 ? 1 : 2;
+    const int qq = q - (i == 0 ? 0 : i == 1 ? b1 : b2);
+    if (qq >= (i == 0 ? n0 : i == 1 ? n1 : n2)) continue;  // padding to the wave boundary
+    const int off = tab[4 * i], RA = tab[4 * i + 1], ty = tab[4 * i + 2], R = tab[4 * i + 3];
+    const int rbase = i == 0 ? 0 : i == 1 ? ph.v0 : ph.v0 + ph.v1;
+    const int row = qq % R, bp = qq / R, blk = H == 2 ? bp >> 1 : bp;
+    uint32_t* e = chain + (blk * ph.rtot + rbase + row) * 12;
+    const float xd = __uint_as_float(S[s.s_xd + blk]);
+#pragma unroll 1
+    for (int p = H == 2 ? (bp & 1) : 0; p < (H == 2 ? (bp & 1) + 1 : 2); ++p) {
+      if (ty == MCPM_TYPE_Q4_K)
+        q4k_half(ph.w + off, RA, blk, row, p, S + s.s_xs + blk * 68, S + s.s_xbp + blk * 4, xd, e);
+      else
+        q6k_half(ph.w + off, RA, ph.nb, blk, row, p, S + s.s_xs + blk * 68, S + s.s_xbs + blk * 16, xd, e);
+    }
+  }
+}
+
+// The float chain over the blocks, in order (the per-token GEMV's TILE
+// chain): 4 lanes per row, lane c the accumulators of lane sums c and c+4,
+// then ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) by DPP row shifts, plus the
+// Q4_K min chain.  Row values to vrow.
+__device__ __forceinline__ void pd_chain(const PdPhase& ph, const int* tab, const uint32_t* chain, float* vrow) {
+  const int t = static_cast<int>(threadIdx.x), row = t >> 2, c = t & 3;
+  if (row >= ph.rtot) return;  // whole groups of 4 lanes
+  const int i = row < ph.v0 ? 0 : row < ph.v0 + ph.v1 ? 1 : 2;
+  const bool q4 = tab[4 * i + 2] == MCPM_TYPE_Q4_K;
+  float a0 = 0.0f, a1 = 0.0f, am = 0.0f;
+  const int nb = ph.nb;
+#pragma unroll 1
+  for (int bq = 0; bq < nb; bq += CHAIN_BATCH_PD) {
+    int i0[CHAIN_BATCH_PD], i1[CHAIN_BATCH_PD];
+    f32x4 dv[CHAIN_BATCH_PD];
+#pragma unroll
+    for (int k = 0; k < CHAIN_BATCH_PD; ++k) {
+      const uint32_t* e = chain + (min(bq + k, nb - 1) * ph.rtot + row) * 12;
+      i0[k] = static_cast<int>(e[c]);
+      i1[k] = static_cast<int>(e[c + 4]);
+      dv[k] = *reinterpret_cast<const f32x4*>(e + 8);
+    }
+#pragma unroll
+    for (int k = 0; k < CHAIN_BATCH_PD; ++k) {
+      if (bq + k < nb) {
+        a0 = __builtin_fmaf(dv[k].x, static_cast<float>(i0[k]), a0);
+        a1 = __builtin_fmaf(dv[k].x, static_cast<float>(i1[k]), a1);
+        am = __builtin_fmaf(-dv[k].y, static_cast<float>(__float_as_int(dv[k].z)), am);
+      }
+    }
+  }
+  float v = a0 + a1;
+  v = v + dpp_f<0x102>(v);  // row_shl:2
+  v = v + dpp_f<0x101>(v);  // row_shl:1
+  if (q4) v = v + am;
+  if (c == 0) vrow[row] = v;
+}
+
+// A Q8_K prologue from fp32 values x[t + 256k] (k < nbx) of every thread:
+// RMSNorm with gamma (the 256-slot tree over x[t], x[t+256], ...), then the
+// ties-away quantization of each block by a row of 16 lanes (block r16, lane
+// j values 16j..16j+15).
+__device__ __forceinline__ void pd_norm_quant(const PdShape& s, uint32_t* S, const uint32_t (&xv)[PD_NBX],
+                                              const f32x4 (&gam)[4]) {
+  const int t = static_cast<int>(threadIdx.x), r16 = t >> 4, j = t & 15;
+  float* U = reinterpret_cast<float*>(S + s.s_u);
+  float p = 0.0f;
+#pragma unroll
+  for (int k = 0; k < PD_NBX; ++k) {
+    if (k < s.nbx) {
+      const float x = __uint_as_float(xv[k]);
+      p = p + x * x;
+      U[t + 256 * k] = x;
+    }
+  }
+  const float rms = pd_rms(p, s.dim, s.eps, reinterpret_cast<float*>(S + s.s_red));
+  if (r16 < s.nbx) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 x4 = *reinterpret_cast<const f32x4*>(U + r16 * 256 + 16 * j + 4 * i);
+      v[4 * i] = (x4.x * rms) * gam[i].x;
+      v[4 * i + 1] = (x4.y * rms) * gam[i].y;
+      v[4 * i + 2] = (x4.z * rms) * gam[i].z;
+      v[4 * i + 3] = (x4.w * rms) * gam[i].w;
+    }
+    u32x4 packed;
+    float d;
+    int gsum;
+    quant_block_row16(v, true, packed, d, gsum);
+    pd_store_xblock(S, s, r16, j, packed, d, gsum);
+  }
+  pd_bar();
+}
+
+__device__ __forceinline__ const uint8_t* pd_slab(const PdArgs& a, int l, int r) {
+  return a.slab + (static_cast<size_t>(l) * a.s.G + blockIdx.x) * a.s.slab_stride + a.s.reg_off[r];
+}
+__device__ __forceinline__ void pd_copy_region(const PdArgs& a, uint8_t* LDS, int l, int r) {
+  pd_copy(pd_slab(a, l, r), LDS + a.s.reg_off[r], a.s.reg_sz[r]);
+}
+
+// Q (kind 0), O (2), G (3) or D (4) of layer l.
+__device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_t* LDS, uint32_t* S, uint32_t tag,
+                                        int pos, uint32_t& vit) {
+  const PdShape& s = a.s;
+  const PdRows me = pd_rows(s, static_cast<int>(blockIdx.x));
+  const int t = static_cast<int>(threadIdx.x), r16 = t >> 4, j = t & 15;
+  uint32_t* misc = S + s.s_misc;
+  float* vrow = reinterpret_cast<float*>(S + s.s_vrow);
+  float* ownx = reinterpret_cast<float*>(S + s.s_ownx);
+  float* ownx2 = reinterpret_cast<float*>(S + s.s_ownx2);
+
+  PdPhase ph;
+  if (kind == 0) {
+    ph = pd_phase(LDS + s.reg_off[0], s.sq, s.sk, s.sv, s.nq, s.nk, s.nk, 3, s.nbx, s.nq + 2 * s.nk);
+  } else if (kind == 2) {
+    ph = pd_phase(LDS + s.reg_off[1], s.so, s.so, s.so, me.nh, 0, 0, 1, s.nbq, me.nh);
+  } else if (kind == 3) {
+    ph = pd_phase(LDS + s.reg_off[2], s.sg, s.su, s.su, me.np, me.np, 0, 2, s.nbx, 2 * me.np);
+  } else {
+    ph = pd_phase(LDS + s.reg_off[3], s.sd, s.sd, s.sd, me.nh, 0, 0, 1, s.nbh, me.nh);
+  }
+
+  // the sub-regions' table for the task loop (read after the prologue's
+  // barrier)
+  int* tab = reinterpret_cast<int*>(misc + 12);
+  if (t == 0) {
+    tab[0] = ph.off0;
+    tab[1] = ph.R0;
+    tab[2] = ph.ty0;
+    tab[3] = ph.v0;
+    tab[4] = ph.off1;
+    tab[5] = ph.R1;
+    tab[6] = ph.ty1;
+    tab[7] = ph.v1;
+    tab[8] = ph.off2;
+    tab[9] = ph.R2;
+    tab[10] = ph.ty2;
+    tab[11] = ph.v2;
+  }
+
+  // loads that do not depend on the hand-off go first: the RMSNorm gains in
+  // the quantization layout, and the RoPE (cos, sin) of the thread's
+  // epilogue row
+  f32x4 gam[4];
+  if (kind == 0 || kind == 3) {
+    const float* g = a.norms + (static_cast<size_t>(2 * l) + (kind == 0 ? 0 : 1)) * s.dim;
+    if (r16 < s.nbx) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gam[i] = reinterpret_cast<const f32x4*>(g + r16 * 256 + 16 * j)[i];
+    }
+  }
+  float2 cs = make_float2(0.0f, 0.0f);
+  if (kind == 0 && t < s.nq + s.nk) {
+    const int r = t < s.nq ? me.qr0 + t : me.kr0 + (t - s.nq);
+    cs = a.rope[static_cast<size_t>(pos) * (s.hd / 2) + ((r % s.hd) >> 1)];
+  }
+
+  // weight copies for later phases, issued while this phase waits for its
+  // hand-off (the waves are idle then, and a copy stalls the wave issuing it
+  // for most of its transfer): each region after its last use, before the
+  // wait of a phase ahead of its next.  Q: this layer's O; O: the next
+  // layer's QKV, and this layer's gate/up except on the kv heads' combining
+  // work groups (the O wait is long elsewhere: it waits for those); G: this
+  // layer's down (the attention's staging is done); D: on the combining work
+  // groups, the next layer's gate/up.
+  if (kind == 0) pd_copy_region(a, LDS, l, 1);
+  if (kind == 2) {
+    if (l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 0);
+    if (me.k != 0) pd_copy_region(a, LDS, l, 2);
+  }
+  if (kind == 3) pd_copy_region(a, LDS, l, 3);
+  if (kind == 4 && me.k == 0 && l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 2);
+
+  // hand-off and prologue: the Q8_K activations into the scratch
+  if (kind == 0 || kind == 3) {
+    uint32_t xv[PD_NBX];
+    const int nbx = s.nbx;
+    if (!pd_poll<PD_NBX>(a, kind == 0 ? a.rx : a.rx2, tag, [&](int k) { return k < nbx ? t + 256 * k : -1; }, xv,
+                         misc, vit))
+      return false;
+    pd_norm_quant(s, S, xv, gam);
+  } else if (kind == 2) {
+    uint32_t v[3];
+    const int n = s.nbq * PD_REC_BLK;
+    if (!pd_poll<3>(a, a.ratt, tag, [&](int k) { return t + 256 * k < n ? t + 256 * k : -1; }, v, misc, vit))
+      return false;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int i = t + 256 * k;
+      if (i < n) {
+        const int blk = i / PD_REC_BLK, w = i - blk * PD_REC_BLK;
+        if (w == 0) S[s.s_xd + blk] = v[k];
+        else if (w <= 64) S[s.s_xs + blk * 68 + w - 1] = v[k];
+        else if (w <= 80) S[s.s_xbs + blk * 16 + w - 65] = v[k];
+        else S[s.s_xbp + blk * 4 + w - 81] = v[k];
+      }
+    }
+    pd_bar();
+  } else {
+    // h in rounds of up to 16 blocks: records t + 256k of the round (lanes
+    // on consecutive records) into the staging area, then block r16 of the
+    // round quantized by its row of 16 lanes (zero past ffn)
+    const int nbh = s.nbh, ffn = s.ffn;
+    float* U = reinterpret_cast<float*>(S + s.s_u);
+#pragma unroll 1
+    for (int b0 = 0; b0 < nbh; b0 += 16) {
+      const int nbr = min(16, nbh - b0), e0 = b0 * 256;
+      uint32_t hv[16];
+      if (!pd_poll<16>(a, a.rh, tag,
+                       [&](int k) {
+                         const int e = e0 + t + 256 * k;
+                         return k < nbr && e < ffn ? e : -1;
+                       },
+                       hv, misc, vit))
+        return false;
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (k < nbr) U[t + 256 * k] = __uint_as_float(hv[k]);
+      pd_bar();
+      if (r16 < nbr) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 x4 = *reinterpret_cast<const f32x4*>(U + r16 * 256 + 16 * j + 4 * i);
+          v[4 * i] = x4.x;
+          v[4 * i + 1] = x4.y;
+          v[4 * i + 2] = x4.z;
+          v[4 * i + 3] = x4.w;
+        }
+        u32x4 packed;
+        float d;
+        int gsum;
+        quant_block_row16(v, true, packed, d, gsum);
+        pd_store_xblock(S, s, b0 + r16, j, packed, d, gsum);
+      }
+      pd_bar();  // the staging area's readers are done before the next round
+    }
+  }
+
+  uint32_t* chain = S + s.s_u;  // the prologue's x staging is no longer read
+  pd_tasks(s, ph, S, tab, chain);
+  pd_bar();
+  pd_chain(ph, tab, chain, vrow);
+  pd_bar();
+
+  // epilogues
+  if (kind == 0) {
+    if (t < ph.rtot) {
+      const float v = vrow[t];
+      const int kvd = s.kvd;
+      const size_t row_off = static_cast<size_t>(l) * a.max_seq * kvd + static_cast<size_t>(pos) * kvd;
+      uint64_t* qrec = a.rqkv + static_cast<size_t>(me.kvh) * (s.gh + 2 * s.hd);
+      if (t < s.nq + s.nk) {
+        // adjacent-pair RoPE (src/ops/ops.cpp:502-516) on q and k rows
+        const float partner = vrow[t ^ 1];
+        const int r = t < s.nq ? me.qr0 + t : me.kr0 + (t - s.nq);
+        const int i = r % s.hd;
+        float o;
+        if ((i & 1) == 0) o = v * cs.x - partner * cs.y;
+        else o = partner * cs.y + v * cs.x;
+        if (t < s.nq) {
+          rec_stf(qrec + (r - me.kvh * s.gh), o, tag);
+        } else {
+          a.kc[row_off + r] = o;
+          rec_stf(qrec + s.gh + (r - me.kvh * s.hd), o, tag);
+        }
+      } else {
+        const int r = me.kr0 + (t - s.nq - s.nk);
+        a.vc[row_off + r] = v;
+        rec_stf(qrec + s.gh + s.hd + (r - me.kvh * s.hd), v, tag);
+      }
+    }
+  } else if (kind == 2) {
+    if (t < me.nh) {
+      const float x2 = ownx[t] + vrow[t];
+      ownx2[t] = x2;
+      rec_stf(a.rx2 + me.hr0 + t, x2, tag);
+    }
+  } else if (kind == 3) {
+    if (t < me.np) {
+      const float g = vrow[t], u = vrow[me.np + t];
+      const float silu = g / (1.0f + exp_f32(-g));
+      rec_stf(a.rh + me.fp0 + t, silu * u, tag);
+    }
+  } else {
+    if (t < me.nh) {
+      const float x = ownx2[t] + vrow[t];
+      ownx[t] = x;
+      if (l + 1 < s.L) rec_stf(a.rx + me.hr0 + t, x, tag + 1);
+      else a.x_out[me.hr0 + t] = x;
+    }
+  }
+  return true;
+}
+
+// Register slots of K and V rows at position T-1 (and the clamped slots past
+// it) from the rows handed over by the QKV phase (LDS kr, vr).
+__device__ __forceinline__ void pd_fill_last(AttnRegs<4>& R, const float* kr, const float* vr, int c, int T) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int f = static_cast<int>(threadIdx.x) + 256 * u;
+    const int jr = f >> 4, c4 = f & 15;
+    if (min(c * ATTN_CHUNK + jr, T - 1) == T - 1) {
+      R.k[u] = *reinterpret_cast<const f32x4*>(kr + 4 * c4);
+      R.v[u] = *reinterpret_cast<const f32x4*>(vr + 4 * c4);
+    }
+  }
+}
+
+// The attention of layer l (src/ops/ops.cpp:537-628) for kv head h = b % 8,
+// head_dim 64, a head group of 256 outputs (gh).
+__device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LDS, uint32_t* S, uint32_t tag, int T,
+                                             uint32_t& vit) {
+  const PdShape& s = a.s;
+  const int t = static_cast<int>(threadIdx.x), h = static_cast<int>(blockIdx.x) % PD_XCDS,
+            k = static_cast<int>(blockIdx.x) / PD_XCDS, W = s.W;
+  uint32_t* misc = S + s.s_misc;
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  if (k >= nch) return true;  // no chunk of this context
+  constexpr int HD = 64, GH = 256, OPT = ATTN_MAX_GROUP * HD / 256;
+  const int group = s.group, kvd = s.kvd;
+  const size_t lay = static_cast<size_t>(l) * a.max_seq * kvd;
+  const float* kc = a.kc + lay;
+  const float* vc = a.vc + lay;
+  const AttnLds<HD> A(reinterpret_cast<float*>(LDS + s.reg_off[3]));
+  AttnRegs<4> R;
+  const size_t head_off = static_cast<size_t>(h) * HD;
+  // chunk k's rows before pos are in the cache since earlier launches
+  attn_load_chunk<4, true>(R, kc, vc, k, T, kvd, head_off, HD / 4, ATTN_CHUNK * HD / 4);
+  // q of the head group and the K and V rows at pos, from the QKV phase
+  constexpr int NREC = GH + 2 * HD;
+  uint32_t qv[2];
+  if (!pd_poll<2>(a, a.rqkv + static_cast<size_t>(h) * NREC, tag,
+                  [&](int kk) { return t + 256 * kk < NREC ? t + 256 * kk : -1; }, qv, misc, vit))
+    return false;
+  float* kr = reinterpret_cast<float*>(S + s.s_u);
+  float* vr = kr + HD;
+  float* sX = vr + HD;       // [GH] the combined output
+  float* sO = sX + GH;       // [2][GH] this work group's chunks' o_c
+  float* sM = sO + 2 * GH;   // [max_chunks][group] m_c (combining work group)
+  float* sZ = sM + 64 * ATTN_MAX_GROUP;
+  A.sQ[(t / HD) * HD + t % HD] = __uint_as_float(qv[0]);
+  if (t < 2 * HD) kr[t] = __uint_as_float(qv[1]);  // kr, vr contiguous
+  pd_bar();
+  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+#pragma unroll 1
+  for (int cc = 0; cc < 2; ++cc) {
+    const int c = k + W * cc;
+    if (c >= nch) break;  // uniform
+    if (c == nch - 1) pd_fill_last(R, kr, vr, c, T);
+    pd_bar();  // readers of the previous chunk are done
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int f = t + 256 * u, jr = f >> 4, c4 = f & 15;
+      *reinterpret_cast<f32x4*>(&A.sK[jr * (HD + 4) + c4 * 4]) = R.k[u];
+      *reinterpret_cast<f32x4*>(&A.sV[jr * HD + c4 * 4]) = R.v[u];
+    }
+    if (c + W < nch) attn_load_chunk<4, true>(R, kc, vc, c + W, T, kvd, head_off, HD / 4, ATTN_CHUNK * HD / 4);
+    pd_bar();
+    float o[OPT];
+    attn_token_chunk<HD, OPT, true>(A.sK, A.sV, A.sQ, A.sE, A.sMZ + cc * ATTN_MAX_GROUP, c, T, group, HD, GH, scale,
+                                    o, t);
+    sO[cc * GH + t] = o[0];
+  }
+  pd_bar();  // (m_c, z_c) of every head, every chunk's o_c
+  const int ppc = GH + 2 * group;
+  uint64_t* part = a.rpart + static_cast<size_t>(h) * s.max_chunks * ppc;
+  if (k != 0) {
+#pragma unroll 1
+    for (int cc = 0; cc < 2; ++cc) {
+      const int c = k + W * cc;
+      if (c >= nch) break;
+      uint64_t* pr = part + static_cast<size_t>(c) * ppc;
+      rec_stf(pr + t, sO[cc * GH + t], tag);
+      if (t < group) {
+        const float2 mz = A.sMZ[cc * ATTN_MAX_GROUP + t];
+        rec_stf(pr + GH + t, mz.x, tag);
+        rec_stf(pr + GH + group + t, mz.y, tag);
+      }
+    }
+    return true;
+  }
+  // Work group (h, 0) combines the chunks in chunk order with the per-token
+  // path's arithmetic: m = max m_c; f_c = exp(m_c - m); Z = fma(z_c, f_c, Z);
+  // O = fma(o_c, f_c, O); out = O / Z.  Own chunks 0 and W come from LDS,
+  // the others from their records: in one wait, every chunk's (m_c, z_c)
+  // (one (chunk, head) per thread, into LDS) and this thread's o_c of chunks
+  // 1..8; later chunks' o_c in batches of 8 as the chain reaches them.
+  bool ok = true;
+  const int hh = t / HD;
+  uint32_t rv[10];
+  {
+    const int cq = t / group, hq = t - cq * group;
+    const bool mz_rec = t < nch * group && cq != 0 && cq != W;
+    const uint64_t* p[10];
+    p[0] = part + static_cast<size_t>(min(cq, nch - 1)) * ppc + GH + hq;
+    p[1] = p[0] + group;
+    uint32_t mask = mz_rec ? 3u : 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = 1 + i;
+      p[2 + i] = part + static_cast<size_t>(min(c, nch - 1)) * ppc + t;
+      if (c < nch && c != W) mask |= 1u << (2 + i);
+    }
+    ok = pd_wait_m<10>(p, mask, tag, a.spin_limit, rv);
+    if (t < nch * group) {
+      float mc, zc;
+      if (cq == 0 || cq == W) {
+        const float2 mz = A.sMZ[(cq == 0 ? 0 : ATTN_MAX_GROUP) + hq];
+        mc = mz.x;
+        zc = mz.y;
+      } else {
+        mc = __uint_as_float(rv[0]);
+        zc = __uint_as_float(rv[1]);
+      }
+      sM[t] = mc;
+      sZ[t] = zc;
+    }
+  }
+  if (pd_any(!ok, misc + 4, vit)) {
+    if (t == 0) st_u32c(a.err, 1u);
+    return false;
+  }
+  float m = sM[hh];
+  for (int c = 1; c < nch; ++c) m = fmaxf(m, sM[c * group + hh]);
+  float Z = 0.0f, O = 0.0f;
+  auto step = [&](int c, float o) {
+    const float f = exp_f32(sM[c * group + hh] - m);
+    Z = __builtin_fmaf(sZ[c * group + hh], f, Z);
+    O = __builtin_fmaf(o, f, O);
+  };
+  step(0, sO[t]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = 1 + i;
+    if (c < nch) step(c, c == W ? sO[GH + t] : __uint_as_float(rv[2 + i]));
+  }
+#pragma unroll 1
+  for (int c0 = 9; c0 < nch && ok; c0 += 8) {
+    const uint64_t* pb[8];
+    uint32_t mask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = c0 + i;
+      pb[i] = part + static_cast<size_t>(min(c, nch - 1)) * ppc + t;
+      if (c < nch && c != W) mask |= 1u << i;
+    }
+    uint32_t ov[8];
+    ok = pd_wait_m<8>(pb, mask, tag, a.spin_limit, ov);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = c0 + i;
+      if (ok && c < nch) step(c, c == W ? sO[GH + t] : __uint_as_float(ov[i]));
+    }
+  }
+  sX[t] = O / Z;
+  if (pd_any(!ok, misc + 4, vit)) {
+    if (t == 0) st_u32c(a.err, 1u);
+    return false;
+  }
+  // the head group's Q8_K block (ties even) on lanes 0..15
+  if (t < 16) {
+    const int j = t;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 x4 = *reinterpret_cast<const f32x4*>(sX + 16 * j + 4 * i);
+      v[4 * i] = x4.x;
+      v[4 * i + 1] = x4.y;
+      v[4 * i + 2] = x4.z;
+      v[4 * i + 3] = x4.w;
+    }
+    u32x4 packed;
+    float d;
+    int gsum;
+    quant_block_row16(v, false, packed, d, gsum);
+    const int vs = gsum + dpp_i<DPP_XOR1>(gsum);
+    const uint32_t w = (static_cast<uint32_t>(vs) & 0xffffu) | (static_cast<uint32_t>(dpp_i<DPP_XOR2>(vs)) << 16);
+    uint64_t* rb = a.ratt + static_cast<size_t>(h) * PD_REC_BLK;
+    rec_st(rb + 1 + 4 * j, packed.x, tag);
+    rec_st(rb + 2 + 4 * j, packed.y, tag);
+    rec_st(rb + 3 + 4 * j, packed.z, tag);
+    rec_st(rb + 4 + 4 * j, packed.w, tag);
+    rec_st(rb + 65 + j, static_cast<uint32_t>(gsum), tag);
+    if (j == 0) rec_stf(rb, d, tag);
+    if ((j & 3) == 0) rec_st(rb + 81 + (j >> 2), w, tag);
+  }
+  return true;
+}
+
+// One launch per token: every layer, from the embedding to the last layer's
+// x (x_out).
+__global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t LDS[];
+  uint32_t* S = reinterpret_cast<uint32_t*>(LDS + a.s.scr_off);
+  uint32_t* misc = S + a.s.s_misc;
+  const int t = static_cast<int>(threadIdx.x);
+  if (t == 0) {
+    misc[0] = 0u;
+    misc[1] = ld_u32c(a.epoch);
+  }
+  pd_bar();
+  const uint32_t ep = misc[1];
+  const int pos = a.state[1], T = pos + 1, L = a.s.L;
+  const uint32_t tag0 = ep * static_cast<uint32_t>(L + 1) + 1u;
+  uint32_t vit = 0;
+  // E: this work group's embedding values, then layer 0's QKV and O weights
+  {
+    const PdRows me = pd_rows(a.s, static_cast<int>(blockIdx.x));
+    float* ownx = reinterpret_cast<float*>(S + a.s.s_ownx);
+    if (t < me.nh) {
+      const int r = me.hr0 + t;
+      const float x = dequant_value(a.embd, a.state[0], r / QK_K, r % QK_K);
+      ownx[t] = x;
+      rec_stf(a.rx + r, x, tag0);
+    }
+  }
+  pd_copy_region(a, LDS, 0, 0);
+  if (blockIdx.x < PD_XCDS) pd_copy_region(a, LDS, 0, 2);  // the combining work groups' first gate/up
+  // one loop over the phases, so that each phase's code exists once
+#pragma unroll 1
+  for (int ph = 0; ph < 5 * L; ++ph) {
+    const int l = ph / 5, kind = ph - 5 * l;
+    const uint32_t tag = tag0 + static_cast<uint32_t>(l);
+    const bool ok = kind == 1 ? pd_attention(a, l, LDS, S, tag, T, vit) : pd_gemv(a, l, kind, LDS, S, tag, pos, vit);
+    if (!ok) return;
+  }
+  // every work group read the launch count before its first hand-off, and
+  // this work group's last wait needed every work group's output of the
+  // phase before, so none reads the count any more
+  if (blockIdx.x == 0 && t == 0) st_u32c(a.epoch, ep + 1u);
+}
+
+// Slab chunk i (16 bytes) of work group blockIdx.y in layer blockIdx.z.
+__global__ void k_build_slab(const PdShape s, const PdLayer* __restrict__ layers, uint8_t* __restrict__ slab) {
+  const int b = static_cast<int>(blockIdx.y), l = static_cast<int>(blockIdx.z);
+  const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (i * 16 >= s.slab_stride) return;
+  const PdLayer& Ly = layers[l];
+  const WView* wv[7] = {&Ly.q, &Ly.k, &Ly.v, &Ly.o, &Ly.g, &Ly.u, &Ly.d};
+  const int rows[7] = {Ly.q.rows, Ly.k.rows, Ly.v.rows, Ly.o.rows, Ly.g.rows, Ly.u.rows, Ly.d.rows};
+  const PdSrc src = pd_slab_src(s, b, i * 16, rows);
+  u32x4 out = u32x4{0u, 0u, 0u, 0u};
+  if (src.tensor >= 0) {
+    const WView& w = *wv[src.tensor];
+    const uint8_t* plane = src.plane == 0 ? w.p0 : src.plane == 1 ? w.p1 : src.plane == 2 ? w.p2 : w.p3;
+    if (src.n == 1) {
+      out = *reinterpret_cast<const u32x4*>(plane + src.src[0]);
+    } else {
+      uint32_t dv[4];
+      for (int k = 0; k < 4; ++k)
+        dv[k] = src.src[k] < 0 ? 0u
+                               : static_cast<uint32_t>(plane[src.src[k]]) | (static_cast<uint32_t>(plane[src.src[k] + 1]) << 8);
+      out = u32x4{dv[0], dv[1], dv[2], dv[3]};
+    }
+  }
+  *reinterpret_cast<u32x4*>(slab + (static_cast<size_t>(l) * s.G + b) * s.slab_stride + static_cast<size_t>(i) * 16) = out;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ host ---
+
+bool pd_plan(const mcpm_model_config& c, int n_cu, int max_seq, int tq, int tk, int tv, int to, int td,
+             PdShape& s, const char** why) {
+  auto no = [&](const char* w) {
+    if (why) *why = w;
+    return false;
+  };
+  s = PdShape{};
+  if (n_cu <= 0 || n_cu % PD_XCDS) return no("CU count not a multiple of 8");
+  s.G = n_cu;
+  s.W = n_cu / PD_XCDS;
+  s.L = c.n_layers;
+  s.dim = c.dim;
+  s.nbx = c.dim / QK_K;
+  s.hd = c.head_dim;
+  s.nkv = c.n_kv_heads;
+  s.group = c.n_kv_heads > 0 ? c.n_heads / c.n_kv_heads : 0;
+  s.gh = s.group * s.hd;
+  s.qd = c.n_heads * c.head_dim;
+  s.nbq = s.qd / QK_K;
+  s.kvd = s.nkv * s.hd;
+  s.ffn = c.ffn;
+  s.ffn_pad = c.ffn_pad;
+  s.nbh = c.ffn_pad / QK_K;
+  s.eps = c.eps;
+  if (s.nkv != PD_XCDS || s.hd != 64) return no("needs 8 kv heads of 64");
+  if (s.gh != QK_K) return no("head group not one Q8_K block");
+  if (s.gh % (2 * s.W) || s.hd % (2 * s.W)) return no("head rows do not split into even runs per work group");
+  if (c.dim % QK_K || s.nbx > PD_NBX || s.nbq > PD_NBQ || c.ffn_pad % QK_K || s.nbh > PD_NBH || c.ffn > c.ffn_pad)
+    return no("dimensions outside the kernel's bounds");
+  if (tq != MCPM_TYPE_Q4_K || tk != MCPM_TYPE_Q4_K) return no("q and k must be Q4_K");
+  for (int ty : {tv, to, td})
+    if (ty != MCPM_TYPE_Q4_K && ty != MCPM_TYPE_Q6_K) return no("weight type without a kernel");
+  s.max_chunks = (max_seq + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  if (s.max_chunks > 2 * s.W) return no("context longer than two chunks per work group");
+  s.nq = s.gh / s.W;
+  s.nk = s.hd / s.W;
+  s.nh_max = (c.dim + s.G - 1) / s.G;
+  s.np_max = (c.ffn + s.G - 1) / s.G;
+  if (s.nq + 2 * s.nk > 64 || 2 * s.np_max > 64 || s.nh_max > 64) return no("too many rows per work group");
+  auto sub = [](int off, int R, int type) { return PdSub{off, R, type}; };
+  s.sq = sub(0, s.nq, tq);
+  s.sk = sub(pd_sub_bytes(tq, s.nq, s.nbx), s.nk, tk);
+  s.sv = sub(s.sk.off + pd_sub_bytes(tk, s.nk, s.nbx), s.nk, tv);
+  const int qkv_bytes = s.sv.off + pd_sub_bytes(tv, s.nk, s.nbx);
+  s.so = sub(0, s.nh_max, to);
+  const int o_bytes = pd_sub_bytes(to, s.nh_max, s.nbq);
+  s.sg = sub(0, s.np_max, MCPM_TYPE_Q4_K);
+  s.su = sub(pd_sub_bytes(MCPM_TYPE_Q4_K, s.np_max, s.nbx), s.np_max, MCPM_TYPE_Q4_K);
+  const int gu_bytes = 2 * pd_sub_bytes(MCPM_TYPE_Q4_K, s.np_max, s.nbx);
+  s.sd = sub(0, s.nh_max, td);
+  const int d_bytes = pd_sub_bytes(td, s.nh_max, s.nbh);
+  const int kib = 1024;
+  auto up = [&](int v) { return (v + kib - 1) / kib * kib; };
+  s.reg_sz[0] = up(qkv_bytes);
+  s.reg_sz[1] = up(o_bytes);
+  s.reg_sz[2] = up(gu_bytes);
+  s.reg_sz[3] = up(d_bytes);
+  s.reg_off[0] = 0;
+  for (int r = 1; r < 4; ++r) s.reg_off[r] = s.reg_off[r - 1] + s.reg_sz[r - 1];
+  s.slab_stride = s.reg_off[3] + s.reg_sz[3];
+  s.wd_lds = std::max(s.reg_sz[3], (PD_ATTN_LDS + 15) & ~15);
+  s.scr_off = s.reg_off[3] + s.wd_lds;
+  // scratch (dwords)
+  const int nbm = std::max({s.nbx, s.nbq, s.nbh});
+  auto a4 = [](int v) { return (v + 3) & ~3; };
+  s.s_xs = 0;
+  s.s_xd = nbm * 68;
+  s.s_xbp = s.s_xd + a4(nbm);
+  s.s_xbs = s.s_xbp + nbm * 4;
+  s.s_red = s.s_xbs + nbm * 16;
+  s.s_u = a4(s.s_red + 260);
+  const int rq = s.nq + 2 * s.nk;
+  // the attention's rows at pos, combined output, own o_c, every chunk's
+  // (m_c, z_c)
+  const int attn_words = 2 * s.hd + 3 * s.gh + 2 * 64 * ATTN_MAX_GROUP;
+  // the down phase stages its hand-off in rounds of up to 16 blocks
+  const int u_words = std::max({c.dim, rq * s.nbx * 12, s.nh_max * s.nbq * 12, 2 * s.np_max * s.nbx * 12,
+                                s.nh_max * s.nbh * 12, attn_words, std::min(s.nbh, 16) * QK_K});
+  s.s_vrow = a4(s.s_u + u_words);
+  const int rmax = std::max({rq, s.nh_max, 2 * s.np_max});
+  s.s_ownx = a4(s.s_vrow + rmax);
+  s.s_ownx2 = a4(s.s_ownx + s.nh_max);
+  s.s_misc = a4(s.s_ownx2 + s.nh_max);
+  s.lds_bytes = s.scr_off + (s.s_misc + 24) * 4;  // abort flag, launch count, two vote sets, sub-region table
+  if (s.lds_bytes > 160 * 1024 - 256) return no("LDS plan above 160 KiB");  // room for the runtime's own LDS words
+  return true;
+}
+
+size_t pd_records(const PdShape& s) {
+  return 2 * static_cast<size_t>(s.dim) + s.ffn + static_cast<size_t>(s.nkv) * (s.gh + 2 * s.hd) +
+         static_cast<size_t>(s.nkv) * s.max_chunks * (s.gh + 2 * s.group) + static_cast<size_t>(s.nbq) * PD_REC_BLK;
+}
+
+void pd_bind_records(PdArgs& a, uint64_t* base) {
+  const PdShape& s = a.s;
+  a.rx = base;
+  a.rx2 = a.rx + s.dim;
+  a.rh = a.rx2 + s.dim;
+  a.rqkv = a.rh + s.ffn;
+  a.rpart = a.rqkv + static_cast<size_t>(s.nkv) * (s.gh + 2 * s.hd);
+  a.ratt = a.rpart + static_cast<size_t>(s.nkv) * s.max_chunks * (s.gh + 2 * s.group);
+}
+
+hipError_t launch_build_slab(const PdShape& s, const PdLayer* d_layers, uint8_t* slab, hipStream_t st) {
+  const int chunks = s.slab_stride / 16;
+  hipLaunchKernelGGL(k_build_slab, dim3((chunks + 255) / 256, s.G, s.L), dim3(256), 0, st, s, d_layers, slab);
+  return hipGetLastError();
+}
+
+hipError_t prepare_decode_persist(const PdShape& s) {
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_decode_persist),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, s.lds_bytes);
+  if (e != hipSuccess) return e;
+  // every work group must be resident at once: at least one per CU
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_decode_persist), 256,
+                                                   s.lds_bytes) != hipSuccess ||
+      occ < 1)
+    return hipErrorNotSupported;
+  return hipSuccess;
+}
+
+hipError_t launch_decode_persist(const PdArgs& a, hipStream_t st) {
+  launch_kernel(k_decode_persist, dim3(a.s.G), dim3(256), static_cast<size_t>(a.s.lds_bytes), st, a);
+  return hipGetLastError();
+}
+
+}  // namespace mcpm

@@ -16,8 +16,8 @@ PKG_DIR = os.path.dirname(_HERE)
 LIB_PATH = os.path.join(PKG_DIR, "libmcpm_hip.so")
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
-KC_QKV, KC_ATTN, KC_OPROJ, KC_GATE_UP, KC_DOWN, KC_LM_HEAD = range(6)
-KC_NAMES = ["qkv", "attn", "oproj", "gate_up", "down", "lm_head"]
+KC_QKV, KC_ATTN, KC_OPROJ, KC_GATE_UP, KC_DOWN, KC_LM_HEAD, KC_LAYERS = range(7)
+KC_NAMES = ["qkv", "attn", "oproj", "gate_up", "down", "lm_head", "layers"]
 
 # ggml block layouts (reference include/ops.h:33-65)
 Q8_0 = np.dtype([("d", "<u2"), ("qs", "i1", 32)])
@@ -121,6 +121,8 @@ _SIGS = {
     "mcpm_engine_generate_sampled_at": (_I, [_P, _P, _I, _I, _I, _F, _F, C.c_uint32, _P]),
     "mcpm_sample_logits": (_I, [_P, _I, _F, _F, _F]),
     "mcpm_engine_set_graph": (_I, [_P, _I]),
+    "mcpm_engine_set_persistent": (_I, [_P, _I]),
+    "mcpm_engine_uses_persistent": (_I, [_P]),
     "mcpm_set_op_timing": (_I, [_P, _I]),
     "mcpm_op_time": (_I, [_P, C.POINTER(C.c_double), C.POINTER(_I64)]),
     "mcpm_engine_set_kernel_timing": (_I, [_P, _I]),
@@ -385,6 +387,12 @@ class Engine:
 
     def set_graph(self, enable: bool):
         check(self.lib.mcpm_engine_set_graph(self.h, int(enable)))
+
+    def set_persistent(self, enable: bool):
+        check(self.lib.mcpm_engine_set_persistent(self.h, int(enable)))
+
+    def uses_persistent(self) -> bool:
+        return bool(self.lib.mcpm_engine_uses_persistent(self.h))
 
     def set_prefill(self, enable: bool):
         check(self.lib.mcpm_engine_set_prefill(self.h, int(enable)))

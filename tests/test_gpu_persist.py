@@ -1,0 +1,117 @@
+"""The persistent decode launch (all layers of a token in one launch, one work
+group per CU, hand-offs through tagged records) against the CPU oracle and
+against the five-launch-per-layer path, bit for bit."""
+import numpy as np
+import pytest
+
+import mcpm
+import oracle as O
+from conftest import announce, assert_bits
+
+pytestmark = pytest.mark.gpu
+
+# 8 kv heads of 64 and head groups of 4 query heads: the shape the persistent
+# launch takes (kv head h on XCD h)
+KV8 = dict(n_layers=3, dim=1024, n_heads=32, n_kv_heads=8, head_dim=64, ffn=2816, vocab=4096)
+
+
+@pytest.fixture(scope="module")
+def kv8_image():
+    return mcpm.synth_gguf(mcpm.make_config(**KV8), seed=11, mix=0)
+
+
+@pytest.fixture(scope="module")
+def engines(ctx, kv8_image):
+    a = mcpm.Engine(ctx, image=kv8_image)
+    b = mcpm.Engine(ctx, image=kv8_image)
+    a.set_persistent(True)
+    b.set_persistent(False)
+    yield a, b
+    a.free()
+    b.free()
+
+
+def test_off_by_default_and_taken_when_asked(ctx, kv8_image, engines):
+    e = mcpm.Engine(ctx, image=kv8_image)
+    e.init_kv_cache(64)
+    assert not e.uses_persistent()
+    e.free()
+    a, b = engines
+    a.init_kv_cache(256)
+    b.init_kv_cache(256)
+    assert a.uses_persistent(), "the 8-kv-head model fits the persistent launch on a 256-CU device"
+    assert not b.uses_persistent()
+
+
+def test_logits_bit_exact_vs_oracle(engines, kv8_image):
+    a, _ = engines
+    a.init_kv_cache(256)
+    assert a.uses_persistent()
+    om = O.OracleModel(kv8_image)
+    om.init_kv(256)
+    rng = np.random.default_rng(5)
+    toks = rng.integers(0, KV8["vocab"], 80)
+    want = np.empty(KV8["vocab"], np.float32)
+    for pos, t in enumerate(toks):
+        announce(f"persistent forward pos={pos}")
+        got, am = a.forward(int(t), pos)
+        om.forward(int(t), pos, want)
+        assert_bits(got, want)
+        assert am == int(np.argmax(want))
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_generation_matches_five_launch_path(engines, graph):
+    a, b = engines
+    prompt = np.arange(3, 19, dtype=np.int32)
+    outs = []
+    for e in (a, b):
+        e.init_kv_cache(512)
+        e.set_graph(graph)
+        announce(f"greedy graph={graph} persistent={e.uses_persistent()}")
+        outs.append((e.generate_greedy(prompt, 200), e.generate_sampled(prompt, 200, 0.9, 0.95, 21)))
+        e.set_graph(True)
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+    assert len(set(outs[0][1].tolist())) > 8, "a near-constant token sequence pins little"
+
+
+def test_long_context_two_chunks_per_work_group(engines):
+    """Positions past 32 chunks of 64 per kv head (the work groups of one
+    XCD): the first work groups take two chunks each, and the combiner reads
+    every partial, its own two from LDS."""
+    a, b = engines
+    rng = np.random.default_rng(9)
+    prompt = rng.integers(0, KV8["vocab"], 2300).astype(np.int32)
+    outs = []
+    for e in (a, b):
+        e.init_kv_cache(4096)
+        announce(f"long context persistent={e.uses_persistent()}")
+        outs.append(e.generate_greedy_at(prompt, 0, 48))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    # the caches now hold the same rows: one more position's logits, bit for bit
+    pos = 2300 + 48
+    la, _ = a.forward(int(outs[0][-1]), pos)
+    lb, _ = b.forward(int(outs[1][-1]), pos)
+    assert_bits(la, lb)
+
+
+def test_prefill_scratch_growth_then_decode(engines):
+    """Prompts of growing length on one engine: each call grows the prefill
+    scratch (freed and allocated again, zeroed), then decodes through the
+    persistent launch; against the five-launch path with every prompt token
+    decoded one at a time (no prefill scratch at all)."""
+    a, b = engines
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, KV8["vocab"], 1100).astype(np.int32)
+    b.set_prefill(False)
+    try:
+        for T in (100, 300, 577, 1000):
+            for e in (a, b):
+                e.init_kv_cache(4096)
+            announce(f"prefill growth T={T}")
+            got = a.generate_greedy_at(prompt[:T], 0, 4)
+            want = b.generate_greedy_at(prompt[:T], 0, 4)
+            np.testing.assert_array_equal(got, want)
+    finally:
+        b.set_prefill(True)

@@ -143,3 +143,14 @@ def test_reference_sources_link_against_the_mirror(tmp_path):
         assert fn in eng_undef, fn
     r = subprocess.run([os.path.join(out, "minicpm5-cli-engine"), "--help"], capture_output=True, text=True)
     assert r.returncode == 0 and "Usage" in r.stdout
+
+
+def test_persistent_decode_plan_checks():
+    """The persistent decode launch's host-side plan (tests/cpp/persist_check):
+    LDS budget, slab regions and their sources, the rows each work group's
+    tasks read, and the shapes it refuses."""
+    prog = os.path.join(ROOT, "tests", "cpp", "persist_check")
+    assert os.access(prog, os.X_OK), f"{prog} not built (make -C tests/cpp)"
+    r = subprocess.run([prog], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    assert "all persistent-kernel plan checks passed" in r.stdout
