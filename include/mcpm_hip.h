@@ -267,6 +267,14 @@ int mcpm_engine_set_graph(mcpm_engine *e, int enable);
 int mcpm_engine_set_persistent(mcpm_engine *e, int enable);
 /* 1 when the next token runs its layers in one launch. */
 int mcpm_engine_uses_persistent(const mcpm_engine *e);
+/* The spin limit of the waits inside the engine's launches: the fused
+ * kernels' grid barrier (MCPM_FUSED_FFN / MCPM_FUSED_ATTN) and the persistent
+ * launch's hand-offs.  A wait that passes it gives up, every work group then
+ * leaves, and the call returns MCPM_ERR_HIP with the wait state reset, so the
+ * next call runs normally.  0 restores the defaults (1<<20 barrier polls,
+ * 1<<18 hand-off polls).  No counterpart in the reference: it lets tests
+ * drive the give-up path with a tiny limit. */
+int mcpm_engine_set_spin_limit(mcpm_engine *e, unsigned limit);
 
 /* Processes tokens[0..n) at positions pos0.. through every layer together
  * (MFMA GEMMs), leaving the KV cache exactly as n calls of

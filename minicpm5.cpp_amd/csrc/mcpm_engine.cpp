@@ -116,6 +116,7 @@ struct mcpm_engine {
   float* d_draws = nullptr;  // out_cap floats
   // the FFN block as one launch (gate/up, grid barrier, down)
   bool fused_ffn = false;
+  unsigned spin_limit = 0;  // waits' spin limit; 0: each kernel's default
   bool fused_attn = false;  // QKV and attention in one launch (launch_qkv_attn)
   unsigned* gsync = nullptr;  // GRID_SYNC_WORDS words
   // every layer of a token in one persistent launch, where the shape fits:
@@ -375,6 +376,9 @@ hipError_t timed(mcpm_engine* e, int kc, F&& launch) {
 // After the stream is idle: a grid barrier of a fused kernel that gave up
 // (spin limit) left its error word set; report it and reset the barrier
 // state for the next launches.
+unsigned grid_spin_limit(const mcpm_engine* e) { return e->spin_limit ? e->spin_limit : 1u << 20; }
+unsigned pd_spin_limit(const mcpm_engine* e) { return e->spin_limit ? e->spin_limit : 1u << 18; }
+
 int check_grid_sync(mcpm_engine* e) {
   hipStream_t s = e->ctx->stream;
   if (e->attn_q8k) {
@@ -450,7 +454,7 @@ int enqueue_token(mcpm_engine* e, bool short_ctx) {
       a.kvd = kvd;
       hipError_t fe = hipErrorNotSupported;
       if (e->fused_attn) {
-        const GridSync gs{e->gsync, e->gsync + 8 * 64, e->gsync + 8 * 64 + 64, 1u << 20};
+        const GridSync gs{e->gsync, e->gsync + 8 * 64, e->gsync + 8 * 64 + 64, grid_spin_limit(e)};
         const AttnArgs at{e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->max_chunks, part.o, part.mz};
         fe = timed(e, MCPM_KC_QKV, [&] { return launch_qkv_attn(a, at, n_cu, gs, s); });
         if (fe != hipSuccess && fe != hipErrorNotSupported) MCPM_HIP(fe);
@@ -518,7 +522,7 @@ int enqueue_token(mcpm_engine* e, bool short_ctx) {
       dn.resid = e->x;
       hipError_t fe = hipErrorNotSupported;
       if (e->fused_ffn) {
-        const GridSync gs{e->gsync, e->gsync + 8 * 64, e->gsync + 8 * 64 + 64, 1u << 20};
+        const GridSync gs{e->gsync, e->gsync + 8 * 64, e->gsync + 8 * 64 + 64, grid_spin_limit(e)};
         fe = timed(e, MCPM_KC_GATE_UP, [&] { return launch_ffn_fused(gu, dn, n_cu, gs, s); });
         if (fe != hipSuccess && fe != hipErrorNotSupported) MCPM_HIP(fe);
       }
@@ -740,7 +744,7 @@ int pd_setup(mcpm_engine* e) {
   pd_bind_records(a, e->pd_rec);
   a.epoch = e->pd_sync;
   a.err = e->pd_sync + 64;
-  a.spin_limit = 1u << 18;
+  a.spin_limit = pd_spin_limit(e);
   a.x_out = e->x;
   e->pd_args = a;
   e->pd = s;
@@ -867,6 +871,15 @@ int mcpm_engine_set_persistent(mcpm_engine* e, int enable) {
 }
 
 int mcpm_engine_uses_persistent(const mcpm_engine* e) { return e && e->pd_ready && e->pd_want ? 1 : 0; }
+
+int mcpm_engine_set_spin_limit(mcpm_engine* e, unsigned limit) {
+  if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_set_spin_limit: null engine");
+  MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
+  e->spin_limit = limit;
+  e->pd_args.spin_limit = pd_spin_limit(e);
+  drop_graph(e);  // captured launches hold the old limit
+  return MCPM_OK;
+}
 
 int mcpm_engine_forward(mcpm_engine* e, int token, int pos, int max_seq_len, float* logits, int* argmax) {
   if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_forward: null engine");

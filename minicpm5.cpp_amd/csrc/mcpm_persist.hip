@@ -155,7 +155,8 @@ __device__ __forceinline__ bool pd_poll(const PdArgs& a, const uint64_t* buf, ui
 #pragma unroll
     for (int k = 0; k < K; ++k)
       if (static_cast<uint32_t>(r[k] >> 32) != tag) pend |= 1u << k;
-    if (threadIdx.x == 0 && (++spins & 63) == 0 && (spins > a.spin_limit || ld_u32c(a.err))) {
+    ++spins;
+    if (threadIdx.x == 0 && (spins > a.spin_limit || ((spins & 63) == 0 && ld_u32c(a.err)))) {
       misc[0] = 1;
       st_u32c(a.err, 1u);
     }

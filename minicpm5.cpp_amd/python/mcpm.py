@@ -18,6 +18,8 @@ LIB_PATH = os.path.join(PKG_DIR, "libmcpm_hip.so")
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
 KC_QKV, KC_ATTN, KC_OPROJ, KC_GATE_UP, KC_DOWN, KC_LM_HEAD, KC_LAYERS = range(7)
 KC_NAMES = ["qkv", "attn", "oproj", "gate_up", "down", "lm_head", "layers"]
+# include/mcpm_hip.h error codes
+ERR_HIP, ERR_ARG, ERR_UNSUPPORTED, ERR_CONTEXT, ERR_IO, ERR_FORMAT, ERR_NOMEM = -1, -2, -3, -4, -5, -6, -7
 
 # ggml block layouts (reference include/ops.h:33-65)
 Q8_0 = np.dtype([("d", "<u2"), ("qs", "i1", 32)])
@@ -123,6 +125,7 @@ _SIGS = {
     "mcpm_engine_set_graph": (_I, [_P, _I]),
     "mcpm_engine_set_persistent": (_I, [_P, _I]),
     "mcpm_engine_uses_persistent": (_I, [_P]),
+    "mcpm_engine_set_spin_limit": (_I, [_P, C.c_uint]),
     "mcpm_set_op_timing": (_I, [_P, _I]),
     "mcpm_op_time": (_I, [_P, C.POINTER(C.c_double), C.POINTER(_I64)]),
     "mcpm_engine_set_kernel_timing": (_I, [_P, _I]),
@@ -393,6 +396,9 @@ class Engine:
 
     def uses_persistent(self) -> bool:
         return bool(self.lib.mcpm_engine_uses_persistent(self.h))
+
+    def set_spin_limit(self, limit: int):
+        check(self.lib.mcpm_engine_set_spin_limit(self.h, int(limit)))
 
     def set_prefill(self, enable: bool):
         check(self.lib.mcpm_engine_set_prefill(self.h, int(enable)))

@@ -6,6 +6,7 @@
 #include "mcpm_oracle.h"
 
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -572,6 +573,11 @@ int or_get_embedding(float *out, int type, const void *embd, int dim, int token)
 }
 
 /* Greedy decoding: first index of the maximum. */
+void or_set_threads(int n) {
+    omp_set_dynamic(0);
+    omp_set_num_threads(n);
+}
+
 int or_argmax(const float *x, int n) {
     int best = 0;
     for (int i = 1; i < n; ++i) if (x[i] > x[best]) best = i;

@@ -99,6 +99,8 @@ int or_attention(float *out, const float *q, const float *k_cur, const float *v_
 /* Returns -1 (zero fill) for unsupported embedding types. */
 int or_get_embedding(float *out, int type, const void *embd, int dim, int token);
 int or_argmax(const float *x, int n);
+/* The OpenMP team of the oracle's parallel loops (a fixed team of n). */
+void or_set_threads(int n);
 
 /* ---- whole model ---- */
 typedef struct {

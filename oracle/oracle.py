@@ -68,6 +68,7 @@ _ORACLE_SIGS = {
     "or_attention": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "or_get_embedding": (_I, [_P, _I, _P, _I, _I]),
     "or_argmax": (_I, [_P, _I]),
+    "or_set_threads": (None, [_I]),
     "or_model_create": (_P, [C.POINTER(OrConfig), _P, _I, _P, _P, _I, C.POINTER(OrLayer)]),
     "or_model_init_kv": (_I, [_P, _I]),
     "or_model_forward": (_I, [_P, _I, _I, _P]),

@@ -151,10 +151,12 @@ def q8k(ref):
 
 def model_greedy(name, cfg, n_prompt, n_gen, seed, use_reference=True, search=1, mix=0, min_distinct=0):
     """Greedy decode of a synthetic model.  With use_reference the tokens are
-    the reference's (its ops, one thread) and the oracle's agreement is
-    recorded; `search` > 1 tries up to that many seeds and keeps the first
-    whose decode the oracle reproduces for all n_gen steps, else the seed
-    with the longest agreement."""
+    the reference's (its ops, one thread) and the number of leading steps the
+    oracle reproduces is recorded as reference_agree_steps; `search` > 1
+    tries up to that many seeds and keeps the first whose decode the oracle
+    reproduces for all n_gen steps, else the seed with the longest agreement.
+    Without use_reference the tokens are the oracle's own and
+    reference_agree_steps is -1 (no reference run was compared)."""
     best = None
     for s in range(seed, seed + search):
         img = mcpm.synth_gguf(cfg, seed=s, mix=mix)
@@ -165,14 +167,14 @@ def model_greedy(name, cfg, n_prompt, n_gen, seed, use_reference=True, search=1,
         if len(set(tokens.tolist())) < min_distinct:
             print(f"{name}: seed {s} gives {len(set(tokens.tolist()))} distinct tokens, skipped", flush=True)
             continue
-        agree = n_gen
+        agree = -1
         if use_reference:
             ot = O.OracleModel(img).generate_greedy(prompt, n_gen)
             agree = int(np.argmax(ot != tokens)) if not np.array_equal(ot, tokens) else n_gen
             print(f"{name}: seed {s} oracle reproduces the reference for {agree}/{n_gen} steps", flush=True)
         if best is None or agree > best[0]:
             best = (agree, s, img, prompt, tokens, logits)
-        if agree == n_gen:
+        if agree == n_gen or not use_reference:
             break
     assert best is not None, f"{name}: no seed gave {min_distinct} distinct tokens"
     agree, s, img, prompt, tokens, logits = best
@@ -180,7 +182,7 @@ def model_greedy(name, cfg, n_prompt, n_gen, seed, use_reference=True, search=1,
     srt = np.sort(L, axis=1)
     out = dict(seed=s, config=np.array([cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn,
                                         cfg.vocab], np.int64), rope_base=np.float32(cfg.rope_base), mix=mix,
-               image_sha=sha(img), prompt=prompt, tokens=tokens, oracle_agree_steps=agree,
+               image_sha=sha(img), prompt=prompt, tokens=tokens, reference_agree_steps=agree,
                top2_margin=(srt[:, -1] - srt[:, -2]), logit_sum=L.astype(np.float64).sum(1),
                logit_absmax=np.abs(L).max(1), logits_sha=np.array([sha(l) for l in L]))
     if L.nbytes <= 256 << 10:

@@ -69,7 +69,7 @@ def test_greedy_matches_oracle_and_reference(small_engine, small_image, graph):
     # the reference's own ops (one thread), for as long as the oracle agrees
     # with them: the untied head's top-2 margins are small, and the
     # reference's -ffast-math RMS and lane sums flip an argmax after that
-    k = int(g["oracle_agree_steps"])
+    k = int(g["reference_agree_steps"])
     assert k >= 16
     np.testing.assert_array_equal(got[:k], g["tokens"][:k])
     small_engine.set_graph(True)
@@ -248,7 +248,7 @@ def test_reference_geometry_tokens(ctx, name):
     n = len(g["tokens"])
     announce(f"{name} greedy")
     got = e.generate_greedy(g["prompt"], n)
-    k = int(g["oracle_agree_steps"])
+    k = int(g["reference_agree_steps"])
     np.testing.assert_array_equal(got[:k], g["tokens"][:k])
     want = O.OracleModel(img).generate_greedy(g["prompt"], n)
     np.testing.assert_array_equal(got, want)
@@ -400,6 +400,42 @@ def test_fused_ffn_block_matches_oracle(ctx, small_image, monkeypatch):
     try:
         e.init_kv_cache(128)
         np.testing.assert_array_equal(e.generate_greedy(gf["prompt"], 32), gf["tokens"][:32])
+    finally:
+        e.free()
+
+
+@pytest.mark.parametrize("env", ["MCPM_FUSED_FFN", "MCPM_FUSED_ATTN"])
+def test_grid_barrier_give_up_then_recovers(ctx, small_image, monkeypatch, env):
+    """The fused kernels' grid barrier with a spin limit of 1 poll: a wait
+    gives up, every work group leaves through its own bounded wait, and the
+    call returns MCPM_ERR_HIP with the barrier state reset; with the default
+    limit restored, the next calls give the oracle's logits bit for bit."""
+    monkeypatch.setenv(env, "1")
+    e = mcpm.Engine(ctx, image=small_image)
+    try:
+        e.init_kv_cache(64)
+        prompt = np.arange(5, 21, dtype=np.int32)
+        e.set_spin_limit(1)
+        codes = []
+        for i in range(6):
+            announce(f"{env}: spin limit 1, call {i}")
+            try:
+                e.generate_greedy(prompt, 4)
+            except mcpm.McpmError as err:
+                codes.append(err.code)
+                break
+        assert codes == [mcpm.ERR_HIP], "no wait gave up at a spin limit of 1"
+        e.set_spin_limit(0)
+        announce(f"{env}: default spin limit after the give-up")
+        om = O.OracleModel(small_image)
+        om.init_kv(64)
+        want = np.empty(4000, np.float32)
+        for pos, t in enumerate(prompt):
+            got, _ = e.forward(int(t), pos)
+            om.forward(int(t), pos, want)
+            assert_bits(got, want)
+        np.testing.assert_array_equal(e.generate_greedy(prompt, 8),
+                                      O.OracleModel(small_image).generate_greedy(prompt, 8))
     finally:
         e.free()
 

@@ -115,3 +115,35 @@ def test_prefill_scratch_growth_then_decode(engines):
             np.testing.assert_array_equal(got, want)
     finally:
         b.set_prefill(True)
+
+
+def test_hand_off_give_up_then_recovers(engines, kv8_image):
+    """Hand-off waits with a spin limit of 1 poll: a wait gives up, every
+    work group leaves, the call returns MCPM_ERR_HIP and the records and
+    launch count are reset; with the default limit restored the next calls
+    give the oracle's logits bit for bit."""
+    a, _ = engines
+    a.init_kv_cache(256)
+    assert a.uses_persistent()
+    prompt = np.arange(40, 56, dtype=np.int32)
+    a.set_spin_limit(1)
+    codes = []
+    try:
+        for i in range(6):
+            announce(f"persistent: spin limit 1, call {i}")
+            try:
+                a.generate_greedy(prompt, 4)
+            except mcpm.McpmError as err:
+                codes.append(err.code)
+                break
+    finally:
+        a.set_spin_limit(0)
+    assert codes == [mcpm.ERR_HIP], "no wait gave up at a spin limit of 1"
+    announce("persistent: default spin limit after the give-up")
+    om = O.OracleModel(kv8_image)
+    om.init_kv(256)
+    want = np.empty(KV8["vocab"], np.float32)
+    for pos, t in enumerate(prompt):
+        got, _ = a.forward(int(t), pos)
+        om.forward(int(t), pos, want)
+        assert_bits(got, want)

@@ -2,7 +2,8 @@
 mcpm_execute_attention, the entry point whose kernels it shares: the same
 output and cache rows bit for bit, on two calls in a row (the second on a
 smaller shape, so stale records of the first stay in the shared scratch
-array beyond what the second reads), and the size limit rejected cleanly."""
+array beyond what the second reads), a second call after one over NaN
+inputs against the oracle, and the size limit rejected cleanly."""
 import numpy as np
 import pytest
 
@@ -43,6 +44,43 @@ def test_noalloc_attention_matches_allocating_entry(ctx, cases):
         want = _run(ctx, ctx.lib.mcpm_execute_attention, q, k, v, kc, vc, pos, cap, nh, nkv, hd)
         for g, w in zip(got, want):
             assert_bits(g, w)
+
+
+@pytest.mark.parametrize("second", [((32, 8, 64), 100, 256), ((16, 2, 128), 700, 1024)])
+def test_noalloc_attention_never_reads_a_previous_calls_records(ctx, orc, second):
+    """A first call over NaN queries, keys and values leaves NaN partial
+    records over 64 chunks of 32 heads in the shared scratch; the second,
+    smaller call reads fewer records, and must equal the oracle's attention
+    and the allocating entry point bit for bit, so a read of a leftover
+    record would show as a NaN or a mismatch."""
+    nh, nkv, hd = 32, 8, 64
+    cap = 4096
+    nan = np.full(cap * nkv * hd, np.nan, np.float32)
+    announce("noalloc attention: NaN call, 64 chunks")
+    out, _, _ = _run(ctx, ctx.lib.mcpm_execute_attention_noalloc, np.full(nh * hd, np.nan, np.float32),
+                     np.full(nkv * hd, np.nan, np.float32), np.full(nkv * hd, np.nan, np.float32), nan, nan.copy(),
+                     4000, cap, nh, nkv, hd)
+    assert np.isnan(out).any()  # the records it left hold NaNs
+    (nh, nkv, hd), pos, cap = second
+    rng = np.random.default_rng(77 + pos)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(nkv * hd).astype(np.float32)
+    v = rng.standard_normal(nkv * hd).astype(np.float32)
+    kc = rng.standard_normal(cap * nkv * hd).astype(np.float32)
+    vc = rng.standard_normal(cap * nkv * hd).astype(np.float32)
+    announce(f"noalloc attention after the NaN call: heads {nh}/{nkv}x{hd} pos {pos} cap {cap}")
+    got = _run(ctx, ctx.lib.mcpm_execute_attention_noalloc, q, k, v, kc, vc, pos, cap, nh, nkv, hd)
+    want = np.zeros(nh * hd, np.float32)
+    kc2, vc2 = kc.copy(), vc.copy()
+    P = lambda a: a.ctypes.data
+    assert orc.or_attention(P(want), P(q), P(k), P(v), P(kc2), P(vc2), pos, cap, nh, nkv, hd) == 0
+    assert not np.isnan(got[0]).any()
+    assert_bits(got[0], want)
+    assert_bits(got[1], kc2)
+    assert_bits(got[2], vc2)
+    alloc = _run(ctx, ctx.lib.mcpm_execute_attention, q, k, v, kc, vc, pos, cap, nh, nkv, hd)
+    for g, w in zip(got, alloc):
+        assert_bits(g, w)
 
 
 def test_noalloc_attention_rejects_sizes_beyond_the_scratch(ctx):
