@@ -9,8 +9,9 @@
 //      h = b % 8 (so head h's rows are computed on XCD h); RoPE; K and V
 //      rows at pos into the cache
 //   A  attention of kv head h: chunk c of 64 positions on work group
-//      (h, c mod W); work group (h, 0) combines the chunks' partials in chunk
-//      order and quantizes the head group's output ties-even (Q8_K blocks)
+//      (h, c mod W); work group (h, W-1), which has no chunk below W chunks,
+//      combines the chunks' partials in chunk order and quantizes the head
+//      group's output ties-even (Q8_K blocks)
 //   O  O projection of this work group's rows of x, residual add
 //   G  RMSNorm + Q8_K (ties away); gate and up rows of its FFN pairs; SwiGLU
 //   D  Q8_K (ties away) of h; down projection of its rows of x; residual add
@@ -31,9 +32,10 @@
 // once from the weight planes), in four regions: QKV, O, gate/up, down.  A
 // region is copied into LDS (direct-to-LDS loads, 1 KiB per wave
 // instruction) after its previous use, during the hand-off wait of a phase
-// before the one that reads it: O at Q, the next layer's QKV at O, gate/up
-// at O (a layer ahead, at D, on the work groups that combine attention
-// chunks), down at G.  The wait ends with every copy landed.
+// before the one that reads it: O at Q, the next layer's QKV and gate/up at
+// O (at A on the work groups that combine attention chunks, which wait there
+// for the chunks' partials), down at G.  The wait ends with every copy
+// landed.
 //
 // Every wait is bounded: past spin_limit, or once another work group has
 // given up, the work group sets the error word and returns.
@@ -542,17 +544,15 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // hand-off (the waves are idle then, and a copy stalls the wave issuing it
   // for most of its transfer): each region after its last use, before the
   // wait of a phase ahead of its next.  Q: this layer's O; O: the next
-  // layer's QKV, and this layer's gate/up except on the kv heads' combining
-  // work groups (the O wait is long elsewhere: it waits for those); G: this
-  // layer's down (the attention's staging is done); D: on the combining work
-  // groups, the next layer's gate/up.
+  // layer's QKV and this layer's gate/up, except on the kv heads' combining
+  // work groups (k = W-1), which take them at A, while they wait for the
+  // chunks' partials; G: this layer's down (the attention's staging is done).
   if (kind == 0) pd_copy_region(a, LDS, l, 1);
-  if (kind == 2) {
+  if (kind == 2 && me.k != s.W - 1) {
     if (l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 0);
-    if (me.k != 0) pd_copy_region(a, LDS, l, 2);
+    pd_copy_region(a, LDS, l, 2);
   }
   if (kind == 3) pd_copy_region(a, LDS, l, 3);
-  if (kind == 4 && me.k == 0 && l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 2);
 
   // hand-off and prologue: the Q8_K activations into the scratch
   if (kind == 0 || kind == 3) {
@@ -691,7 +691,12 @@ __device__ __forceinline__ void pd_fill_last(AttnRegs<4>& R, const float* kr, co
 }
 
 // The attention of layer l (src/ops/ops.cpp:537-628) for kv head h = b % 8,
-// head_dim 64, a head group of 256 outputs (gh).
+// head_dim 64, a head group of 256 outputs (gh).  Chunk c of 64 positions on
+// work group (h, c mod W); work group (h, W-1) combines the head's chunks.
+// Below W chunks the combining work group has no chunk of its own and would
+// wait idle for the partials, so it takes its weight copies for the next
+// phases here (the next layer's QKV, this layer's gate/up), and every other
+// work group its own at O.
 __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LDS, uint32_t* S, uint32_t tag, int T,
                                              uint32_t& vit) {
   const PdShape& s = a.s;
@@ -699,56 +704,63 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
             k = static_cast<int>(blockIdx.x) / PD_XCDS, W = s.W;
   uint32_t* misc = S + s.s_misc;
   const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
-  if (k >= nch) return true;  // no chunk of this context
+  const bool combiner = k == W - 1;
+  if (k >= nch && !combiner) return true;  // no chunk of this context
+  if (combiner) {
+    if (l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 0);
+    pd_copy_region(a, LDS, l, 2);
+  }
   constexpr int HD = 64, GH = 256, OPT = ATTN_MAX_GROUP * HD / 256;
   const int group = s.group, kvd = s.kvd;
-  const size_t lay = static_cast<size_t>(l) * a.max_seq * kvd;
-  const float* kc = a.kc + lay;
-  const float* vc = a.vc + lay;
   const AttnLds<HD> A(reinterpret_cast<float*>(LDS + s.reg_off[3]));
-  AttnRegs<4> R;
-  const size_t head_off = static_cast<size_t>(h) * HD;
-  // chunk k's rows before pos are in the cache since earlier launches
-  attn_load_chunk<4, true>(R, kc, vc, k, T, kvd, head_off, HD / 4, ATTN_CHUNK * HD / 4);
-  // q of the head group and the K and V rows at pos, from the QKV phase
-  constexpr int NREC = GH + 2 * HD;
-  uint32_t qv[2];
-  if (!pd_poll<2>(a, a.rqkv + static_cast<size_t>(h) * NREC, tag,
-                  [&](int kk) { return t + 256 * kk < NREC ? t + 256 * kk : -1; }, qv, misc, vit))
-    return false;
   float* kr = reinterpret_cast<float*>(S + s.s_u);
   float* vr = kr + HD;
   float* sX = vr + HD;       // [GH] the combined output
   float* sO = sX + GH;       // [2][GH] this work group's chunks' o_c
   float* sM = sO + 2 * GH;   // [max_chunks][group] m_c (combining work group)
   float* sZ = sM + 64 * ATTN_MAX_GROUP;
-  A.sQ[(t / HD) * HD + t % HD] = __uint_as_float(qv[0]);
-  if (t < 2 * HD) kr[t] = __uint_as_float(qv[1]);  // kr, vr contiguous
-  pd_bar();
-  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
-#pragma unroll 1
-  for (int cc = 0; cc < 2; ++cc) {
-    const int c = k + W * cc;
-    if (c >= nch) break;  // uniform
-    if (c == nch - 1) pd_fill_last(R, kr, vr, c, T);
-    pd_bar();  // readers of the previous chunk are done
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int f = t + 256 * u, jr = f >> 4, c4 = f & 15;
-      *reinterpret_cast<f32x4*>(&A.sK[jr * (HD + 4) + c4 * 4]) = R.k[u];
-      *reinterpret_cast<f32x4*>(&A.sV[jr * HD + c4 * 4]) = R.v[u];
-    }
-    if (c + W < nch) attn_load_chunk<4, true>(R, kc, vc, c + W, T, kvd, head_off, HD / 4, ATTN_CHUNK * HD / 4);
+  if (k < nch) {
+    const size_t lay = static_cast<size_t>(l) * a.max_seq * kvd;
+    const float* kc = a.kc + lay;
+    const float* vc = a.vc + lay;
+    AttnRegs<4> R;
+    const size_t head_off = static_cast<size_t>(h) * HD;
+    // chunk k's rows before pos are in the cache since earlier launches
+    attn_load_chunk<4, true>(R, kc, vc, k, T, kvd, head_off, HD / 4, ATTN_CHUNK * HD / 4);
+    // q of the head group and the K and V rows at pos, from the QKV phase
+    constexpr int NREC = GH + 2 * HD;
+    uint32_t qv[2];
+    if (!pd_poll<2>(a, a.rqkv + static_cast<size_t>(h) * NREC, tag,
+                    [&](int kk) { return t + 256 * kk < NREC ? t + 256 * kk : -1; }, qv, misc, vit))
+      return false;
+    A.sQ[(t / HD) * HD + t % HD] = __uint_as_float(qv[0]);
+    if (t < 2 * HD) kr[t] = __uint_as_float(qv[1]);  // kr, vr contiguous
     pd_bar();
-    float o[OPT];
-    attn_token_chunk<HD, OPT, true>(A.sK, A.sV, A.sQ, A.sE, A.sMZ + cc * ATTN_MAX_GROUP, c, T, group, HD, GH, scale,
-                                    o, t);
-    sO[cc * GH + t] = o[0];
+    const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+#pragma unroll 1
+    for (int cc = 0; cc < 2; ++cc) {
+      const int c = k + W * cc;
+      if (c >= nch) break;  // uniform
+      if (c == nch - 1) pd_fill_last(R, kr, vr, c, T);
+      pd_bar();  // readers of the previous chunk are done
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int f = t + 256 * u, jr = f >> 4, c4 = f & 15;
+        *reinterpret_cast<f32x4*>(&A.sK[jr * (HD + 4) + c4 * 4]) = R.k[u];
+        *reinterpret_cast<f32x4*>(&A.sV[jr * HD + c4 * 4]) = R.v[u];
+      }
+      if (c + W < nch) attn_load_chunk<4, true>(R, kc, vc, c + W, T, kvd, head_off, HD / 4, ATTN_CHUNK * HD / 4);
+      pd_bar();
+      float o[OPT];
+      attn_token_chunk<HD, OPT, true>(A.sK, A.sV, A.sQ, A.sE, A.sMZ + cc * ATTN_MAX_GROUP, c, T, group, HD, GH,
+                                      scale, o, t);
+      sO[cc * GH + t] = o[0];
+    }
+    pd_bar();  // (m_c, z_c) of every head, every chunk's o_c
   }
-  pd_bar();  // (m_c, z_c) of every head, every chunk's o_c
   const int ppc = GH + 2 * group;
   uint64_t* part = a.rpart + static_cast<size_t>(h) * s.max_chunks * ppc;
-  if (k != 0) {
+  if (!combiner) {
 #pragma unroll 1
     for (int cc = 0; cc < 2; ++cc) {
       const int c = k + W * cc;
@@ -763,33 +775,36 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
     }
     return true;
   }
-  // Work group (h, 0) combines the chunks in chunk order with the per-token
-  // path's arithmetic: m = max m_c; f_c = exp(m_c - m); Z = fma(z_c, f_c, Z);
-  // O = fma(o_c, f_c, O); out = O / Z.  Own chunks 0 and W come from LDS,
-  // the others from their records: in one wait, every chunk's (m_c, z_c)
-  // (one (chunk, head) per thread, into LDS) and this thread's o_c of chunks
-  // 1..8; later chunks' o_c in batches of 8 as the chain reaches them.
+  // The combining work group takes the chunks in chunk order with the
+  // per-token path's arithmetic: m = max m_c; f_c = exp(m_c - m);
+  // Z = fma(z_c, f_c, Z); O = fma(o_c, f_c, O); out = O / Z.  Its own chunks
+  // (W-1 and 2W-1, where they exist) come from LDS, the others from their
+  // records: in one wait, every chunk's (m_c, z_c) (one (chunk, head) per
+  // thread, into LDS) and this thread's o_c of chunks 0..7; later chunks' o_c
+  // in batches of 8 as the chain reaches them.
+  const int own0 = W - 1, own1 = 2 * W - 1;
   bool ok = true;
   const int hh = t / HD;
   uint32_t rv[10];
   {
     const int cq = t / group, hq = t - cq * group;
-    const bool mz_rec = t < nch * group && cq != 0 && cq != W;
+    const bool mine = cq == own0 || cq == own1;
+    const bool mz_rec = t < nch * group && !mine;
     const uint64_t* p[10];
     p[0] = part + static_cast<size_t>(min(cq, nch - 1)) * ppc + GH + hq;
     p[1] = p[0] + group;
     uint32_t mask = mz_rec ? 3u : 0u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int c = 1 + i;
+      const int c = i;
       p[2 + i] = part + static_cast<size_t>(min(c, nch - 1)) * ppc + t;
-      if (c < nch && c != W) mask |= 1u << (2 + i);
+      if (c < nch && c != own0 && c != own1) mask |= 1u << (2 + i);
     }
     ok = pd_wait_m<10>(p, mask, tag, a.spin_limit, rv);
     if (t < nch * group) {
       float mc, zc;
-      if (cq == 0 || cq == W) {
-        const float2 mz = A.sMZ[(cq == 0 ? 0 : ATTN_MAX_GROUP) + hq];
+      if (mine) {
+        const float2 mz = A.sMZ[(cq == own0 ? 0 : ATTN_MAX_GROUP) + hq];
         mc = mz.x;
         zc = mz.y;
       } else {
@@ -812,28 +827,27 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
     Z = __builtin_fmaf(sZ[c * group + hh], f, Z);
     O = __builtin_fmaf(o, f, O);
   };
-  step(0, sO[t]);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int c = 1 + i;
-    if (c < nch) step(c, c == W ? sO[GH + t] : __uint_as_float(rv[2 + i]));
+    const int c = i;
+    if (c < nch) step(c, c == own0 ? sO[t] : c == own1 ? sO[GH + t] : __uint_as_float(rv[2 + i]));
   }
 #pragma unroll 1
-  for (int c0 = 9; c0 < nch && ok; c0 += 8) {
+  for (int c0 = 8; c0 < nch && ok; c0 += 8) {
     const uint64_t* pb[8];
     uint32_t mask = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int c = c0 + i;
       pb[i] = part + static_cast<size_t>(min(c, nch - 1)) * ppc + t;
-      if (c < nch && c != W) mask |= 1u << i;
+      if (c < nch && c != own0 && c != own1) mask |= 1u << i;
     }
     uint32_t ov[8];
     ok = pd_wait_m<8>(pb, mask, tag, a.spin_limit, ov);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int c = c0 + i;
-      if (ok && c < nch) step(c, c == W ? sO[GH + t] : __uint_as_float(ov[i]));
+      if (ok && c < nch) step(c, c == own0 ? sO[t] : c == own1 ? sO[GH + t] : __uint_as_float(ov[i]));
     }
   }
   sX[t] = O / Z;
@@ -899,7 +913,6 @@ __global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
     }
   }
   pd_copy_region(a, LDS, 0, 0);
-  if (blockIdx.x < PD_XCDS) pd_copy_region(a, LDS, 0, 2);  // the combining work groups' first gate/up
   // one loop over the phases, so that each phase's code exists once
 #pragma unroll 1
   for (int ph = 0; ph < 5 * L; ++ph) {
