@@ -136,6 +136,34 @@ __device__ __forceinline__ void pd_copy(const uint8_t* src, uint8_t* lds, int by
   }
 }
 
+// K and V rows of chunk c (positions 64c .. 64c+63) of the kv head at
+// head_off into the attention's staging (K rows at a stride of 68 floats, V
+// rows at 64: AttnLds<64>) with direct-to-LDS loads, 17 + 16 wave
+// instructions of 1 KiB: lane i of instruction n writes bytes 1024n + 16i,
+// so its source is the row and column that land there (a K row's padding
+// reads the dummy).  Rows at or past T-1 read the dummy too: row T-1 is
+// written in this launch (it comes from the QKV phase's records) and later
+// rows are outside the context.  Like pd_copy, the data is there once the
+// issuing waves have waited for their vector memory counter.
+__device__ __forceinline__ void pd_stage_chunk(const float* kc, const float* vc, int c, int T, int kvd,
+                                               size_t head_off, const float* dummy, uint8_t* lds) {
+  const int wave = static_cast<int>(threadIdx.x >> 6), lane = static_cast<int>(threadIdx.x & 63);
+  const uint32_t l0 = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(lds)));
+  constexpr int KROW = (64 + 4) * 4, VROW = 64 * 4, KB = 64 * KROW / 1024, VB = 64 * VROW / 1024;
+  for (int n = wave; n < KB + VB; n += 4) {
+    const bool isk = n < KB;
+    const int pos = ((isk ? n : n - KB) << 10) + lane * 16;  // byte offset within the K or V rows
+    const int rb = isk ? KROW : VROW;
+    const int row = pos / rb, cb = pos - row * rb, j = ATTN_CHUNK * c + row;
+    const float* src = cb < VROW && j < T - 1
+                           ? (isk ? kc : vc) + static_cast<size_t>(j) * kvd + head_off + (cb >> 2)
+                           : dummy;
+    const uint32_t m = __builtin_amdgcn_readfirstlane(l0 + static_cast<uint32_t>(n << 10));
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m), "v"(src) : "m0", "memory");
+  }
+}
+
 // ------------------------------------------------------------ hand-offs ---
 // Waits (the whole work group) until record idx(k) of buf carries `tag` for
 // every k < K of every thread (idx < 0: no record, value 0); values to v.
@@ -547,7 +575,15 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // layer's QKV and this layer's gate/up, except on the kv heads' combining
   // work groups (k = W-1), which take them at A, while they wait for the
   // chunks' partials; G: this layer's down (the attention's staging is done).
-  if (kind == 0) pd_copy_region(a, LDS, l, 1);
+  if (kind == 0) {
+    pd_copy_region(a, LDS, l, 1);
+    // this layer's attention chunk (the down region is free until G)
+    if (me.k < (pos + ATTN_CHUNK) / ATTN_CHUNK) {
+      const size_t lay = static_cast<size_t>(l) * a.max_seq * s.kvd;
+      pd_stage_chunk(a.kc + lay, a.vc + lay, me.k, pos + 1, s.kvd, static_cast<size_t>(me.kvh) * s.hd, a.norms,
+                     LDS + s.reg_off[3]);
+    }
+  }
   if (kind == 2 && me.k != s.W - 1) {
     if (l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 0);
     pd_copy_region(a, LDS, l, 2);
@@ -725,8 +761,7 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
     const float* vc = a.vc + lay;
     AttnRegs<4> R;
     const size_t head_off = static_cast<size_t>(h) * HD;
-    // chunk k's rows before pos are in the cache since earlier launches
-    attn_load_chunk<4, true>(R, kc, vc, k, T, kvd, head_off, HD / 4, ATTN_CHUNK * HD / 4);
+    // chunk k's rows before pos are in LDS since the QKV phase (pd_stage_chunk);
     // q of the head group and the K and V rows at pos, from the QKV phase
     constexpr int NREC = GH + 2 * HD;
     uint32_t qv[2];
@@ -741,13 +776,22 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
     for (int cc = 0; cc < 2; ++cc) {
       const int c = k + W * cc;
       if (c >= nch) break;  // uniform
-      if (c == nch - 1) pd_fill_last(R, kr, vr, c, T);
-      pd_bar();  // readers of the previous chunk are done
+      if (cc == 0) {
+        // row T-1 of the staged chunk from the hand-off
+        if (c == nch - 1 && t < 2 * HD) {
+          const int jr = T - 1 - c * ATTN_CHUNK;
+          if (t < HD) A.sK[jr * (HD + 4) + t] = kr[t];
+          else A.sV[jr * HD + (t - HD)] = vr[t - HD];
+        }
+      } else {
+        if (c == nch - 1) pd_fill_last(R, kr, vr, c, T);
+        pd_bar();  // readers of the previous chunk are done
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int f = t + 256 * u, jr = f >> 4, c4 = f & 15;
-        *reinterpret_cast<f32x4*>(&A.sK[jr * (HD + 4) + c4 * 4]) = R.k[u];
-        *reinterpret_cast<f32x4*>(&A.sV[jr * HD + c4 * 4]) = R.v[u];
+        for (int u = 0; u < 4; ++u) {
+          const int f = t + 256 * u, jr = f >> 4, c4 = f & 15;
+          *reinterpret_cast<f32x4*>(&A.sK[jr * (HD + 4) + c4 * 4]) = R.k[u];
+          *reinterpret_cast<f32x4*>(&A.sV[jr * HD + c4 * 4]) = R.v[u];
+        }
       }
       if (c + W < nch) attn_load_chunk<4, true>(R, kc, vc, c + W, T, kvd, head_off, HD / 4, ATTN_CHUNK * HD / 4);
       pd_bar();
