@@ -618,23 +618,12 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   } else {
     // h in rounds of up to 16 blocks: records t + 256k of the round (lanes
     // on consecutive records) into the staging area, then block r16 of the
-    // round quantized by its row of 16 lanes (zero past ffn)
+    // round quantized by its row of 16 lanes (zero past ffn).  Up to 24
+    // blocks every record is waited for at once (two rounds from registers),
+    // so the second round costs no second round trip.
     const int nbh = s.nbh, ffn = s.ffn;
     float* U = reinterpret_cast<float*>(S + s.s_u);
-#pragma unroll 1
-    for (int b0 = 0; b0 < nbh; b0 += 16) {
-      const int nbr = min(16, nbh - b0), e0 = b0 * 256;
-      uint32_t hv[16];
-      if (!pd_poll<16>(a, a.rh, tag,
-                       [&](int k) {
-                         const int e = e0 + t + 256 * k;
-                         return k < nbr && e < ffn ? e : -1;
-                       },
-                       hv, misc, vit))
-        return false;
-#pragma unroll
-      for (int k = 0; k < 16; ++k)
-        if (k < nbr) U[t + 256 * k] = __uint_as_float(hv[k]);
+    auto quant_round = [&](int b0, int nbr) {
       pd_bar();
       if (r16 < nbr) {
         float v[16];
@@ -653,6 +642,43 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
         pd_store_xblock(S, s, b0 + r16, j, packed, d, gsum);
       }
       pd_bar();  // the staging area's readers are done before the next round
+    };
+    if (nbh <= 24) {
+      uint32_t hv[24];
+      if (!pd_poll<24>(a, a.rh, tag,
+                       [&](int k) {
+                         const int e = t + 256 * k;
+                         return k < nbh && e < ffn ? e : -1;
+                       },
+                       hv, misc, vit))
+        return false;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int b0 = 16 * rr, nbr = min(16, nbh - b0);
+        if (nbr > 0) {  // uniform
+#pragma unroll
+          for (int k = 0; k < 16; ++k)
+            if (k < nbr) U[t + 256 * k] = __uint_as_float(hv[b0 + k < 24 ? b0 + k : 0]);
+          quant_round(b0, nbr);
+        }
+      }
+    } else {
+#pragma unroll 1
+      for (int b0 = 0; b0 < nbh; b0 += 16) {
+        const int nbr = min(16, nbh - b0), e0 = b0 * 256;
+        uint32_t hv[16];
+        if (!pd_poll<16>(a, a.rh, tag,
+                         [&](int k) {
+                           const int e = e0 + t + 256 * k;
+                           return k < nbr && e < ffn ? e : -1;
+                         },
+                         hv, misc, vit))
+          return false;
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          if (k < nbr) U[t + 256 * k] = __uint_as_float(hv[k]);
+        quant_round(b0, nbr);
+      }
     }
   }
 
