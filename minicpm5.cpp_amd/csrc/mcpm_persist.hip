@@ -32,10 +32,11 @@
 // once from the weight planes), in four regions: QKV, O, gate/up, down.  A
 // region is copied into LDS (direct-to-LDS loads, 1 KiB per wave
 // instruction) after its previous use, during the hand-off wait of a phase
-// before the one that reads it: O at Q, the next layer's QKV and gate/up at
-// O (at A on the work groups that combine attention chunks, which wait there
-// for the chunks' partials), down at G.  The wait ends with every copy
-// landed.
+// before the one that reads it: O at Q; the next layer's QKV, this layer's
+// gate/up and down at O (at A on the work groups that combine attention
+// chunks, which wait there for the chunks' partials).  The wait ends with
+// every copy landed.  The chunk owners' K and V rows go into the down region
+// at Q, the attention's staging.
 //
 // Every wait is bounded: past spin_limit, or once another work group has
 // given up, the work group sets the error word and returns.
@@ -571,10 +572,12 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // weight copies for later phases, issued while this phase waits for its
   // hand-off (the waves are idle then, and a copy stalls the wave issuing it
   // for most of its transfer): each region after its last use, before the
-  // wait of a phase ahead of its next.  Q: this layer's O; O: the next
-  // layer's QKV and this layer's gate/up, except on the kv heads' combining
-  // work groups (k = W-1), which take them at A, while they wait for the
-  // chunks' partials; G: this layer's down (the attention's staging is done).
+  // wait of a phase ahead of its next.  Q: this layer's O (and the chunk
+  // owners' attention rows, into the down region); O: the next layer's QKV,
+  // this layer's gate/up and down (the attention's staging is done), except
+  // on the kv heads' combining work groups (k = W-1), which take them at A,
+  // while they wait for the chunks' partials (down at G where they own a
+  // chunk, whose staging holds the down region until then).
   if (kind == 0) {
     pd_copy_region(a, LDS, l, 1);
     // this layer's attention chunk (the down region is free until G)
@@ -587,8 +590,11 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   if (kind == 2 && me.k != s.W - 1) {
     if (l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 0);
     pd_copy_region(a, LDS, l, 2);
+    pd_copy_region(a, LDS, l, 3);
   }
-  if (kind == 3) pd_copy_region(a, LDS, l, 3);
+  // the combining work group with a chunk of its own (its staging is the
+  // down region until its chunks are done)
+  if (kind == 3 && me.k == s.W - 1 && me.k <= pos / ATTN_CHUNK) pd_copy_region(a, LDS, l, 3);
 
   // hand-off and prologue: the Q8_K activations into the scratch
   if (kind == 0 || kind == 3) {
@@ -771,6 +777,7 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
   if (combiner) {
     if (l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 0);
     pd_copy_region(a, LDS, l, 2);
+    if (k >= nch) pd_copy_region(a, LDS, l, 3);  // no chunk staged in the down region
   }
   constexpr int HD = 64, GH = 256, OPT = ATTN_MAX_GROUP * HD / 256;
   const int group = s.group, kvd = s.kvd;
