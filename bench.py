@@ -342,6 +342,12 @@ def host_cpu():
             info["model"] = kv["Model name"]
         if kv.get("BIOS Model name"):
             info["bios_model"] = kv["BIOS Model name"]
+        # where the model name is generic (a virtual machine's "AMD EPYC"),
+        # the vendor, family, model and stepping still identify the part
+        for key, name in (("Vendor ID", "vendor"), ("CPU family", "family"), ("Model", "model_number"),
+                          ("Stepping", "stepping")):
+            if kv.get(key):
+                info[name] = kv[key]
         sockets = int(kv.get("Socket(s)", "0") or 0)
         per = int(kv.get("Core(s) per socket", "0") or 0)
         info["sockets"] = sockets or None
