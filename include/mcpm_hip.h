@@ -263,7 +263,9 @@ int mcpm_engine_set_graph(mcpm_engine *e, int enable);
  * per kv head, a CU count that is a multiple of 8, at most 2 attention chunks
  * of 64 positions per CU), every layer of a token runs in one persistent
  * launch, the per-token loop of MiniCPM5Engine::forward (src/model.cpp:171-226)
- * as one kernel; 0: five launches per layer.  Results are the same. */
+ * as one kernel; 0: five launches per layer.  Results are the same.  While
+ * it is on (and a KV cache is set up) the engine holds the launch's weight
+ * slab, the layer weights once more in the launch's layout; 0 frees it. */
 int mcpm_engine_set_persistent(mcpm_engine *e, int enable);
 /* 1 when the next token runs its layers in one launch. */
 int mcpm_engine_uses_persistent(const mcpm_engine *e);

@@ -678,9 +678,25 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
 // (built once per layout), hand-off records, launch count and arguments.
 // Leaves pd_ready false (the five-launch path) when the shape or the
 // context does not fit.
+// The persistent launch's large buffers (the weight slab: the model's layer
+// weights once more) are held only while the launch is asked for.
+void pd_release(mcpm_engine* e) {
+  for (void** p : {reinterpret_cast<void**>(&e->pd_slab), reinterpret_cast<void**>(&e->d_pd_layers),
+                   reinterpret_cast<void**>(&e->pd_rec)}) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+  }
+  e->pd_slab_stride = 0;
+  e->pd_ready = false;
+}
+
 int pd_setup(mcpm_engine* e) {
   e->pd_ready = false;
   const mcpm_model_config& c = e->cfg;
+  if (!e->pd_want) {
+    pd_release(e);
+    return MCPM_OK;
+  }
   if (!e->kc || c.n_layers <= 0) return MCPM_OK;
   const Layer& L0 = e->L[0];
   PdShape s{};
@@ -865,9 +881,10 @@ int mcpm_engine_set_graph(mcpm_engine* e, int enable) {
 int mcpm_engine_set_persistent(mcpm_engine* e, int enable) {
   if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_set_persistent: null engine");
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
-  e->pd_want = enable != 0;
   drop_graph(e);
-  return MCPM_OK;
+  if ((enable != 0) == e->pd_want && (e->pd_ready || !enable || !e->kc)) return MCPM_OK;
+  e->pd_want = enable != 0;
+  return pd_setup(e);  // builds the slab (with a KV cache) or releases it
 }
 
 int mcpm_engine_uses_persistent(const mcpm_engine* e) { return e && e->pd_ready && e->pd_want ? 1 : 0; }

@@ -147,3 +147,44 @@ def test_hand_off_give_up_then_recovers(engines, kv8_image):
         got, _ = a.forward(int(t), pos)
         om.forward(int(t), pos, want)
         assert_bits(got, want)
+
+
+# The 2.4B shape's own plan (hidden 2304, FFN 5760: 23 blocks of h, the
+# single-wait down prologue, staging in the down region) on 3 layers
+SHAPE24 = dict(n_layers=3, dim=2304, n_heads=32, n_kv_heads=8, head_dim=64, ffn=5760, vocab=4096)
+
+
+def test_2p4b_shape_vs_oracle_and_five_launch_path(ctx):
+    img = mcpm.synth_gguf(mcpm.make_config(**SHAPE24), seed=23, mix=0)
+    a = mcpm.Engine(ctx, image=img)
+    b = mcpm.Engine(ctx, image=img)
+    try:
+        a.set_persistent(True)
+        a.init_kv_cache(512)
+        b.init_kv_cache(512)
+        assert a.uses_persistent() and not b.uses_persistent()
+        om = O.OracleModel(img)
+        om.init_kv(512)
+        rng = np.random.default_rng(8)
+        toks = rng.integers(0, SHAPE24["vocab"], 40)
+        want = np.empty(SHAPE24["vocab"], np.float32)
+        for pos, t in enumerate(toks):
+            announce(f"2.4B-shaped persistent forward pos={pos}")
+            got, _ = a.forward(int(t), pos)
+            om.forward(int(t), pos, want)
+            assert_bits(got, want)
+        # past 192 positions (several chunks per head), sampled, against the
+        # five launches
+        prompt = rng.integers(0, SHAPE24["vocab"], 200).astype(np.int32)
+        announce("2.4B-shaped persistent vs five launches, 200-token prompt")
+        np.testing.assert_array_equal(a.generate_sampled(prompt, 96, 0.9, 0.95, 5),
+                                      b.generate_sampled(prompt, 96, 0.9, 0.95, 5))
+        # off frees the slab and runs the five launches; on builds it again
+        a.set_persistent(False)
+        assert not a.uses_persistent()
+        a.set_persistent(True)
+        assert a.uses_persistent()
+        np.testing.assert_array_equal(a.generate_greedy(prompt[:50], 32), b.generate_greedy(prompt[:50], 32))
+    finally:
+        a.free()
+        b.free()
