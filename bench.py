@@ -131,6 +131,28 @@ def kernel_breakdown(eng, n_tokens=8):
     return out
 
 
+def persistent_measure(eng, prompt, steps, warmup, default_tps):
+    """The same decode (prompt, warmup, then `steps` timed steps) through the
+    persistent launch (every layer of a token in one launch; off by default,
+    mcpm_engine_set_persistent), on the same engine and KV cache, graph
+    replay as the default launches; None where the shape does not fit it."""
+    eng.set_persistent(True)
+    try:
+        if not eng.uses_persistent():
+            return None
+        eng.generate_greedy(prompt, 1 + warmup)
+        eng.sync()
+        t0 = time.perf_counter()
+        eng.decode_steps(steps)
+        eng.sync()
+        dt = time.perf_counter() - t0
+        return {"tokens_per_s": round(steps / dt, 2), "ms_per_step": round(1e3 * dt / steps, 4),
+                "over_default_launches": round(steps / dt / default_tps, 4),
+                "launch": "one launch per token for every layer (one work group per CU), hipGraph per token"}
+    finally:
+        eng.set_persistent(False)
+
+
 def prefill_measure(eng, cfg, n_prompt=1024, reps=3):
     """The long-context configuration's prompt: n_prompt random token ids
     through the batched prefill (MFMA GEMMs).  Times the prefill of the first
@@ -419,6 +441,8 @@ def main():
     ap.add_argument("--mix", type=int, default=0, help="0: Q6_K v/down in every layer; 1: llama.cpp layers")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of a graph replay")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 1024-token prefill measurement")
+    ap.add_argument("--no-persistent", action="store_true",
+                    help="skip the same decode through the persistent launch (opt-in, off by default)")
     ap.add_argument("--no-sampled", action="store_true",
                     help="skip the sampled decode after a 1024-token prompt (device sampler)")
     ap.add_argument("--no-ops", action="store_true",
@@ -475,6 +499,13 @@ def main():
         log(f"  {k:8s} {v['avg_us']:8.2f} us x {v['launches_per_token']:.0f}/token "
             f"= {v['us_per_token']:8.1f} us/token  "
             f"{v['bytes_per_launch'] / (v['avg_us'] * 1e-6) / 1e9 if v['bytes_per_launch'] and v['avg_us'] else 0:7.1f} GB/s")
+
+    persistent = None
+    if not args.no_persistent and not args.eager:
+        persistent = persistent_measure(eng, prompt, args.steps, args.warmup, tps)
+        if persistent:
+            log(f"persistent launch, same decode: {persistent['tokens_per_s']:.1f} tok/s "
+                f"({persistent['over_default_launches']:.3f} of the default launches)")
 
     if args.copy_calibration_mb > 0:
         nbytes = args.copy_calibration_mb << 20
@@ -563,6 +594,7 @@ def main():
                      "timing": "eager launches of the class, HIP events around each kernel on the engine stream",
                      "rocprof": prof},
         "cpu_baseline": cpu,
+        "persistent_decode": persistent,
         "prefill": prefill,
         "sampled_decode": sampled,
         "ops": ops,
