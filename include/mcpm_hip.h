@@ -269,6 +269,13 @@ int mcpm_engine_set_graph(mcpm_engine *e, int enable);
 int mcpm_engine_set_persistent(mcpm_engine *e, int enable);
 /* 1 when the next token runs its layers in one launch. */
 int mcpm_engine_uses_persistent(const mcpm_engine *e);
+/* 1 when that launch also hands the records read on one XCD only (a kv
+ * head's q/k/v rows, its attention chunks' partials) through that XCD's L2:
+ * set up when every work group b runs on the XCD of work group b % 8
+ * (checked at set-up, and by each launch, which otherwise fails with
+ * MCPM_ERR_HIP); MCPM_PD_XCD_LOCAL=0 keeps every hand-off at agent scope.
+ * No counterpart in the reference. */
+int mcpm_engine_persistent_xcd_local(const mcpm_engine *e);
 /* The spin limit of the waits inside the engine's launches: the fused
  * kernels' grid barrier (MCPM_FUSED_FFN / MCPM_FUSED_ATTN) and the persistent
  * launch's hand-offs.  A wait that passes it gives up, every work group then

@@ -132,6 +132,7 @@ struct mcpm_engine {
   uint64_t* pd_rec = nullptr;
   unsigned* pd_sync = nullptr;  // [0] launch count, [64] error word
   float* pd_norms = nullptr;    // [L][2][dim] RMSNorm gains
+  int* pd_xcc = nullptr;        // [G] the XCD of each work group at set-up
   PdArgs pd_args{};
 };
 
@@ -188,7 +189,7 @@ void free_engine(mcpm_engine* e) {
                   e->d_sample, static_cast<void*>(e->gsync), static_cast<void*>(e->d_draws),
                   static_cast<void*>(e->att_q8), static_cast<void*>(e->attn_err), static_cast<void*>(e->d_pd_layers),
                   static_cast<void*>(e->pd_slab), static_cast<void*>(e->pd_rec), static_cast<void*>(e->pd_sync),
-                  static_cast<void*>(e->pd_norms)})
+                  static_cast<void*>(e->pd_norms), static_cast<void*>(e->pd_xcc)})
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
   free_prefill(e->pf);
@@ -403,6 +404,10 @@ int check_grid_sync(mcpm_engine* e) {
       MCPM_HIP(hipMemsetAsync(e->pd_sync, 0, 128 * sizeof(unsigned), s));
       MCPM_HIP(hipMemcpyAsync(e->pd_sync, init, sizeof init, hipMemcpyHostToDevice, s));
       MCPM_HIP(hipStreamSynchronize(s));
+      if (perr == 2u)
+        return fail(MCPM_ERR_HIP,
+                    "the persistent decode launch ran a work group on another XCD than at set-up; results of the call "
+                    "are invalid (MCPM_PD_XCD_LOCAL=0 keeps every hand-off at agent scope)");
       return fail(MCPM_ERR_HIP, "the persistent decode launch gave up waiting (spin limit); results of the call are invalid");
     }
   }
@@ -682,7 +687,7 @@ int prefill_pass(mcpm_engine* e, const int* tokens, int n, int pos0) {
 // weights once more) are held only while the launch is asked for.
 void pd_release(mcpm_engine* e) {
   for (void** p : {reinterpret_cast<void**>(&e->pd_slab), reinterpret_cast<void**>(&e->d_pd_layers),
-                   reinterpret_cast<void**>(&e->pd_rec)}) {
+                   reinterpret_cast<void**>(&e->pd_rec), reinterpret_cast<void**>(&e->pd_xcc)}) {
     if (*p) (void)hipFree(*p);
     *p = nullptr;
   }
@@ -732,8 +737,11 @@ int pd_setup(mcpm_engine* e) {
     e->pd_slab_stride = s.slab_stride;
   }
   if (e->pd_rec) (void)hipFree(e->pd_rec);
+  if (e->pd_xcc) (void)hipFree(e->pd_xcc);
   e->pd_rec = nullptr;
+  e->pd_xcc = nullptr;
   int rc = alloc_dev(reinterpret_cast<void**>(&e->pd_rec), pd_records(s) * sizeof(uint64_t));
+  if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->pd_xcc), static_cast<size_t>(s.G) * sizeof(int));
   if (!rc && !e->pd_sync) rc = alloc_dev(reinterpret_cast<void**>(&e->pd_sync), 128 * sizeof(unsigned));
   if (!rc && !e->pd_norms)
     rc = alloc_dev(reinterpret_cast<void**>(&e->pd_norms), static_cast<size_t>(c.n_layers) * 2 * c.dim * sizeof(float));
@@ -743,6 +751,13 @@ int pd_setup(mcpm_engine* e) {
     MCPM_HIP(hipMemcpyAsync(dst, e->L[l].attn_norm, c.dim * sizeof(float), hipMemcpyDeviceToDevice, st));
     MCPM_HIP(hipMemcpyAsync(dst + c.dim, e->L[l].ffn_norm, c.dim * sizeof(float), hipMemcpyDeviceToDevice, st));
   }
+  // XCD-local records (workgroup-scope stores read from the XCD's L2) need
+  // every work group b on the XCD of b % 8; MCPM_PD_XCD_LOCAL=0 keeps every
+  // record at agent scope
+  bool same_xcd = false;
+  MCPM_HIP(pd_probe_xcd(s.G, e->pd_xcc, st, same_xcd));
+  const char* xv = std::getenv("MCPM_PD_XCD_LOCAL");
+  const bool xcd_local = same_xcd && !(xv && std::atoi(xv) == 0);
   const unsigned init[2] = {1u, 0u};  // launch count 1: no record (all zero) carries a tag
   MCPM_HIP(hipMemsetAsync(e->pd_sync, 0, 128 * sizeof(unsigned), st));
   MCPM_HIP(hipMemcpyAsync(e->pd_sync, init, sizeof(unsigned), hipMemcpyHostToDevice, st));
@@ -762,6 +777,8 @@ int pd_setup(mcpm_engine* e) {
   a.err = e->pd_sync + 64;
   a.spin_limit = pd_spin_limit(e);
   a.x_out = e->x;
+  a.xcd_local = xcd_local ? 1 : 0;
+  a.xcc = e->pd_xcc;
   e->pd_args = a;
   e->pd = s;
   e->pd_ready = true;
@@ -888,6 +905,10 @@ int mcpm_engine_set_persistent(mcpm_engine* e, int enable) {
 }
 
 int mcpm_engine_uses_persistent(const mcpm_engine* e) { return e && e->pd_ready && e->pd_want ? 1 : 0; }
+
+int mcpm_engine_persistent_xcd_local(const mcpm_engine* e) {
+  return mcpm_engine_uses_persistent(e) && e->pd_args.xcd_local ? 1 : 0;
+}
 
 int mcpm_engine_set_spin_limit(mcpm_engine* e, unsigned limit) {
   if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_set_spin_limit: null engine");

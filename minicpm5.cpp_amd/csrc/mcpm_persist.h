@@ -29,6 +29,7 @@ constexpr int PD_NBX = 16;     // largest dim / 256
 constexpr int PD_NBH = 32;     // largest ffn_pad / 256
 constexpr int PD_NBQ = 9;      // largest n_heads * head_dim / 256
 constexpr int PD_REC_BLK = 85; // records of one Q8_K block: d, 64 code dwords, 16 bsums, 4 bsum-pair words
+constexpr int PD_REC_LINE = 16;  // records per 128-byte cache line
 constexpr int PD_ATTN_LDS = ((ATTN_CHUNK * 68 + ATTN_CHUNK * 64 + 8 * 64 + 8 * ATTN_CHUNK) * 4 + 64 * 8 + 15) & ~15;
 
 struct PdShape {
@@ -48,6 +49,7 @@ struct PdShape {
   int lds_bytes;
   int slab_stride;  // bytes per (layer, work group)
   int max_chunks;   // attention partial records per kv head
+  int part_stride;  // record slots per chunk of partials: gh + 2*group in whole lines
 };
 
 // Per-layer pointers: norms and the weight planes (the slab builder's source).
@@ -75,12 +77,19 @@ struct PdArgs {
   uint64_t* rx2;   // [dim]   x after the O projection
   uint64_t* rh;    // [ffn]   SwiGLU output
   uint64_t* rqkv;  // [nkv][gh + 2*hd]  q of the head group, K and V rows at pos
-  uint64_t* rpart; // [nkv][max_chunks][gh + 2*group]  chunk partials o_c, m_c, z_c
+  uint64_t* rpart; // [nkv][max_chunks][part_stride]  chunk partials o_c, m_c, z_c
   uint64_t* ratt;  // [nbq][PD_REC_BLK]  attention output as Q8_K blocks
   unsigned* epoch; // launch counter (tags), advanced by each launch
   unsigned* err;   // set when a wait passed spin_limit
   unsigned spin_limit;
   float* x_out;    // x after the last layer (plain stores, for the LM head)
+  // 1 when every work group b runs on the XCD of work group b % 8 (checked
+  // at set-up, and by each launch against xcc): the records read only on
+  // their writer's XCD (a kv head's q/k/v rows, its chunks' partials) are
+  // stored at workgroup scope and stay in that XCD's L2, where the readers'
+  // agent-scope loads find them; 0: every record at agent scope
+  int xcd_local;
+  const int* xcc;  // [G] the XCD each work group ran on at set-up
 };
 
 // Rows of work group b.
@@ -196,10 +205,14 @@ bool pd_plan(const mcpm_model_config& c, int n_cu, int max_seq, int tq, int tk, 
              PdShape& s, const char** why);
 // Copies every layer's weights into the slab layout (device gather).
 hipError_t launch_build_slab(const PdShape& s, const PdLayer* d_layers, uint8_t* slab, hipStream_t st);
-// Record buffer sizes (records) for the shape.
+// Record buffer sizes (records) for the shape, every array starting on a
+// cache line.
 size_t pd_records(const PdShape& s);
 // Points the record arrays of a at one allocation of pd_records(s) records.
 void pd_bind_records(PdArgs& a, uint64_t* base);
+// Writes the XCD that work group b of a G-wide launch runs on to xcc[b];
+// same = every b on the XCD of b % 8.
+hipError_t pd_probe_xcd(int G, int* xcc, hipStream_t st, bool& same);
 // The launch's LDS attribute and the check that one work group fits a CU
 // (outside any graph capture); then the launch.
 hipError_t prepare_decode_persist(const PdShape& s);

@@ -43,6 +43,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <vector>
 
 #include "mcpm_attn.h"
 #include "mcpm_device.h"
@@ -64,6 +65,18 @@ __device__ __forceinline__ void rec_st(uint64_t* p, uint32_t v, uint32_t tag) {
   __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void rec_stf(uint64_t* p, float v, uint32_t tag) { rec_st(p, __float_as_uint(v), tag); }
+// A record read only on its writer's XCD (a kv head's q/k/v rows, its
+// chunks' partials): in the XCD-local instance (XL) a workgroup-scope
+// store, which leaves it in that XCD's L2 (the vector L1 writes through),
+// where the readers' agent-scope loads find it; else an agent-scope store.
+// The scope is a template parameter: a run-time choice costs code in a
+// kernel whose loop fills the instruction cache.
+template <bool XL>
+__device__ __forceinline__ void rec_stf_xcd(uint64_t* p, float v, uint32_t tag) {
+  const uint64_t r = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
+  if constexpr (XL) __hip_atomic_store(p, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else __hip_atomic_store(p, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ unsigned ld_u32c(const unsigned* p) {
   return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -513,6 +526,7 @@ __device__ __forceinline__ void pd_copy_region(const PdArgs& a, uint8_t* LDS, in
 }
 
 // Q (kind 0), O (2), G (3) or D (4) of layer l.
+template <bool XL>
 __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_t* LDS, uint32_t* S, uint32_t tag,
                                         int pos, uint32_t& vit) {
   const PdShape& s = a.s;
@@ -710,15 +724,15 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
         if ((i & 1) == 0) o = v * cs.x - partner * cs.y;
         else o = partner * cs.y + v * cs.x;
         if (t < s.nq) {
-          rec_stf(qrec + (r - me.kvh * s.gh), o, tag);
+          rec_stf_xcd<XL>(qrec + (r - me.kvh * s.gh), o, tag);
         } else {
           a.kc[row_off + r] = o;
-          rec_stf(qrec + s.gh + (r - me.kvh * s.hd), o, tag);
+          rec_stf_xcd<XL>(qrec + s.gh + (r - me.kvh * s.hd), o, tag);
         }
       } else {
         const int r = me.kr0 + (t - s.nq - s.nk);
         a.vc[row_off + r] = v;
-        rec_stf(qrec + s.gh + s.hd + (r - me.kvh * s.hd), v, tag);
+        rec_stf_xcd<XL>(qrec + s.gh + s.hd + (r - me.kvh * s.hd), v, tag);
       }
     }
   } else if (kind == 2) {
@@ -765,6 +779,7 @@ __device__ __forceinline__ void pd_fill_last(AttnRegs<4>& R, const float* kr, co
 // wait idle for the partials, so it takes its weight copies for the next
 // phases here (the next layer's QKV, this layer's gate/up), and every other
 // work group its own at O.
+template <bool XL>
 __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LDS, uint32_t* S, uint32_t tag, int T,
                                              uint32_t& vit) {
   const PdShape& s = a.s;
@@ -835,7 +850,7 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
     }
     pd_bar();  // (m_c, z_c) of every head, every chunk's o_c
   }
-  const int ppc = GH + 2 * group;
+  const int ppc = s.part_stride;  // o_c (GH), m_c (group), z_c (group), in whole lines
   uint64_t* part = a.rpart + static_cast<size_t>(h) * s.max_chunks * ppc;
   if (!combiner) {
 #pragma unroll 1
@@ -843,11 +858,11 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
       const int c = k + W * cc;
       if (c >= nch) break;
       uint64_t* pr = part + static_cast<size_t>(c) * ppc;
-      rec_stf(pr + t, sO[cc * GH + t], tag);
+      rec_stf_xcd<XL>(pr + t, sO[cc * GH + t], tag);
       if (t < group) {
         const float2 mz = A.sMZ[cc * ATTN_MAX_GROUP + t];
-        rec_stf(pr + GH + t, mz.x, tag);
-        rec_stf(pr + GH + group + t, mz.y, tag);
+        rec_stf_xcd<XL>(pr + GH + t, mz.x, tag);
+        rec_stf_xcd<XL>(pr + GH + group + t, mz.y, tag);
       }
     }
     return true;
@@ -964,6 +979,7 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
 
 // One launch per token: every layer, from the embedding to the last layer's
 // x (x_out).
+template <bool XL>
 __global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t LDS[];
   uint32_t* S = reinterpret_cast<uint32_t*>(LDS + a.s.scr_off);
@@ -972,8 +988,15 @@ __global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
   if (t == 0) {
     misc[0] = 0u;
     misc[1] = ld_u32c(a.epoch);
+    // the XCD (XCC_ID register, bits 3:0) must be the one seen at set-up,
+    // where this work group's XCD-local records are read
+    if (XL && static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u) != a.xcc[blockIdx.x]) {
+      misc[0] = 1u;
+      st_u32c(a.err, 2u);
+    }
   }
   pd_bar();
+  if (misc[0]) return;
   const uint32_t ep = misc[1];
   const int pos = a.state[1], T = pos + 1, L = a.s.L;
   const uint32_t tag0 = ep * static_cast<uint32_t>(L + 1) + 1u;
@@ -995,7 +1018,8 @@ __global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
   for (int ph = 0; ph < 5 * L; ++ph) {
     const int l = ph / 5, kind = ph - 5 * l;
     const uint32_t tag = tag0 + static_cast<uint32_t>(l);
-    const bool ok = kind == 1 ? pd_attention(a, l, LDS, S, tag, T, vit) : pd_gemv(a, l, kind, LDS, S, tag, pos, vit);
+    const bool ok =
+        kind == 1 ? pd_attention<XL>(a, l, LDS, S, tag, T, vit) : pd_gemv<XL>(a, l, kind, LDS, S, tag, pos, vit);
     if (!ok) return;
   }
   // every work group read the launch count before its first hand-off, and
@@ -1067,6 +1091,7 @@ bool pd_plan(const mcpm_model_config& c, int n_cu, int max_seq, int tq, int tk, 
   for (int ty : {tv, to, td})
     if (ty != MCPM_TYPE_Q4_K && ty != MCPM_TYPE_Q6_K) return no("weight type without a kernel");
   s.max_chunks = (max_seq + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  s.part_stride = (s.gh + 2 * s.group + PD_REC_LINE - 1) / PD_REC_LINE * PD_REC_LINE;
   if (s.max_chunks > 2 * s.W) return no("context longer than two chunks per work group");
   s.nq = s.gh / s.W;
   s.nk = s.hd / s.W;
@@ -1122,19 +1147,52 @@ bool pd_plan(const mcpm_model_config& c, int n_cu, int max_seq, int tq, int tk, 
   return true;
 }
 
+namespace {
+// Record counts of the arrays rx, rx2, rh, rqkv, rpart, ratt, each rounded
+// to whole cache lines, so that the blocks stored at workgroup scope (a kv
+// head's q/k/v rows, a chunk's partials) share no line with another XCD's.
+void pd_record_arrays(const PdShape& s, size_t (&n)[6]) {
+  const size_t v[6] = {static_cast<size_t>(s.dim), static_cast<size_t>(s.dim), static_cast<size_t>(s.ffn),
+                       static_cast<size_t>(s.nkv) * (s.gh + 2 * s.hd),
+                       static_cast<size_t>(s.nkv) * s.max_chunks * s.part_stride,
+                       static_cast<size_t>(s.nbq) * PD_REC_BLK};
+  for (int i = 0; i < 6; ++i) n[i] = (v[i] + PD_REC_LINE - 1) / PD_REC_LINE * PD_REC_LINE;
+}
+
+__global__ void k_xcd_probe(int* xcc) {
+  if (threadIdx.x == 0) xcc[blockIdx.x] = static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);
+}
+}  // namespace
+
 size_t pd_records(const PdShape& s) {
-  return 2 * static_cast<size_t>(s.dim) + s.ffn + static_cast<size_t>(s.nkv) * (s.gh + 2 * s.hd) +
-         static_cast<size_t>(s.nkv) * s.max_chunks * (s.gh + 2 * s.group) + static_cast<size_t>(s.nbq) * PD_REC_BLK;
+  size_t n[6], tot = 0;
+  pd_record_arrays(s, n);
+  for (size_t v : n) tot += v;
+  return tot;
 }
 
 void pd_bind_records(PdArgs& a, uint64_t* base) {
-  const PdShape& s = a.s;
-  a.rx = base;
-  a.rx2 = a.rx + s.dim;
-  a.rh = a.rx2 + s.dim;
-  a.rqkv = a.rh + s.ffn;
-  a.rpart = a.rqkv + static_cast<size_t>(s.nkv) * (s.gh + 2 * s.hd);
-  a.ratt = a.rpart + static_cast<size_t>(s.nkv) * s.max_chunks * (s.gh + 2 * s.group);
+  size_t n[6];
+  pd_record_arrays(a.s, n);
+  uint64_t** arr[6] = {&a.rx, &a.rx2, &a.rh, &a.rqkv, &a.rpart, &a.ratt};
+  for (int i = 0; i < 6; ++i) {
+    *arr[i] = base;
+    base += n[i];
+  }
+}
+
+hipError_t pd_probe_xcd(int G, int* xcc, hipStream_t st, bool& same) {
+  same = false;
+  hipLaunchKernelGGL(k_xcd_probe, dim3(G), dim3(256), 0, st, xcc);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  std::vector<int> h(G);
+  e = hipMemcpyAsync(h.data(), xcc, G * sizeof(int), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return e;
+  same = true;
+  for (int b = 0; b < G; ++b) same = same && h[b] == h[b % PD_XCDS];
+  return hipSuccess;
 }
 
 hipError_t launch_build_slab(const PdShape& s, const PdLayer* d_layers, uint8_t* slab, hipStream_t st) {
@@ -1144,20 +1202,23 @@ hipError_t launch_build_slab(const PdShape& s, const PdLayer* d_layers, uint8_t*
 }
 
 hipError_t prepare_decode_persist(const PdShape& s) {
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_decode_persist),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, s.lds_bytes);
-  if (e != hipSuccess) return e;
-  // every work group must be resident at once: at least one per CU
-  int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_decode_persist), 256,
-                                                   s.lds_bytes) != hipSuccess ||
-      occ < 1)
-    return hipErrorNotSupported;
+  for (const void* k : {reinterpret_cast<const void*>(k_decode_persist<false>),
+                        reinterpret_cast<const void*>(k_decode_persist<true>)}) {
+    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, s.lds_bytes);
+    if (e != hipSuccess) return e;
+    // every work group must be resident at once: at least one per CU
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, 256, s.lds_bytes) != hipSuccess || occ < 1)
+      return hipErrorNotSupported;
+  }
   return hipSuccess;
 }
 
 hipError_t launch_decode_persist(const PdArgs& a, hipStream_t st) {
-  launch_kernel(k_decode_persist, dim3(a.s.G), dim3(256), static_cast<size_t>(a.s.lds_bytes), st, a);
+  if (a.xcd_local)
+    launch_kernel(k_decode_persist<true>, dim3(a.s.G), dim3(256), static_cast<size_t>(a.s.lds_bytes), st, a);
+  else
+    launch_kernel(k_decode_persist<false>, dim3(a.s.G), dim3(256), static_cast<size_t>(a.s.lds_bytes), st, a);
   return hipGetLastError();
 }
 

@@ -125,6 +125,7 @@ _SIGS = {
     "mcpm_engine_set_graph": (_I, [_P, _I]),
     "mcpm_engine_set_persistent": (_I, [_P, _I]),
     "mcpm_engine_uses_persistent": (_I, [_P]),
+    "mcpm_engine_persistent_xcd_local": (_I, [_P]),
     "mcpm_engine_set_spin_limit": (_I, [_P, C.c_uint]),
     "mcpm_set_op_timing": (_I, [_P, _I]),
     "mcpm_op_time": (_I, [_P, C.POINTER(C.c_double), C.POINTER(_I64)]),
@@ -396,6 +397,9 @@ class Engine:
 
     def uses_persistent(self) -> bool:
         return bool(self.lib.mcpm_engine_uses_persistent(self.h))
+
+    def persistent_xcd_local(self) -> bool:
+        return bool(self.lib.mcpm_engine_persistent_xcd_local(self.h))
 
     def set_spin_limit(self, limit: int):
         check(self.lib.mcpm_engine_set_spin_limit(self.h, int(limit)))

@@ -8,7 +8,8 @@
 //    plane, and every byte the kernel's lane-sum tasks read maps back to the
 //    (row, block, chunk) of the weight it expects;
 //  - the hand-offs: the row ranges of the work groups cover each consumer's
-//    records exactly once;
+//    records exactly once, every record array starts on a cache line, and
+//    the blocks stored at workgroup scope fill whole lines;
 //  - shapes the kernel does not take are refused.
 // Prints one line per shape; exit status 0 when every check holds.
 #include <cstdio>
@@ -99,6 +100,26 @@ static void check_shape(const char* name, const mcpm_model_config& c, int n_cu, 
       qx[me.kvh * (s.gh + 2 * s.hd) + s.gh + (me.kr0 + i - me.kvh * s.hd)]++;
       qx[me.kvh * (s.gh + 2 * s.hd) + s.gh + s.hd + (me.kr0 + i - me.kvh * s.hd)]++;
     }
+  }
+  // records: every array on a cache line, in order, inside the allocation;
+  // the blocks stored at workgroup scope (a kv head's q/k/v rows, a chunk's
+  // partials) in whole lines, so no line holds two XCDs' blocks
+  {
+    std::vector<uint64_t> rec(pd_records(s));
+    PdArgs a{};
+    a.s = s;
+    pd_bind_records(a, rec.data());
+    const uint64_t* arr[6] = {a.rx, a.rx2, a.rh, a.rqkv, a.rpart, a.ratt};
+    const size_t need[6] = {size_t(c.dim), size_t(c.dim), size_t(c.ffn), size_t(s.nkv) * (s.gh + 2 * s.hd),
+                            size_t(s.nkv) * s.max_chunks * s.part_stride, size_t(s.nbq) * PD_REC_BLK};
+    for (int i = 0; i < 6; ++i) {
+      const size_t off = static_cast<size_t>(arr[i] - rec.data());
+      const size_t end = i + 1 < 6 ? static_cast<size_t>(arr[i + 1] - rec.data()) : rec.size();
+      CHECK(off % PD_REC_LINE == 0 && end >= off + need[i], "%s: record array %d", name, i);
+    }
+    CHECK((s.gh + 2 * s.hd) % PD_REC_LINE == 0 && s.part_stride % PD_REC_LINE == 0 &&
+              s.part_stride >= s.gh + 2 * s.group,
+          "%s: workgroup-scope record blocks in whole lines", name);
   }
   for (int v : hx) CHECK(v == 1, "%s: rows of x", name);
   for (int v : fx) CHECK(v == 1, "%s: FFN pairs", name);

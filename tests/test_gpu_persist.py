@@ -41,6 +41,9 @@ def test_off_by_default_and_taken_when_asked(ctx, kv8_image, engines):
     b.init_kv_cache(256)
     assert a.uses_persistent(), "the 8-kv-head model fits the persistent launch on a 256-CU device"
     assert not b.uses_persistent()
+    # work group b on the XCD of b % 8 (the device dispatches work groups
+    # round-robin over its 8 XCDs): the XCD-local records are taken
+    assert a.persistent_xcd_local()
 
 
 def test_logits_bit_exact_vs_oracle(engines, kv8_image):
@@ -74,6 +77,27 @@ def test_generation_matches_five_launch_path(engines, graph):
     np.testing.assert_array_equal(outs[0][0], outs[1][0])
     np.testing.assert_array_equal(outs[0][1], outs[1][1])
     assert len(set(outs[0][1].tolist())) > 8, "a near-constant token sequence pins little"
+
+
+def test_agent_scope_hand_offs_match(ctx, kv8_image, engines, monkeypatch):
+    """MCPM_PD_XCD_LOCAL=0: every record at agent scope; the same tokens as
+    the five-launch path."""
+    _, b = engines
+    monkeypatch.setenv("MCPM_PD_XCD_LOCAL", "0")
+    e = mcpm.Engine(ctx, image=kv8_image)
+    try:
+        e.set_persistent(True)
+        e.init_kv_cache(512)
+        assert e.uses_persistent() and not e.persistent_xcd_local()
+        prompt = np.arange(5, 21, dtype=np.int32)
+        b.init_kv_cache(512)
+        announce("greedy and sampled, agent-scope hand-offs")
+        got = (e.generate_greedy(prompt, 150), e.generate_sampled(prompt, 150, 0.9, 0.95, 33))
+        want = (b.generate_greedy(prompt, 150), b.generate_sampled(prompt, 150, 0.9, 0.95, 33))
+    finally:
+        e.free()
+    np.testing.assert_array_equal(got[0], want[0])
+    np.testing.assert_array_equal(got[1], want[1])
 
 
 def test_long_context_two_chunks_per_work_group(engines):
@@ -163,6 +187,7 @@ def test_2p4b_shape_vs_oracle_and_five_launch_path(ctx):
         a.init_kv_cache(512)
         b.init_kv_cache(512)
         assert a.uses_persistent() and not b.uses_persistent()
+        assert a.persistent_xcd_local()
         om = O.OracleModel(img)
         om.init_kv(512)
         rng = np.random.default_rng(8)
