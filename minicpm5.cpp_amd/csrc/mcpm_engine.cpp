@@ -90,11 +90,22 @@ struct mcpm_engine {
   int attn_q8k_chunks = ATTN_Q8K_CHUNKS;  // up to this many chunks (MCPM_ATTN_Q8K=n: n)
   BlockQ8K* att_q8 = nullptr;
   unsigned* attn_err = nullptr;
+  // contexts of one chunk (at most 64 positions): the O projection's
+  // work groups form the attention themselves (PRO_ATTN_ONE: each XCD's work
+  // groups split the heads and share them through tagged records in that
+  // XCD's L2), with no attention launch.  Needs head_dim 64, 4 query heads
+  // per kv head, at most 2048 query dims, work group b on the XCD of b % 8
+  // (checked at set-up) and enough O work groups per XCD; MCPM_ATTN_IN_O=0
+  // turns it off.
+  bool attn_in_o = false;
+  uint64_t* xo_rec = nullptr;  // [8][heads * 64] records of each XCD
+  unsigned* xo_words = nullptr;  // [0] token epoch, [64] error word, [128..135] XCD of work groups b % 8
   // graph
   bool use_graph = true;
   // [greedy (argmax at the end), sampled][longer contexts, contexts the
-  // per-kv-head attention covers]
-  hipGraphExec_t graph[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+  // per-kv-head attention covers, one-chunk contexts with the attention in
+  // the O projection]
+  hipGraphExec_t graph[2][3] = {{nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr}};
   // timing
   int timing_class = -1;
   std::vector<TimedPair> events;
@@ -189,7 +200,8 @@ void free_engine(mcpm_engine* e) {
                   e->d_sample, static_cast<void*>(e->gsync), static_cast<void*>(e->d_draws),
                   static_cast<void*>(e->att_q8), static_cast<void*>(e->attn_err), static_cast<void*>(e->d_pd_layers),
                   static_cast<void*>(e->pd_slab), static_cast<void*>(e->pd_rec), static_cast<void*>(e->pd_sync),
-                  static_cast<void*>(e->pd_norms), static_cast<void*>(e->pd_xcc)})
+                  static_cast<void*>(e->pd_norms), static_cast<void*>(e->pd_xcc), static_cast<void*>(e->xo_rec),
+                  static_cast<void*>(e->xo_words)})
     if (p) (void)hipFree(p);
   if (e->h_st) (void)hipHostFree(e->h_st);
   free_prefill(e->pf);
@@ -312,6 +324,33 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
     if (e->attn_q8k) rc = alloc_dev(reinterpret_cast<void**>(&e->att_q8), (qd / QK_K) * sizeof(BlockQ8K));
     if (!rc && e->attn_q8k) rc = alloc_dev(reinterpret_cast<void**>(&e->attn_err), sizeof(unsigned));
   }
+  if (!rc && c.head_dim == 64 && c.n_heads == 4 * c.n_kv_heads && qd / QK_K <= 8 && qd % QK_K == 0 &&
+      c.n_layers > 0) {
+    const char* v = std::getenv("MCPM_ATTN_IN_O");
+    GemvArgs o{};
+    o.reg[0] = GemvRegion{view_of(e->L[0].wo), nullptr, 0, c.dim};
+    o.nreg = 1;
+    o.total_rows = c.dim;
+    o.nb = qd / QK_K;
+    bool same_types = true;
+    for (const Layer& y : e->L) same_types = same_types && y.wo.type == e->L[0].wo.type;
+    if ((!v || std::atoi(v) != 0) && same_types && gemv_attn_one_hpw(o, ctx->n_cu) > 0) {
+      rc = alloc_dev(reinterpret_cast<void**>(&e->xo_words), 192 * sizeof(unsigned));
+      if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&e->xo_rec), static_cast<size_t>(8) * qd * sizeof(uint64_t));
+      int* probe = nullptr;
+      if (!rc) rc = alloc_dev(reinterpret_cast<void**>(&probe), 256 * sizeof(int));
+      bool same = false;
+      if (!rc && pd_probe_xcd(256, probe, ctx->stream, same) != hipSuccess) rc = MCPM_ERR_HIP;
+      if (!rc && same) {
+        rc = hipMemcpyAsync(e->xo_words + 128, probe, 8 * sizeof(int), hipMemcpyDeviceToDevice, ctx->stream) ==
+                     hipSuccess && hipStreamSynchronize(ctx->stream) == hipSuccess
+                 ? MCPM_OK
+                 : MCPM_ERR_HIP;
+        e->attn_in_o = !rc;
+      }
+      if (probe) (void)hipFree(probe);
+    }
+  }
   if (rc) {
     free_engine(e);
     return rc;
@@ -382,6 +421,25 @@ unsigned pd_spin_limit(const mcpm_engine* e) { return e->spin_limit ? e->spin_li
 
 int check_grid_sync(mcpm_engine* e) {
   hipStream_t s = e->ctx->stream;
+  // every error source is read and reset before the first one is reported,
+  // so that the next call starts clean whichever waits gave up
+  const char* msg = nullptr;
+  auto note = [&](const char* m) {
+    if (!msg) msg = m;
+  };
+  if (e->attn_in_o) {
+    unsigned xerr = 0;
+    MCPM_HIP(hipMemcpyAsync(&xerr, e->xo_words + 64, sizeof xerr, hipMemcpyDeviceToHost, s));
+    MCPM_HIP(hipStreamSynchronize(s));
+    if (xerr) {
+      // the epoch advances every token, so no record of the abandoned
+      // launches carries a later tag
+      MCPM_HIP(hipMemsetAsync(e->xo_words + 64, 0, sizeof(unsigned), s));
+      MCPM_HIP(hipStreamSynchronize(s));
+      note("the O projection's attention hand-off gave up waiting (spin limit, or a work group on another XCD); "
+           "results of the call are invalid (MCPM_ATTN_IN_O=0 runs the attention as its own launch)");
+    }
+  }
   if (e->attn_q8k) {
     unsigned aerr = 0;
     MCPM_HIP(hipMemcpyAsync(&aerr, e->attn_err, sizeof aerr, hipMemcpyDeviceToHost, s));
@@ -389,7 +447,7 @@ int check_grid_sync(mcpm_engine* e) {
     if (aerr) {
       MCPM_HIP(hipMemsetAsync(e->attn_err, 0, sizeof(unsigned), s));
       MCPM_HIP(hipStreamSynchronize(s));
-      return fail(MCPM_ERR_HIP, "the per-kv-head attention ran past its context limit; results of the call are invalid");
+      note("the per-kv-head attention ran past its context limit; results of the call are invalid");
     }
   }
   if (e->pd_ready) {
@@ -404,37 +462,40 @@ int check_grid_sync(mcpm_engine* e) {
       MCPM_HIP(hipMemsetAsync(e->pd_sync, 0, 128 * sizeof(unsigned), s));
       MCPM_HIP(hipMemcpyAsync(e->pd_sync, init, sizeof init, hipMemcpyHostToDevice, s));
       MCPM_HIP(hipStreamSynchronize(s));
-      if (perr == 2u)
-        return fail(MCPM_ERR_HIP,
-                    "the persistent decode launch ran a work group on another XCD than at set-up; results of the call "
-                    "are invalid (MCPM_PD_XCD_LOCAL=0 keeps every hand-off at agent scope)");
-      return fail(MCPM_ERR_HIP, "the persistent decode launch gave up waiting (spin limit); results of the call are invalid");
+      note(perr == 2u ? "the persistent decode launch ran a work group on another XCD than at set-up; results of "
+                        "the call are invalid (MCPM_PD_XCD_LOCAL=0 keeps every hand-off at agent scope)"
+                      : "the persistent decode launch gave up waiting (spin limit); results of the call are invalid");
     }
   }
-  if (!e->fused_ffn && !e->fused_attn) return MCPM_OK;
-  unsigned err = 0;
-  MCPM_HIP(hipMemcpyAsync(&err, e->gsync + 8 * 64 + 64, sizeof err, hipMemcpyDeviceToHost, s));
-  MCPM_HIP(hipStreamSynchronize(s));
-  if (!err) return MCPM_OK;
-  MCPM_HIP(hipMemsetAsync(e->gsync, 0, GRID_SYNC_WORDS * sizeof(unsigned), s));
-  MCPM_HIP(hipStreamSynchronize(s));
-  return fail(MCPM_ERR_HIP, "a fused kernel's grid barrier timed out; results of the call are invalid");
+  if (e->fused_ffn || e->fused_attn) {
+    unsigned err = 0;
+    MCPM_HIP(hipMemcpyAsync(&err, e->gsync + 8 * 64 + 64, sizeof err, hipMemcpyDeviceToHost, s));
+    MCPM_HIP(hipStreamSynchronize(s));
+    if (err) {
+      MCPM_HIP(hipMemsetAsync(e->gsync, 0, GRID_SYNC_WORDS * sizeof(unsigned), s));
+      MCPM_HIP(hipStreamSynchronize(s));
+      note("a fused kernel's grid barrier timed out; results of the call are invalid");
+    }
+  }
+  return msg ? fail(MCPM_ERR_HIP, msg) : MCPM_OK;
 }
 
 // All kernels of one token, reading token and pos from e->st.  short_ctx:
-// the context (pos + 1) has at most ATTN_Q8K_MAX_CHUNKS chunks.
-int enqueue_token(mcpm_engine* e, bool short_ctx) {
+// the context (pos + 1) has at most ATTN_Q8K_MAX_CHUNKS chunks; one_chunk:
+// at most one chunk, and the O projection forms the attention (attn_in_o).
+int enqueue_token(mcpm_engine* e, bool short_ctx, bool one_chunk) {
   const mcpm_model_config& c = e->cfg;
   hipStream_t s = e->ctx->stream;
   const int n_cu = e->ctx->n_cu;
   const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
   const int* st = reinterpret_cast<const int*>(e->st);
-  const bool q8k = short_ctx && e->attn_q8k && !e->fused_attn;
+  const bool in_o = one_chunk && e->attn_in_o && !e->fused_attn;
+  const bool q8k = short_ctx && e->attn_q8k && !e->fused_attn && !in_o;
   const bool persist = e->pd_ready && e->pd_want;
   if (persist)
     MCPM_HIP(timed(e, MCPM_KC_LAYERS, [&] { return launch_decode_persist(e->pd_args, s); }));
   else
-    MCPM_HIP(launch_embedding(view_of(e->embd), st, c.dim, e->x, s));
+    MCPM_HIP(launch_embedding(view_of(e->embd), st, c.dim, e->x, s, e->attn_in_o ? e->xo_words : nullptr));
   for (int l = 0; l < c.n_layers && !persist; ++l) {
     const Layer& L = e->L[l];
     float* kc = e->kc + static_cast<size_t>(l) * e->max_seq * kvd;
@@ -466,7 +527,7 @@ int enqueue_token(mcpm_engine* e, bool short_ctx) {
       }
       if (fe == hipErrorNotSupported) {
         MCPM_HIP(timed(e, MCPM_KC_QKV, [&] { return launch_gemv(a, PRO_NORM_AWAY, EPI_QKV, n_cu, s); }));
-        MCPM_HIP(timed(e, MCPM_KC_ATTN, [&] {
+        if (!in_o) MCPM_HIP(timed(e, MCPM_KC_ATTN, [&] {
           if (q8k)
             return launch_attention_q8k(e->q, kc, vc, st, c.n_heads, c.n_kv_heads, c.head_dim, e->att_q8,
                                         e->attn_err, s);
@@ -474,7 +535,30 @@ int enqueue_token(mcpm_engine* e, bool short_ctx) {
         }));
       }
     }
-    if (q8k) {
+    if (in_o) {
+      // every head's attention over the one chunk, then its ties-even Q8_K,
+      // in the O projection's prologue
+      GemvArgs a{};
+      a.reg[0] = GemvRegion{view_of(L.wo), nullptr, 0, c.dim};
+      a.nreg = 1;
+      a.total_rows = c.dim;
+      a.nb = qd / QK_K;
+      a.resid = e->x;
+      a.x = e->q;
+      a.state = st;
+      a.head_dim = c.head_dim;
+      a.k_cache = kc;
+      a.v_cache = vc;
+      a.kvd = kvd;
+      a.xrec = e->xo_rec;
+      a.epoch = e->xo_words;
+      a.tag_mul = static_cast<unsigned>(c.n_layers + 1);
+      a.tag_add = static_cast<unsigned>(l + 1);
+      a.xcc = reinterpret_cast<const int*>(e->xo_words + 128);
+      a.err = e->xo_words + 64;
+      a.spin_limit = grid_spin_limit(e);
+      MCPM_HIP(timed(e, MCPM_KC_OPROJ, [&] { return launch_gemv(a, PRO_ATTN_ONE, EPI_RESID, n_cu, s); }));
+    } else if (q8k) {
       // the attention output is already the O projection's Q8_K input
       GemvArgs a{};
       a.reg[0] = GemvRegion{view_of(L.wo), nullptr, 0, c.dim};
@@ -561,15 +645,17 @@ int enqueue_token(mcpm_engine* e, bool short_ctx) {
 // token's kernels run): the graph for its context length.
 int run_token(mcpm_engine* e, int pos) {
   const bool short_ctx = pos / ATTN_CHUNK + 1 <= e->attn_q8k_chunks;
+  const bool one_chunk = pos < ATTN_CHUNK;
   // Events recorded inside a captured graph cannot be read back with
   // hipEventElapsedTime, so a timed kernel class runs the same launches eagerly.
-  if (!e->use_graph || e->timing_class >= 0) return enqueue_token(e, short_ctx);
-  hipGraphExec_t& graph = e->graph[e->sample_mode ? 1 : 0][short_ctx && e->attn_q8k ? 1 : 0];
+  if (!e->use_graph || e->timing_class >= 0) return enqueue_token(e, short_ctx, one_chunk);
+  const int regime = one_chunk && e->attn_in_o ? 2 : short_ctx && e->attn_q8k ? 1 : 0;
+  hipGraphExec_t& graph = e->graph[e->sample_mode ? 1 : 0][regime];
   if (!graph) {
     hipStream_t s = e->ctx->stream;
     MCPM_HIP(hipStreamSynchronize(s));
     MCPM_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    const int rc = enqueue_token(e, short_ctx);
+    const int rc = enqueue_token(e, short_ctx, one_chunk);
     hipGraph_t g = nullptr;
     const hipError_t ce = hipStreamEndCapture(s, &g);
     if (rc) {

@@ -56,14 +56,16 @@ __device__ __forceinline__ T pick(int reg, T a, T b, T c) {
 //   xbs  [nb][16]  bsums as ints
 //   red  [260]     reduction scratch
 //   vrow [NW][64]  TILE: row values of each wave's current item
-//   U              PRO_ATTN_EVEN: the combined fp32 activations (nb*256),
-//                  later the TILE chain areas (NW waves x nb*S*12)
+//   U              PRO_ATTN_EVEN / PRO_ATTN_ONE: the fp32 attention output
+//                  (nb*256), later the TILE chain areas (NW waves x nb*S*12)
+//   at             PRO_ATTN_ONE: the staged chunk of one kv head (AttnLds)
 // Every region starts on a 16-byte boundary.
 struct LdsPlan {
-  int xs, xd, xbp, xbs, red, vrow, u, words;
+  int xs, xd, xbp, xbs, red, vrow, u, at, words;
 };
 
-__host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool attn, int NW) {
+// attn: 0 none, 1 PRO_ATTN_EVEN, 2 PRO_ATTN_ONE
+__host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, int attn, int NW) {
   LdsPlan L;
   L.xs = 0;
   L.xd = nb * 68;
@@ -74,7 +76,14 @@ __host__ __device__ inline LdsPlan lds_plan(int nb, int S, bool tile, bool attn,
   L.u = L.vrow + (tile ? NW * 64 : 0);
   const int usz = tile ? NW * nb * S * 12 : 0;
   L.words = L.u + (attn && nb * QK_K > usz ? nb * QK_K : usz);
+  L.at = L.words;
+  if (attn == 2) L.words += static_cast<int>((AttnLds<64>::bytes + 15) / 16 * 4);
   return L;
+}
+
+template <int PRO>
+constexpr int lds_attn() {
+  return PRO == PRO_ATTN_EVEN ? 1 : PRO == PRO_ATTN_ONE ? 2 : 0;
 }
 
 // ------------------------------------------------------------- prologue ----
@@ -100,6 +109,8 @@ struct ProRegs {
   float xp[MAX_NB];  // RMSNorm: x[t], x[t+256], ... of thread t < 256 (its partial's terms)
   f32x4 ao[ATTN_RB][2];  // PRO_ATTN_EVEN: o_c of thread t's 8 values, chunks 0..ATTN_RB-1
   float2 amz[ATTN_MZ];   // (m_c, z_c) of its head, chunks 0..ATTN_MZ-1
+  AttnRegs<4> kv;        // PRO_ATTN_ONE: the chunk's K and V rows of the work group's kv head
+  f32x4 aq;              // and a float4 of its query heads
   u32x4 q[NR];     // Q8_K codes of the lane's 16 values
   int bs[NR];      // Q8_K bsums[j]
   float d[NR];     // Q8_K d
@@ -120,7 +131,7 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
   for (int r = 0; r < NR; ++r) {
     if (4 * NW * r + 4 * wave < nb) {  // uniform in the wave: waves past the blocks skip
       const int b = min(4 * NW * r + 4 * wave + row, nb - 1);
-      if constexpr (PRO == PRO_ATTN_EVEN) {
+      if constexpr (PRO == PRO_ATTN_EVEN || PRO == PRO_ATTN_ONE) {
         // the activations are formed in LDS by prologue_compute
       } else if constexpr (PRO == PRO_Q8K) {
         const BlockQ8K* blk = a.xq + b;
@@ -141,6 +152,17 @@ __device__ __forceinline__ void prologue_load(const GemvArgs& a, int NW, int wav
           for (int i = 0; i < 4; ++i) X.g[r][i] = gp[i];
         }
       }
+    }
+  }
+  if constexpr (PRO == PRO_ATTN_ONE) {
+    // this work group's kv head's chunk and query heads (attn_xcd_heads), issued
+    // before the weights
+    const int t = static_cast<int>(threadIdx.x), jw = static_cast<int>(blockIdx.x) / 8, hpw = a.attn_hpw;
+    const int h0 = jw * hpw;
+    if (h0 < nb * QK_K / 64) {
+      attn_load_chunk<4>(X.kv, a.k_cache, a.v_cache, 0, a.state[1] + 1, a.kvd, static_cast<size_t>(h0 / 4) * 64,
+                         16, ATTN_CHUNK * 16);
+      if (t < hpw * 16) X.aq = reinterpret_cast<const f32x4*>(a.x + static_cast<size_t>(h0) * 64)[t];
     }
   }
   if constexpr (PRO == PRO_ATTN_EVEN) {
@@ -281,6 +303,84 @@ __device__ __forceinline__ void attn_combine(const GemvArgs& a, const ProRegs& X
   __syncthreads();
 }
 
+// PRO_ATTN_ONE: the attention output of every head over a context of
+// T = pos + 1 <= 64 positions (one chunk), into sx (src/ops/ops.cpp:537-628,
+// the oracle's or_attention), shared among the work groups of each XCD:
+// work group b runs on XCD x = b % 8 and is the j = b / 8-th there; for
+// j*hpw < heads it computes query heads h0 = j*hpw .. h0+hpw-1 (one kv
+// head's) with attn_token_chunk on the chunk's K and V rows (R, loaded by
+// prologue_load ahead of the weights) and its queries (q) staged in LDS,
+// then the one-chunk combine x = fma(o, f, 0) / fma(z_c, f, 0),
+// f = exp(m_c - m), m = m_c, and stores each value as a (value, tag) record
+// in XCD x's array at workgroup scope: the vector L1 writes through and the
+// line stays in that XCD's L2.  Every work group then waits for all records
+// of its XCD (agent-scope loads, which miss the L1 and find them in the
+// L2), at most spin_limit polls; past it, or on a work group that does not
+// run on the XCD recorded at set-up, the error word is set and the values
+// are not used.  All work groups of the launch must be resident (grid <=
+// CUs).  Needs 256 threads; ends with a barrier.
+__device__ __forceinline__ void attn_xcd_heads(const GemvArgs& a, const AttnRegs<4>& R, f32x4 q, float* sx,
+                                               float* scratch) {
+  constexpr int HD = 64;
+  const int t = static_cast<int>(threadIdx.x), b = static_cast<int>(blockIdx.x);
+  const int x = b % 8, jw = b / 8, T = a.state[1] + 1, nh = a.nb * QK_K / HD, hpw = a.attn_hpw;
+  const uint32_t tag = a.epoch[0] * a.tag_mul + a.tag_add;
+  uint64_t* rec = a.xrec + static_cast<size_t>(x) * nh * HD;
+  bool bad = static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u) != a.xcc[x];  // XCC_ID, bits 3:0
+  if (jw * hpw < nh && !bad) {
+    const int h0 = jw * hpw;
+    const AttnLds<HD> A(scratch);
+    if (t < hpw * (HD / 4)) reinterpret_cast<f32x4*>(A.sQ)[t] = q;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int f = t + 256 * u, jr = f >> 4, c4 = f & 15;
+      *reinterpret_cast<f32x4*>(&A.sK[jr * (HD + 4) + c4 * 4]) = R.k[u];
+      *reinterpret_cast<f32x4*>(&A.sV[jr * HD + c4 * 4]) = R.v[u];
+    }
+    __syncthreads();
+    float o[1];
+    attn_token_chunk<HD, 1>(A.sK, A.sV, A.sQ, A.sE, A.sMZ, 0, T, hpw, HD, hpw * HD,
+                            1.0f / sqrtf(static_cast<float>(HD)), o, t);
+    if (t < hpw * HD) {
+      const float2 mz = A.sMZ[t / HD];
+      const float f = exp_f32(mz.x - mz.x);  // one chunk: m = m_c
+      const float v = __builtin_fmaf(o[0], f, 0.0f) / __builtin_fmaf(mz.y, f, 0.0f);
+      __hip_atomic_store(rec + h0 * HD + t, (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+  // every record of the XCD: thread t's records t + 256k
+  constexpr int KR = ATTN_MAX_NB;  // nh*64 = nb*256 <= 2048
+  uint64_t r[KR];
+#pragma unroll
+  for (int k = 0; k < KR; ++k) {
+    const int i = t + 256 * k;
+    r[k] = i < nh * HD && !bad ? __hip_atomic_load(rec + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : static_cast<uint64_t>(tag) << 32;
+  }
+  for (unsigned spins = 0;; ++spins) {
+    unsigned pend = 0;
+#pragma unroll
+    for (int k = 0; k < KR; ++k)
+      if (static_cast<uint32_t>(r[k] >> 32) != tag) pend |= 1u << k;
+    if (!pend) break;
+    if (spins >= a.spin_limit) {
+      bad = true;
+      break;
+    }
+#pragma unroll
+    for (int k = 0; k < KR; ++k)
+      if (pend >> k & 1u) r[k] = __hip_atomic_load(rec + t + 256 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (bad) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int k = 0; k < KR; ++k) {
+    const int i = t + 256 * k;
+    if (i < nh * HD) sx[i] = __uint_as_float(static_cast<uint32_t>(r[k]));
+  }
+  __syncthreads();
+}
+
 // Q8_K activations of the work group into LDS: as given (PRO_Q8K), or
 // quantized from fp32 (ties-even or ties-away), optionally after RMSNorm
 // (src/ops/ops.cpp:676-723, 745-789).  Ends with a work-group barrier.
@@ -299,8 +399,10 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, int NW, int 
   } else {
     constexpr bool norm = (PRO == PRO_NORM_AWAY || PRO == PRO_NORM_EVEN);
     constexpr bool away = (PRO == PRO_QUANT_AWAY || PRO == PRO_NORM_AWAY);
-    constexpr bool attn = (PRO == PRO_ATTN_EVEN);
-    if constexpr (attn) attn_combine(a, X, reinterpret_cast<float*>(L + P.u));
+    constexpr bool attn = (PRO == PRO_ATTN_EVEN || PRO == PRO_ATTN_ONE);
+    if constexpr (PRO == PRO_ATTN_EVEN) attn_combine(a, X, reinterpret_cast<float*>(L + P.u));
+    if constexpr (PRO == PRO_ATTN_ONE)
+      attn_xcd_heads(a, X.kv, X.aq, reinterpret_cast<float*>(L + P.u), reinterpret_cast<float*>(L + P.at));
     float rms = 1.0f;
     if constexpr (norm) {
       // thread t's partial runs over x[t], x[t+256], ... (multiply then add)
@@ -720,7 +822,7 @@ __device__ __forceinline__ void gemv_core(const GemvArgs& a, int n_items, int S,
   static_assert(TILE || !GRP, "GRP is a TILE shape");
   const GemvPlan<EPI, TILE, WT, GRP, COH> pl(a, n_items, S, KB, vb, vg);
   const int lane = pl.lane, wave = pl.wave, NW = pl.NW, nb = pl.nb;
-  const LdsPlan P = lds_plan(nb, S, TILE, PRO == PRO_ATTN_EVEN, GRP ? 1 : NW);
+  const LdsPlan P = lds_plan(nb, S, TILE, lds_attn<PRO>(), GRP ? 1 : NW);
   const int stride = pl.stride, first = pl.first, n_steps = pl.n_steps, pos = pl.pos;
   const Region &A = pl.A, &B = pl.B, &C = pl.C;
   auto ref_at = [&](int t, int& b, int& s) { return pl.ref_at(t, b, s); };
@@ -1172,7 +1274,8 @@ Shape pick_shape(const GemvArgs& a, int prologue, int epilogue, int n_cu) {
 }
 
 size_t lds_bytes(const GemvArgs& a, const Shape& sh, int prologue) {
-  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, prologue == PRO_ATTN_EVEN, sh.grp ? 1 : sh.NW).words) * 4;
+  const int attn = prologue == PRO_ATTN_EVEN ? 1 : prologue == PRO_ATTN_ONE ? 2 : 0;
+  return static_cast<size_t>(lds_plan(a.nb, sh.S, sh.tile, attn, sh.grp ? 1 : sh.NW).words) * 4;
 }
 
 template <int PRO, int EPI, bool TILE, int WT, bool GRP = false>
@@ -1198,11 +1301,27 @@ int n_items_of(GemvArgs& a, const Shape& sh) {
   return n;
 }
 
+// PRO_ATTN_ONE: query heads per work group (1, 2 or 4, one kv head's) so
+// that the work groups of every XCD (at least grid / 8 of them) cover every
+// head; 0 when they cannot.
+int attn_one_hpw(int grid, int nb) {
+  const int nh = nb * QK_K / 64, per_xcd = grid / 8;
+  for (int hpw = 1; hpw <= 4; hpw *= 2)
+    if (per_xcd * hpw >= nh) return hpw;
+  return 0;
+}
+
 template <int PRO, int EPI, bool TILE, int WT, bool GRP = false>
-hipError_t launch_one(const GemvArgs& a, int n_items, const Shape& sh, int n_cu, size_t lds, hipStream_t s) {
+hipError_t launch_one(const GemvArgs& a0, int n_items, const Shape& sh, int n_cu, size_t lds, hipStream_t s) {
   if (TILE && sh.NW != GEMV_TILE_WAVES) return hipErrorInvalidValue;  // the kernel's launch bound
-  if (GRP && (sh.S * a.nb > 256 * sh.KB || sh.S > 64)) return hipErrorInvalidValue;
+  if (GRP && (sh.S * a0.nb > 256 * sh.KB || sh.S > 64)) return hipErrorInvalidValue;
   const int grid = grid_for<PRO, EPI, TILE, WT, GRP>(n_items, sh, n_cu, lds);
+  GemvArgs a = a0;
+  if constexpr (PRO == PRO_ATTN_ONE) {
+    // every work group resident at once (grid_for: one round), 4 waves
+    a.attn_hpw = attn_one_hpw(grid, a.nb);
+    if (!a.attn_hpw || sh.NW != 4 || !a.xrec || !a.epoch || !a.xcc || !a.err) return hipErrorNotSupported;
+  }
   // the argmax partials: one per wave of the grid, as many as the caller sized
   if (EPI == EPI_LOGITS && grid * sh.NW != a.argmax_parts) return hipErrorInvalidValue;
   if (grid <= 0) return hipSuccess;
@@ -1239,6 +1358,18 @@ hipError_t launch_pe(const GemvArgs& a0, const Shape& sh, int n_cu, hipStream_t 
 }
 
 }  // namespace
+
+int gemv_attn_one_hpw(const GemvArgs& a0, int n_cu) {
+  GemvArgs a = a0;
+  const Shape sh = pick_shape(a, PRO_ATTN_ONE, EPI_RESID, n_cu);
+  const int n_items = n_items_of(a, sh);
+  const size_t lds = lds_bytes(a, sh, PRO_ATTN_ONE);
+  int grid = 0;
+  if (sh.grp && weight_kind(a) == WT_Q4) grid = grid_for<PRO_ATTN_ONE, EPI_RESID, true, WT_Q4, true>(n_items, sh, n_cu, lds);
+  else if (sh.grp && weight_kind(a) == WT_Q6) grid = grid_for<PRO_ATTN_ONE, EPI_RESID, true, WT_Q6, true>(n_items, sh, n_cu, lds);
+  else return 0;
+  return sh.NW == 4 ? attn_one_hpw(grid, a.nb) : 0;
+}
 
 int gemv_grid(const GemvArgs& a0, int n_cu) {
   // number of argmax partials the LM-head launch (PRO_NORM_EVEN, EPI_LOGITS)
@@ -1289,6 +1420,10 @@ hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, 
   if (a.nb <= 0 || a.nb > MAX_NB) return hipErrorInvalidValue;
   if (prologue == PRO_ATTN_EVEN && (a.nb > ATTN_MAX_NB || a.head_dim <= 0 || a.head_dim % ATTN_VALS))
     return hipErrorInvalidValue;
+  // PRO_ATTN_ONE: head_dim 64, four query heads per kv head (nb*256 = 4 * kvd)
+  if (prologue == PRO_ATTN_ONE && (a.nb > ATTN_MAX_NB || a.head_dim != 64 || a.kvd * 4 != a.nb * QK_K ||
+                                   !a.k_cache || !a.v_cache || !a.state || !a.x))
+    return hipErrorInvalidValue;
   if (a.pair && a.reg[0].w.type != a.reg[1].w.type) return hipErrorInvalidValue;
   GemvArgs b = a;
   if (!b.pair && epilogue == EPI_LOGITS) {
@@ -1303,6 +1438,7 @@ hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, 
   MCPM_PE(PRO_QUANT_EVEN, EPI_STORE)
   MCPM_PE(PRO_QUANT_EVEN, EPI_RESID)
   MCPM_PE(PRO_ATTN_EVEN, EPI_RESID)
+  MCPM_PE(PRO_ATTN_ONE, EPI_RESID)
   MCPM_PE(PRO_QUANT_AWAY, EPI_RESID)
   MCPM_PE(PRO_NORM_AWAY, EPI_QKV)
   MCPM_PE(PRO_NORM_AWAY, EPI_SWIGLU)

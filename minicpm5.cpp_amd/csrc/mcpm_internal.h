@@ -159,6 +159,9 @@ enum Prologue : int {
   PRO_NORM_AWAY = 3,  // RMSNorm then quantize, ties away (rmsnorm_and_quantize_q8k)
   PRO_NORM_EVEN = 4,  // RMSNorm then quantize, ties to even (rmsnorm + matmul)
   PRO_ATTN_EVEN = 5,  // combine the attention partials, then quantize ties to even
+  PRO_ATTN_ONE = 6,   // attention of every head over a one-chunk context (q in x, K and V
+                      // rows in k_cache / v_cache), shared among each XCD's work groups
+                      // through tagged records, then quantize ties to even
 };
 
 // Epilogue modes.
@@ -212,6 +215,18 @@ struct GemvArgs {
   float* h_out;
   float2* argmax_part;   // per wave (value, index as float bits)
   int argmax_parts;      // EPI_LOGITS: entries of argmax_part (the launch must write exactly these)
+  // PRO_ATTN_ONE: work group j of an XCD computes query heads j*attn_hpw ..
+  // and stores them as (value, tag) records in its XCD's array of xrec
+  // ([8][heads*64]); tag = epoch[0] * tag_mul + tag_add.  xcc[x]: the XCD
+  // that work groups b % 8 == x ran on at set-up.  A wait past spin_limit
+  // polls, or a work group on another XCD, sets err.
+  uint64_t* xrec;
+  const unsigned* epoch;
+  unsigned tag_mul, tag_add;
+  int attn_hpw;
+  const int* xcc;
+  unsigned* err;
+  unsigned spin_limit;
 };
 
 // Device step state shared by the engine's kernels.
@@ -223,6 +238,10 @@ struct StepState {
 };
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, int epilogue, int n_cu, hipStream_t s);
+// The query heads per work group a PRO_ATTN_ONE / EPI_RESID launch of a would
+// take (its grid's work groups per XCD covering every head), 0 when it
+// cannot run.
+int gemv_attn_one_hpw(const GemvArgs& a, int n_cu);
 
 // The grid barrier state of the fused kernels (device memory, zeroed at
 // allocation): ctr[64 * x] arrivals of XCD x, the launch count, and an error
@@ -346,7 +365,9 @@ hipError_t launch_attention_batch(const float* q, const float* kc, const float* 
 // ties-even into q (the O projection's input), in one pass.
 hipError_t launch_quant_batch_attn(const AttnPart& part, size_t tok_stride_o, size_t tok_stride_mz, int pos0,
                                    int n_tok, int n_heads, int head_dim, int max_chunks, QuantBatch q, hipStream_t s);
-hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s);
+// epoch (optional): advanced by one (the tags of the token's XCD records).
+hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s,
+                            unsigned* epoch = nullptr);
 hipError_t launch_dequant_rows(const WView& w, int row0, int n_rows, int cols, float* out, hipStream_t s);
 hipError_t launch_gemv_f32(const float* w, const float* x, float* out, int rows, int cols, hipStream_t s);
 hipError_t launch_stream_read(const void* src, size_t bytes, int grid, uint32_t* out, hipStream_t s);

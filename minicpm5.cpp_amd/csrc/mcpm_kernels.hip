@@ -664,16 +664,19 @@ hipError_t launch_dequant_rows(const WView& w, int row0, int n_rows, int cols, f
 }
 
 // get_embedding: row `token` (from the step state) dequantized to x; one
-// work group per 256-value block, one value per thread.
+// work group per 256-value block, one value per thread.  epoch (optional):
+// advanced by one, by one thread.
 __global__ void __launch_bounds__(256) k_embedding(const WView w, const int* __restrict__ state, int dim,
-                                                   float* __restrict__ out) {
+                                                   float* __restrict__ out, unsigned* epoch) {
   const int token = state[0];
   const int i = blockIdx.x * QK_K + threadIdx.x;
   if (i < dim) out[i] = dequant_value(w, token, blockIdx.x, threadIdx.x);
+  if (epoch && i == 0) epoch[0] = epoch[0] + 1u;
 }
 
-hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s) {
-  hipLaunchKernelGGL(k_embedding, dim3((dim + QK_K - 1) / QK_K), dim3(QK_K), 0, s, w, state, dim, out);
+hipError_t launch_embedding(const WView& w, const int* state, int dim, float* out, hipStream_t s,
+                            unsigned* epoch) {
+  hipLaunchKernelGGL(k_embedding, dim3((dim + QK_K - 1) / QK_K), dim3(QK_K), 0, s, w, state, dim, out, epoch);
   return hipGetLastError();
 }
 

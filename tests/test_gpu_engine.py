@@ -518,3 +518,95 @@ def test_fused_qkv_attention_matches_oracle(ctx, small_image, monkeypatch, case)
         want = list(om.generate_greedy(prompt, 8))
         om.close()
         assert got == want
+
+
+# 32 query heads of 64 over 8 kv heads (the 2.4B shape's head geometry): the
+# O projection's 64 work groups (8 per XCD) take 4 heads each; and 16 over 4
+# with 8 work groups per XCD taking 2 heads each
+IN_O_SHAPES = {"kv8": (2, 1024, 32, 8, 64, 2816, 1000), "kv4": (2, 1024, 16, 4, 64, 2048, 1000)}
+
+
+@pytest.mark.parametrize("shape", sorted(IN_O_SHAPES))
+def test_attention_in_o_projection_matches_oracle(ctx, monkeypatch, shape):
+    """Contexts of one chunk (at most 64 positions) form the attention in the
+    O projection: each XCD's work groups split the query heads and share the
+    outputs through tagged records in the XCD's L2, with no attention launch
+    (counted: no attention launch below 64 positions, one per layer past it).
+    Logits bit-identical to the oracle at positions 0..79 (across the switch
+    at 64), and greedy and sampled tokens identical to the engine with the
+    attention as its own launch (MCPM_ATTN_IN_O=0)."""
+    cfg = mcpm.make_config(*IN_O_SHAPES[shape])
+    img = mcpm.synth_gguf(cfg, seed=77, mix=0)
+    rng = np.random.default_rng(5)
+    toks = [int(t) for t in rng.integers(0, 1000, 80)]
+    om = O.OracleModel(img)
+    om.init_kv(128)
+    want = np.empty(1000, np.float32)
+    eng = mcpm.Engine(ctx, image=img)
+    try:
+        eng.init_kv_cache(128)
+        for pos, t in enumerate(toks):
+            announce(f"attention in the O projection ({shape}): forward pos={pos}")
+            got, _ = eng.forward(t, pos)
+            om.forward(t, pos, want)
+            assert_bits(got, want)
+        eng.set_prefill(False)
+        for n_prompt in (20, 70):
+            # positions 0..n_prompt-1 (one generated token): an attention
+            # launch per layer only at positions 64 and past
+            eng.set_kernel_timing(mcpm.KC_ATTN)
+            eng.generate_greedy(np.array(toks[:n_prompt], np.int32), 1)
+            _, n = eng.kernel_time()
+            eng.set_kernel_timing(-1)
+            assert n == max(0, n_prompt - 64) * cfg.n_layers, (n_prompt, n)
+        prompt = np.array(toks[:24], np.int32)
+        got = (eng.generate_greedy(prompt, 60), eng.generate_sampled(prompt, 60, 0.9, 0.95, 7))
+    finally:
+        eng.free()
+    om.close()
+    monkeypatch.setenv("MCPM_ATTN_IN_O", "0")
+    ref = mcpm.Engine(ctx, image=img)
+    try:
+        ref.init_kv_cache(128)
+        announce(f"attention as its own launch ({shape})")
+        want_toks = (ref.generate_greedy(prompt, 60), ref.generate_sampled(prompt, 60, 0.9, 0.95, 7))
+    finally:
+        ref.free()
+    np.testing.assert_array_equal(got[0], want_toks[0])
+    np.testing.assert_array_equal(got[1], want_toks[1])
+
+
+def test_attention_in_o_give_up_then_recovers(ctx):
+    """The O projection's wait for its XCD's attention records with a spin
+    limit of 1 poll: the call returns MCPM_ERR_HIP; with the default limit
+    restored the next calls give the oracle's logits bit for bit (the token
+    epoch moved on, so no record of the abandoned calls matches a later
+    tag)."""
+    cfg = mcpm.make_config(*IN_O_SHAPES["kv8"])
+    img = mcpm.synth_gguf(cfg, seed=78, mix=0)
+    e = mcpm.Engine(ctx, image=img)
+    try:
+        e.init_kv_cache(64)
+        prompt = np.arange(5, 21, dtype=np.int32)
+        e.set_spin_limit(1)
+        codes = []
+        for i in range(6):
+            announce(f"attention in the O projection: spin limit 1, call {i}")
+            try:
+                e.generate_greedy(prompt, 4)
+            except mcpm.McpmError as err:
+                codes.append(err.code)
+                break
+        assert codes == [mcpm.ERR_HIP], "no wait gave up at a spin limit of 1"
+        e.set_spin_limit(0)
+        announce("attention in the O projection: default spin limit after the give-up")
+        om = O.OracleModel(img)
+        om.init_kv(64)
+        want = np.empty(1000, np.float32)
+        for pos, t in enumerate(prompt):
+            got, _ = e.forward(int(t), pos)
+            om.forward(int(t), pos, want)
+            assert_bits(got, want)
+        om.close()
+    finally:
+        e.free()
