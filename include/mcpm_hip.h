@@ -277,8 +277,9 @@ int mcpm_engine_uses_persistent(const mcpm_engine *e);
  * No counterpart in the reference. */
 int mcpm_engine_persistent_xcd_local(const mcpm_engine *e);
 /* The spin limit of the waits inside the engine's launches: the fused
- * kernels' grid barrier (MCPM_FUSED_FFN / MCPM_FUSED_ATTN) and the persistent
- * launch's hand-offs.  A wait that passes it gives up, every work group then
+ * kernels' grid barrier (MCPM_FUSED_FFN / MCPM_FUSED_ATTN), the persistent
+ * launch's hand-offs and the O projection's wait for its XCD's attention
+ * records (contexts of at most 64 positions).  A wait that passes it gives up, every work group then
  * leaves, and the call returns MCPM_ERR_HIP with the wait state reset, so the
  * next call runs normally.  0 restores the defaults (1<<20 barrier polls,
  * 1<<18 hand-off polls).  No counterpart in the reference: it lets tests
