@@ -51,6 +51,8 @@ PROFILE_CLASSES = {
     "qkv": "k_gemv<3, 1, true, 2, false>",
     "attn": "k_attention_q8k",
     "oproj": "k_gemv<0, 2, true, 0, true>",
+    # contexts of at most 64 positions: the attention inside the O projection
+    "oproj_attn": "k_gemv<6, 2, true, 0, true>",
     "gate_up": "k_gemv<3, 3, true, 0, false>",
     "down": "k_gemv<2, 2, true, 1, true>",
     "lm_head": "k_gemv<4, 4, false, 1, false>",
