@@ -27,8 +27,6 @@ namespace mcpm {
 // Partials (AttnPart): o_c at o[(h*max_chunks + c)*head_dim + i], (m_c, z_c)
 // at mz[h*max_chunks + c].  Every load of a chunk's K and V rows is issued at
 // once, one chunk ahead, and the rows are staged through LDS.
-constexpr int ATTN_MAX_GROUP = 8;
-constexpr int ATTN_CPW = 8;
 constexpr int ATTN_MAX_SPLITS = 64;
 
 __host__ __device__ inline int attn_chunks_per_split(int nch) {

@@ -18,6 +18,8 @@ constexpr int QK_K = 256;
 constexpr int QK8_0 = 32;
 constexpr int MAX_NB = 32;        // largest K / 256 the Q8_K GEMVs accept (K <= 8192)
 constexpr int ATTN_CHUNK = 64;    // positions per attention split
+constexpr int ATTN_MAX_GROUP = 8;  // query heads per kv head the attention kernels take, at most
+constexpr int ATTN_CPW = 8;        // chunks one attention split takes, at most
 constexpr int GEMV_MAX_WAVES = 8;  // GEMV work groups: 4..8 waves (ROW shape)
 constexpr int GEMV_TILE_WAVES = 4;  // TILE shape: one wave per SIMD
 constexpr int ROWS_PER_GROUP = 8; // output rows per GEMV work item (8 lanes each)

@@ -3,6 +3,10 @@
 // kernels.
 #pragma once
 
+#include <algorithm>
+#include <cstring>
+#include <initializer_list>
+
 #include "mcpm_internal.h"
 
 namespace mcpm {
@@ -20,7 +24,7 @@ struct PdSub {
   int off, R, type;
 };
 
-__host__ __device__ inline int pd_sub_bytes(int type, int R, int nb) {
+__host__ __device__ constexpr int pd_sub_bytes(int type, int R, int nb) {
   return type == MCPM_TYPE_Q4_K ? 144 * R * nb : 208 * R * nb + ((4 * R * nb + 15) & ~15);
 }
 
@@ -201,8 +205,124 @@ __host__ __device__ inline PdSrc pd_slab_src(const PdShape& s, int b, int off, c
 // persistent kernel: n_cu a multiple of 8, 8 kv heads of 64 (head h's rows
 // and attention on XCD h), a head group of one Q8_K block (4 query heads),
 // at most two attention chunks per work group, LDS within 160 KiB.
-bool pd_plan(const mcpm_model_config& c, int n_cu, int max_seq, int tq, int tk, int tv, int to, int td,
-             PdShape& s, const char** why);
+constexpr bool pd_plan(const mcpm_model_config& c, int n_cu, int max_seq, int tq, int tk, int tv, int to, int td,
+                       PdShape& s, const char** why) {
+  auto no = [&](const char* w) {
+    if (why) *why = w;
+    return false;
+  };
+  s = PdShape{};
+  if (n_cu <= 0 || n_cu % PD_XCDS) return no("CU count not a multiple of 8");
+  s.G = n_cu;
+  s.W = n_cu / PD_XCDS;
+  s.L = c.n_layers;
+  s.dim = c.dim;
+  s.nbx = c.dim / QK_K;
+  s.hd = c.head_dim;
+  s.nkv = c.n_kv_heads;
+  s.group = c.n_kv_heads > 0 ? c.n_heads / c.n_kv_heads : 0;
+  s.gh = s.group * s.hd;
+  s.qd = c.n_heads * c.head_dim;
+  s.nbq = s.qd / QK_K;
+  s.kvd = s.nkv * s.hd;
+  s.ffn = c.ffn;
+  s.ffn_pad = c.ffn_pad;
+  s.nbh = c.ffn_pad / QK_K;
+  s.eps = c.eps;
+  if (s.nkv != PD_XCDS || s.hd != 64) return no("needs 8 kv heads of 64");
+  if (s.gh != QK_K) return no("head group not one Q8_K block");
+  if (s.gh % (2 * s.W) || s.hd % (2 * s.W)) return no("head rows do not split into even runs per work group");
+  if (c.dim % QK_K || s.nbx > PD_NBX || s.nbq > PD_NBQ || c.ffn_pad % QK_K || s.nbh > PD_NBH || c.ffn > c.ffn_pad)
+    return no("dimensions outside the kernel's bounds");
+  if (tq != MCPM_TYPE_Q4_K || tk != MCPM_TYPE_Q4_K) return no("q and k must be Q4_K");
+  for (int ty : {tv, to, td})
+    if (ty != MCPM_TYPE_Q4_K && ty != MCPM_TYPE_Q6_K) return no("weight type without a kernel");
+  s.max_chunks = (max_seq + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  s.part_stride = (s.gh + 2 * s.group + PD_REC_LINE - 1) / PD_REC_LINE * PD_REC_LINE;
+  if (s.max_chunks > 2 * s.W) return no("context longer than two chunks per work group");
+  s.nq = s.gh / s.W;
+  s.nk = s.hd / s.W;
+  s.nh_max = (c.dim + s.G - 1) / s.G;
+  s.np_max = (c.ffn + s.G - 1) / s.G;
+  if (s.nq + 2 * s.nk > 64 || 2 * s.np_max > 64 || s.nh_max > 64) return no("too many rows per work group");
+  auto sub = [](int off, int R, int type) { return PdSub{off, R, type}; };
+  s.sq = sub(0, s.nq, tq);
+  s.sk = sub(pd_sub_bytes(tq, s.nq, s.nbx), s.nk, tk);
+  s.sv = sub(s.sk.off + pd_sub_bytes(tk, s.nk, s.nbx), s.nk, tv);
+  const int qkv_bytes = s.sv.off + pd_sub_bytes(tv, s.nk, s.nbx);
+  s.so = sub(0, s.nh_max, to);
+  const int o_bytes = pd_sub_bytes(to, s.nh_max, s.nbq);
+  s.sg = sub(0, s.np_max, MCPM_TYPE_Q4_K);
+  s.su = sub(pd_sub_bytes(MCPM_TYPE_Q4_K, s.np_max, s.nbx), s.np_max, MCPM_TYPE_Q4_K);
+  const int gu_bytes = 2 * pd_sub_bytes(MCPM_TYPE_Q4_K, s.np_max, s.nbx);
+  s.sd = sub(0, s.nh_max, td);
+  const int d_bytes = pd_sub_bytes(td, s.nh_max, s.nbh);
+  const int kib = 1024;
+  auto up = [&](int v) { return (v + kib - 1) / kib * kib; };
+  s.reg_sz[0] = up(qkv_bytes);
+  s.reg_sz[1] = up(o_bytes);
+  s.reg_sz[2] = up(gu_bytes);
+  s.reg_sz[3] = up(d_bytes);
+  s.reg_off[0] = 0;
+  for (int r = 1; r < 4; ++r) s.reg_off[r] = s.reg_off[r - 1] + s.reg_sz[r - 1];
+  s.slab_stride = s.reg_off[3] + s.reg_sz[3];
+  s.wd_lds = std::max(s.reg_sz[3], (PD_ATTN_LDS + 15) & ~15);
+  s.scr_off = s.reg_off[3] + s.wd_lds;
+  // scratch (dwords)
+  const int nbm = std::max({s.nbx, s.nbq, s.nbh});
+  auto a4 = [](int v) { return (v + 3) & ~3; };
+  s.s_xs = 0;
+  s.s_xd = nbm * 68;
+  s.s_xbp = s.s_xd + a4(nbm);
+  s.s_xbs = s.s_xbp + nbm * 4;
+  s.s_red = s.s_xbs + nbm * 16;
+  s.s_u = a4(s.s_red + 260);
+  const int rq = s.nq + 2 * s.nk;
+  // the attention's rows at pos, combined output, own o_c, every chunk's
+  // (m_c, z_c)
+  const int attn_words = 2 * s.hd + 3 * s.gh + 2 * 64 * ATTN_MAX_GROUP;
+  // the down phase stages its hand-off in rounds of up to 16 blocks
+  const int u_words = std::max({c.dim, rq * s.nbx * 12, s.nh_max * s.nbq * 12, 2 * s.np_max * s.nbx * 12,
+                                s.nh_max * s.nbh * 12, attn_words, std::min(s.nbh, 16) * QK_K});
+  s.s_vrow = a4(s.s_u + u_words);
+  const int rmax = std::max({rq, s.nh_max, 2 * s.np_max});
+  s.s_ownx = a4(s.s_vrow + rmax);
+  s.s_ownx2 = a4(s.s_ownx + s.nh_max);
+  s.s_misc = a4(s.s_ownx2 + s.nh_max);
+  s.lds_bytes = s.scr_off + (s.s_misc + 24) * 4;  // abort flag, launch count, two vote sets, sub-region table
+  if (s.lds_bytes > 160 * 1024 - 256) return no("LDS plan above 160 KiB");  // room for the runtime's own LDS words
+  return true;
+}
+
+// The plan of the shape the launch has a compiled instance for, the
+// 2.4B-shaped decoder (40 layers, hidden 2304, 32 query and 8 kv heads of 64,
+// FFN 5760, Q4_K q/k/o/gate/up with Q6_K v and down, RMSNorm eps 1e-6) on 256
+// CUs: that instance takes every field of the plan but the layer count and the
+// chunk count as compile-time constants, which frees the registers and the
+// instructions that reading them from the launch's arguments takes.
+constexpr PdShape pd_fixed_plan() {
+  mcpm_model_config c{};
+  c.n_layers = 40;
+  c.dim = 2304;
+  c.n_heads = 32;
+  c.n_kv_heads = 8;
+  c.head_dim = 64;
+  c.ffn = 5760;
+  c.ffn_pad = 5888;
+  c.eps = 1e-6f;
+  PdShape s{};
+  pd_plan(c, 256, 4096, MCPM_TYPE_Q4_K, MCPM_TYPE_Q4_K, MCPM_TYPE_Q6_K, MCPM_TYPE_Q4_K, MCPM_TYPE_Q6_K, s, nullptr);
+  return s;
+}
+
+// True when s is pd_fixed_plan() in every field but the layer count and the
+// chunk count (the plans hold ints and one float, no padding).
+inline bool pd_fixed_shape(const PdShape& s) {
+  PdShape f = pd_fixed_plan(), c = s;
+  c.L = f.L;
+  c.max_chunks = f.max_chunks;
+  return std::memcmp(&c, &f, sizeof f) == 0;
+}
 // Copies every layer's weights into the slab layout (device gather).
 hipError_t launch_build_slab(const PdShape& s, const PdLayer* d_layers, uint8_t* slab, hipStream_t st);
 // Record buffer sizes (records) for the shape, every array starting on a

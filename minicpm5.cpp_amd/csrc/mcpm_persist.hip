@@ -55,6 +55,16 @@ static_assert(PD_ATTN_LDS == static_cast<int>(AttnLds<64>::bytes), "attention st
 
 namespace {
 
+// The fixed plan's fields as compile-time constants for the instance built
+// for it (FS); the other instance reads the launch's plan.  The layer count
+// and the chunk count always come from the launch (a.s).
+__device__ constexpr PdShape kPdFixed = pd_fixed_plan();
+template <bool FS>
+__device__ __forceinline__ const PdShape& pd_s(const PdArgs& a) {
+  if constexpr (FS) return kPdFixed;
+  else return a.s;
+}
+
 typedef short pd_i16x2 __attribute__((ext_vector_type(2)));
 constexpr int CHAIN_BATCH_PD = 12;  // chain entries read per LDS round trip
 
@@ -518,18 +528,22 @@ __device__ __forceinline__ void pd_norm_quant(const PdShape& s, uint32_t* S, con
   pd_bar();
 }
 
+template <bool FS>
 __device__ __forceinline__ const uint8_t* pd_slab(const PdArgs& a, int l, int r) {
-  return a.slab + (static_cast<size_t>(l) * a.s.G + blockIdx.x) * a.s.slab_stride + a.s.reg_off[r];
+  const PdShape& s = pd_s<FS>(a);
+  return a.slab + (static_cast<size_t>(l) * s.G + blockIdx.x) * s.slab_stride + s.reg_off[r];
 }
+template <bool FS>
 __device__ __forceinline__ void pd_copy_region(const PdArgs& a, uint8_t* LDS, int l, int r) {
-  pd_copy(pd_slab(a, l, r), LDS + a.s.reg_off[r], a.s.reg_sz[r]);
+  const PdShape& s = pd_s<FS>(a);
+  pd_copy(pd_slab<FS>(a, l, r), LDS + s.reg_off[r], s.reg_sz[r]);
 }
 
 // Q (kind 0), O (2), G (3) or D (4) of layer l.
-template <bool XL>
+template <bool XL, bool FS>
 __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_t* LDS, uint32_t* S, uint32_t tag,
                                         int pos, uint32_t& vit) {
-  const PdShape& s = a.s;
+  const PdShape& s = pd_s<FS>(a);
   const PdRows me = pd_rows(s, static_cast<int>(blockIdx.x));
   const int t = static_cast<int>(threadIdx.x), r16 = t >> 4, j = t & 15;
   uint32_t* misc = S + s.s_misc;
@@ -593,7 +607,7 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // while they wait for the chunks' partials (down at G where they own a
   // chunk, whose staging holds the down region until then).
   if (kind == 0) {
-    pd_copy_region(a, LDS, l, 1);
+    pd_copy_region<FS>(a, LDS, l, 1);
     // this layer's attention chunk (the down region is free until G)
     if (me.k < (pos + ATTN_CHUNK) / ATTN_CHUNK) {
       const size_t lay = static_cast<size_t>(l) * a.max_seq * s.kvd;
@@ -602,13 +616,13 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
     }
   }
   if (kind == 2 && me.k != s.W - 1) {
-    if (l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 0);
-    pd_copy_region(a, LDS, l, 2);
-    pd_copy_region(a, LDS, l, 3);
+    if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
+    pd_copy_region<FS>(a, LDS, l, 2);
+    pd_copy_region<FS>(a, LDS, l, 3);
   }
   // the combining work group with a chunk of its own (its staging is the
   // down region until its chunks are done)
-  if (kind == 3 && me.k == s.W - 1 && me.k <= pos / ATTN_CHUNK) pd_copy_region(a, LDS, l, 3);
+  if (kind == 3 && me.k == s.W - 1 && me.k <= pos / ATTN_CHUNK) pd_copy_region<FS>(a, LDS, l, 3);
 
   // hand-off and prologue: the Q8_K activations into the scratch
   if (kind == 0 || kind == 3) {
@@ -751,7 +765,7 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
     if (t < me.nh) {
       const float x = ownx2[t] + vrow[t];
       ownx[t] = x;
-      if (l + 1 < s.L) rec_stf(a.rx + me.hr0 + t, x, tag + 1);
+      if (l + 1 < a.s.L) rec_stf(a.rx + me.hr0 + t, x, tag + 1);
       else a.x_out[me.hr0 + t] = x;
     }
   }
@@ -779,10 +793,10 @@ __device__ __forceinline__ void pd_fill_last(AttnRegs<4>& R, const float* kr, co
 // wait idle for the partials, so it takes its weight copies for the next
 // phases here (the next layer's QKV, this layer's gate/up), and every other
 // work group its own at O.
-template <bool XL>
+template <bool XL, bool FS>
 __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LDS, uint32_t* S, uint32_t tag, int T,
                                              uint32_t& vit) {
-  const PdShape& s = a.s;
+  const PdShape& s = pd_s<FS>(a);
   const int t = static_cast<int>(threadIdx.x), h = static_cast<int>(blockIdx.x) % PD_XCDS,
             k = static_cast<int>(blockIdx.x) / PD_XCDS, W = s.W;
   uint32_t* misc = S + s.s_misc;
@@ -790,9 +804,9 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
   const bool combiner = k == W - 1;
   if (k >= nch && !combiner) return true;  // no chunk of this context
   if (combiner) {
-    if (l + 1 < s.L) pd_copy_region(a, LDS, l + 1, 0);
-    pd_copy_region(a, LDS, l, 2);
-    if (k >= nch) pd_copy_region(a, LDS, l, 3);  // no chunk staged in the down region
+    if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
+    pd_copy_region<FS>(a, LDS, l, 2);
+    if (k >= nch) pd_copy_region<FS>(a, LDS, l, 3);  // no chunk staged in the down region
   }
   constexpr int HD = 64, GH = 256, OPT = ATTN_MAX_GROUP * HD / 256;
   const int group = s.group, kvd = s.kvd;
@@ -851,7 +865,7 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
     pd_bar();  // (m_c, z_c) of every head, every chunk's o_c
   }
   const int ppc = s.part_stride;  // o_c (GH), m_c (group), z_c (group), in whole lines
-  uint64_t* part = a.rpart + static_cast<size_t>(h) * s.max_chunks * ppc;
+  uint64_t* part = a.rpart + static_cast<size_t>(h) * a.s.max_chunks * ppc;
   if (!combiner) {
 #pragma unroll 1
     for (int cc = 0; cc < 2; ++cc) {
@@ -979,11 +993,11 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
 
 // One launch per token: every layer, from the embedding to the last layer's
 // x (x_out).
-template <bool XL>
+template <bool XL, bool FS>
 __global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t LDS[];
-  uint32_t* S = reinterpret_cast<uint32_t*>(LDS + a.s.scr_off);
-  uint32_t* misc = S + a.s.s_misc;
+  uint32_t* S = reinterpret_cast<uint32_t*>(LDS + pd_s<FS>(a).scr_off);
+  uint32_t* misc = S + pd_s<FS>(a).s_misc;
   const int t = static_cast<int>(threadIdx.x);
   if (t == 0) {
     misc[0] = 0u;
@@ -1003,8 +1017,8 @@ __global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
   uint32_t vit = 0;
   // E: this work group's embedding values, then layer 0's QKV and O weights
   {
-    const PdRows me = pd_rows(a.s, static_cast<int>(blockIdx.x));
-    float* ownx = reinterpret_cast<float*>(S + a.s.s_ownx);
+    const PdRows me = pd_rows(pd_s<FS>(a), static_cast<int>(blockIdx.x));
+    float* ownx = reinterpret_cast<float*>(S + pd_s<FS>(a).s_ownx);
     if (t < me.nh) {
       const int r = me.hr0 + t;
       const float x = dequant_value(a.embd, a.state[0], r / QK_K, r % QK_K);
@@ -1012,14 +1026,14 @@ __global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
       rec_stf(a.rx + r, x, tag0);
     }
   }
-  pd_copy_region(a, LDS, 0, 0);
+  pd_copy_region<FS>(a, LDS, 0, 0);
   // one loop over the phases, so that each phase's code exists once
 #pragma unroll 1
   for (int ph = 0; ph < 5 * L; ++ph) {
     const int l = ph / 5, kind = ph - 5 * l;
     const uint32_t tag = tag0 + static_cast<uint32_t>(l);
     const bool ok =
-        kind == 1 ? pd_attention<XL>(a, l, LDS, S, tag, T, vit) : pd_gemv<XL>(a, l, kind, LDS, S, tag, pos, vit);
+        kind == 1 ? pd_attention<XL, FS>(a, l, LDS, S, tag, T, vit) : pd_gemv<XL, FS>(a, l, kind, LDS, S, tag, pos, vit);
     if (!ok) return;
   }
   // every work group read the launch count before its first hand-off, and
@@ -1057,95 +1071,6 @@ __global__ void k_build_slab(const PdShape s, const PdLayer* __restrict__ layers
 }  // namespace
 
 // ------------------------------------------------------------------ host ---
-
-bool pd_plan(const mcpm_model_config& c, int n_cu, int max_seq, int tq, int tk, int tv, int to, int td,
-             PdShape& s, const char** why) {
-  auto no = [&](const char* w) {
-    if (why) *why = w;
-    return false;
-  };
-  s = PdShape{};
-  if (n_cu <= 0 || n_cu % PD_XCDS) return no("CU count not a multiple of 8");
-  s.G = n_cu;
-  s.W = n_cu / PD_XCDS;
-  s.L = c.n_layers;
-  s.dim = c.dim;
-  s.nbx = c.dim / QK_K;
-  s.hd = c.head_dim;
-  s.nkv = c.n_kv_heads;
-  s.group = c.n_kv_heads > 0 ? c.n_heads / c.n_kv_heads : 0;
-  s.gh = s.group * s.hd;
-  s.qd = c.n_heads * c.head_dim;
-  s.nbq = s.qd / QK_K;
-  s.kvd = s.nkv * s.hd;
-  s.ffn = c.ffn;
-  s.ffn_pad = c.ffn_pad;
-  s.nbh = c.ffn_pad / QK_K;
-  s.eps = c.eps;
-  if (s.nkv != PD_XCDS || s.hd != 64) return no("needs 8 kv heads of 64");
-  if (s.gh != QK_K) return no("head group not one Q8_K block");
-  if (s.gh % (2 * s.W) || s.hd % (2 * s.W)) return no("head rows do not split into even runs per work group");
-  if (c.dim % QK_K || s.nbx > PD_NBX || s.nbq > PD_NBQ || c.ffn_pad % QK_K || s.nbh > PD_NBH || c.ffn > c.ffn_pad)
-    return no("dimensions outside the kernel's bounds");
-  if (tq != MCPM_TYPE_Q4_K || tk != MCPM_TYPE_Q4_K) return no("q and k must be Q4_K");
-  for (int ty : {tv, to, td})
-    if (ty != MCPM_TYPE_Q4_K && ty != MCPM_TYPE_Q6_K) return no("weight type without a kernel");
-  s.max_chunks = (max_seq + ATTN_CHUNK - 1) / ATTN_CHUNK;
-  s.part_stride = (s.gh + 2 * s.group + PD_REC_LINE - 1) / PD_REC_LINE * PD_REC_LINE;
-  if (s.max_chunks > 2 * s.W) return no("context longer than two chunks per work group");
-  s.nq = s.gh / s.W;
-  s.nk = s.hd / s.W;
-  s.nh_max = (c.dim + s.G - 1) / s.G;
-  s.np_max = (c.ffn + s.G - 1) / s.G;
-  if (s.nq + 2 * s.nk > 64 || 2 * s.np_max > 64 || s.nh_max > 64) return no("too many rows per work group");
-  auto sub = [](int off, int R, int type) { return PdSub{off, R, type}; };
-  s.sq = sub(0, s.nq, tq);
-  s.sk = sub(pd_sub_bytes(tq, s.nq, s.nbx), s.nk, tk);
-  s.sv = sub(s.sk.off + pd_sub_bytes(tk, s.nk, s.nbx), s.nk, tv);
-  const int qkv_bytes = s.sv.off + pd_sub_bytes(tv, s.nk, s.nbx);
-  s.so = sub(0, s.nh_max, to);
-  const int o_bytes = pd_sub_bytes(to, s.nh_max, s.nbq);
-  s.sg = sub(0, s.np_max, MCPM_TYPE_Q4_K);
-  s.su = sub(pd_sub_bytes(MCPM_TYPE_Q4_K, s.np_max, s.nbx), s.np_max, MCPM_TYPE_Q4_K);
-  const int gu_bytes = 2 * pd_sub_bytes(MCPM_TYPE_Q4_K, s.np_max, s.nbx);
-  s.sd = sub(0, s.nh_max, td);
-  const int d_bytes = pd_sub_bytes(td, s.nh_max, s.nbh);
-  const int kib = 1024;
-  auto up = [&](int v) { return (v + kib - 1) / kib * kib; };
-  s.reg_sz[0] = up(qkv_bytes);
-  s.reg_sz[1] = up(o_bytes);
-  s.reg_sz[2] = up(gu_bytes);
-  s.reg_sz[3] = up(d_bytes);
-  s.reg_off[0] = 0;
-  for (int r = 1; r < 4; ++r) s.reg_off[r] = s.reg_off[r - 1] + s.reg_sz[r - 1];
-  s.slab_stride = s.reg_off[3] + s.reg_sz[3];
-  s.wd_lds = std::max(s.reg_sz[3], (PD_ATTN_LDS + 15) & ~15);
-  s.scr_off = s.reg_off[3] + s.wd_lds;
-  // scratch (dwords)
-  const int nbm = std::max({s.nbx, s.nbq, s.nbh});
-  auto a4 = [](int v) { return (v + 3) & ~3; };
-  s.s_xs = 0;
-  s.s_xd = nbm * 68;
-  s.s_xbp = s.s_xd + a4(nbm);
-  s.s_xbs = s.s_xbp + nbm * 4;
-  s.s_red = s.s_xbs + nbm * 16;
-  s.s_u = a4(s.s_red + 260);
-  const int rq = s.nq + 2 * s.nk;
-  // the attention's rows at pos, combined output, own o_c, every chunk's
-  // (m_c, z_c)
-  const int attn_words = 2 * s.hd + 3 * s.gh + 2 * 64 * ATTN_MAX_GROUP;
-  // the down phase stages its hand-off in rounds of up to 16 blocks
-  const int u_words = std::max({c.dim, rq * s.nbx * 12, s.nh_max * s.nbq * 12, 2 * s.np_max * s.nbx * 12,
-                                s.nh_max * s.nbh * 12, attn_words, std::min(s.nbh, 16) * QK_K});
-  s.s_vrow = a4(s.s_u + u_words);
-  const int rmax = std::max({rq, s.nh_max, 2 * s.np_max});
-  s.s_ownx = a4(s.s_vrow + rmax);
-  s.s_ownx2 = a4(s.s_ownx + s.nh_max);
-  s.s_misc = a4(s.s_ownx2 + s.nh_max);
-  s.lds_bytes = s.scr_off + (s.s_misc + 24) * 4;  // abort flag, launch count, two vote sets, sub-region table
-  if (s.lds_bytes > 160 * 1024 - 256) return no("LDS plan above 160 KiB");  // room for the runtime's own LDS words
-  return true;
-}
 
 namespace {
 // Record counts of the arrays rx, rx2, rh, rqkv, rpart, ratt, each rounded
@@ -1202,8 +1127,10 @@ hipError_t launch_build_slab(const PdShape& s, const PdLayer* d_layers, uint8_t*
 }
 
 hipError_t prepare_decode_persist(const PdShape& s) {
-  for (const void* k : {reinterpret_cast<const void*>(k_decode_persist<false>),
-                        reinterpret_cast<const void*>(k_decode_persist<true>)}) {
+  for (const void* k : {reinterpret_cast<const void*>(k_decode_persist<false, false>),
+                        reinterpret_cast<const void*>(k_decode_persist<true, false>),
+                        reinterpret_cast<const void*>(k_decode_persist<false, true>),
+                        reinterpret_cast<const void*>(k_decode_persist<true, true>)}) {
     const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, s.lds_bytes);
     if (e != hipSuccess) return e;
     // every work group must be resident at once: at least one per CU
@@ -1215,10 +1142,16 @@ hipError_t prepare_decode_persist(const PdShape& s) {
 }
 
 hipError_t launch_decode_persist(const PdArgs& a, hipStream_t st) {
-  if (a.xcd_local)
-    launch_kernel(k_decode_persist<true>, dim3(a.s.G), dim3(256), static_cast<size_t>(a.s.lds_bytes), st, a);
-  else
-    launch_kernel(k_decode_persist<false>, dim3(a.s.G), dim3(256), static_cast<size_t>(a.s.lds_bytes), st, a);
+  // the instance compiled for the fixed plan where the launch's plan is it
+  const dim3 g(a.s.G), b(256);
+  const size_t lds = static_cast<size_t>(a.s.lds_bytes);
+  if (pd_fixed_shape(a.s)) {
+    if (a.xcd_local) launch_kernel(k_decode_persist<true, true>, g, b, lds, st, a);
+    else launch_kernel(k_decode_persist<false, true>, g, b, lds, st, a);
+  } else {
+    if (a.xcd_local) launch_kernel(k_decode_persist<true, false>, g, b, lds, st, a);
+    else launch_kernel(k_decode_persist<false, false>, g, b, lds, st, a);
+  }
   return hipGetLastError();
 }
 

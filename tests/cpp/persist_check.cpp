@@ -10,10 +10,15 @@
 //  - the hand-offs: the row ranges of the work groups cover each consumer's
 //    records exactly once, every record array starts on a cache line, and
 //    the blocks stored at workgroup scope fill whole lines;
-//  - shapes the kernel does not take are refused.
+//  - shapes the kernel does not take are refused;
+//  - the plan the fixed-shape instance compiles in (pd_fixed_plan, evaluated
+//    at compile time) equals the plan made at run time for that shape, and
+//    pd_fixed_shape picks that instance for it at any layer count and KV
+//    capacity the kernel takes, and for no other shape or weight type.
 // Prints one line per shape; exit status 0 when every check holds.
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "mcpm_persist.h"
@@ -201,6 +206,45 @@ static void check_refused(const char* name, const mcpm_model_config& c, int n_cu
   std::printf("%s: refused (%s)\n", name, why ? why : "?");
 }
 
+static PdShape plan_of(const mcpm_model_config& c, int n_cu, int max_seq, int tv, int to, int td) {
+  PdShape s{};
+  if (!pd_plan(c, n_cu, max_seq, MCPM_TYPE_Q4_K, MCPM_TYPE_Q4_K, tv, to, td, s, nullptr)) s.G = -1;
+  return s;
+}
+
+static void check_fixed_shape() {
+  constexpr PdShape f = pd_fixed_plan();
+  static_assert(f.G == 256 && f.dim == 2304 && f.nbh == 23, "the fixed plan is the 2.4B shape on 256 CUs");
+  const int Q4 = MCPM_TYPE_Q4_K, Q6 = MCPM_TYPE_Q6_K;
+  const PdShape r = plan_of(cfg(40, 2304, 32, 8, 64, 5760), 256, 4096, Q6, Q4, Q6);
+  CHECK(r.G == 256 && std::memcmp(&r, &f, sizeof f) == 0, "compile-time plan differs from the run-time plan");
+  for (int L : {1, 3, 40, 62})
+    for (int ctx : {1, 64, 288, 1536, 4096})
+      CHECK(pd_fixed_shape(plan_of(cfg(L, 2304, 32, 8, 64, 5760), 256, ctx, Q6, Q4, Q6)),
+            "fixed shape not taken at %d layers, KV capacity %d", L, ctx);
+  struct Other {
+    const char* name;
+    mcpm_model_config c;
+    int n_cu, tv, to, td;
+  };
+  const Other others[] = {
+      {"Q4_K v/down", cfg(40, 2304, 32, 8, 64, 5760), 256, Q4, Q4, Q4},
+      {"Q4_K v", cfg(40, 2304, 32, 8, 64, 5760), 256, Q4, Q4, Q6},
+      {"Q4_K down", cfg(40, 2304, 32, 8, 64, 5760), 256, Q6, Q4, Q4},
+      {"FFN 5632", cfg(40, 2304, 32, 8, 64, 5632), 256, Q6, Q4, Q6},
+      {"hidden 2048", cfg(40, 2048, 32, 8, 64, 5760), 256, Q6, Q4, Q6},
+      {"small 8-kv", cfg(3, 1024, 32, 8, 64, 2816), 256, Q6, Q4, Q6},
+  };
+  for (const Other& o : others) {
+    const PdShape s = plan_of(o.c, o.n_cu, 512, o.tv, o.to, o.td);
+    CHECK(s.G > 0 && !pd_fixed_shape(s), "%s: %s", o.name, s.G > 0 ? "taken as the fixed shape" : "plan refused");
+  }
+  mcpm_model_config e = cfg(40, 2304, 32, 8, 64, 5760);
+  e.eps = 1e-5f;
+  CHECK(!pd_fixed_shape(plan_of(e, 256, 512, Q6, Q4, Q6)), "eps 1e-5 taken as the fixed shape");
+  std::printf("fixed-shape instance: plan %d B of LDS, taken for the 2.4B shape only\n", f.lds_bytes);
+}
+
 int main() {
   // the 2.4B shape on 256 CUs: the benchmark's context, the long-context
   // configuration's, and the longest the kernel takes
@@ -217,6 +261,7 @@ int main() {
   check_refused("head_dim 128", cfg(2, 2048, 16, 8, 128, 6144), 256, 64);
   check_refused("context past 2 chunks per work group", big, 256, 4160);
   check_refused("CU count not a multiple of 8", big, 252, 256);
+  check_fixed_shape();
   if (failures) std::printf("%d check(s) failed\n", failures);
   else std::printf("all persistent-kernel plan checks passed\n");
   return failures ? 1 : 0;
