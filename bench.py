@@ -46,8 +46,12 @@ def log(msg):
 
 
 # Decode kernels of this workload by class (the shapes the launch picker
-# chooses for the 2.4B-shaped model; names as rocprofv3 prints them).
+# chooses for the 2.4B-shaped model; names as rocprofv3 prints them, less
+# namespaces and arguments).
 PROFILE_CLASSES = {
+    # the default decode path: every layer of a token in one launch, the
+    # instance compiled for this shape with XCD-local hand-offs
+    "layers": "k_decode_persist<true, true>",
     "qkv": "k_gemv<3, 1, true, 2, false>",
     "attn": "k_attention_q8k",
     "oproj": "k_gemv<0, 2, true, 0, true>",
@@ -60,17 +64,19 @@ PROFILE_CLASSES = {
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
 
-def summarize_profiles(stats_csv, fetch_csv, write_csv, calib_bytes, out_path):
+def summarize_profiles(stats_csv, fetch_csv, write_csv, calib_bytes, out_path, run):
     """Per-class figures from three rocprofv3 runs of `bench.py --eager`: the
     kernel-trace statistics (average launch duration) and the FETCH_SIZE and
     WRITE_SIZE counters (KiB per dispatch, averaged over a class's
     dispatches), the counters scaled by what they read for the run's device
-    copies of calib_bytes (the largest copy dispatch)."""
+    copies of calib_bytes (the largest copy dispatch).  Classes with no
+    launch in these runs keep what out_path already holds for them (the
+    other decode path's runs); each class names the run it comes from."""
     import csv
 
     def short(name):
-        name = name.split("(")[0].replace("void ", "").replace("mcpm::", "")
-        return name.strip()
+        name = name.replace("(anonymous namespace)::", "").replace("void ", "").replace("mcpm::", "")
+        return name.split("(")[0].strip()
 
     stats = {short(r["Name"]): r for r in csv.DictReader(open(stats_csv))}
 
@@ -89,21 +95,27 @@ def summarize_profiles(stats_csv, fetch_csv, write_csv, calib_bytes, out_path):
     write, _, cw = counter(write_csv, "WRITE_SIZE")
     ff = calib_bytes / (cf * 1024) if cf else None
     fw = calib_bytes / (cw * 1024) if cw else None
-    classes = {}
+    old = {}
+    if os.path.exists(out_path):
+        with open(out_path) as f:
+            old = json.load(f)
+    classes = old.get("classes", {})
     for cls, kern in PROFILE_CLASSES.items():
-        e = {"kernel": kern}
-        if kern in stats:
-            e["kernel_calls"] = int(stats[kern]["Calls"])
-            e["kernel_avg_us"] = round(float(stats[kern]["AverageNs"]) / 1000.0, 3)
+        if kern not in stats:
+            continue
+        e = {"kernel": kern, "run": run, "kernel_calls": int(stats[kern]["Calls"]),
+             "kernel_avg_us": round(float(stats[kern]["AverageNs"]) / 1000.0, 3)}
         if kern in fetch and ff:
             e.update(dispatches=nf[kern], fetch_kib=round(fetch[kern], 1), write_kib=round(write.get(kern, 0.0), 1),
                      fetch_bytes=int(fetch[kern] * 1024 * ff), write_bytes=int(write.get(kern, 0.0) * 1024 * (fw or 1.0)))
         classes[cls] = e
-    out = {"workload": "greedy decode, 2.4B-shaped Q4_K_M decoder, eager launches",
-           "kernel_stats": os.path.basename(stats_csv),
-           "copy_calibration": {"bytes": calib_bytes, "fetch_kib": cf, "write_kib": cw,
-                                "fetch_factor": round(ff, 5) if ff else None, "write_factor": round(fw, 5) if fw else None},
-           "classes": classes}
+    runs = old.get("runs", {})
+    runs[run] = {"kernel_stats": os.path.basename(stats_csv),
+                 "copy_calibration": {"bytes": calib_bytes, "fetch_kib": cf, "write_kib": cw,
+                                      "fetch_factor": round(ff, 5) if ff else None,
+                                      "write_factor": round(fw, 5) if fw else None}}
+    out = {"workload": "greedy decode, 2.4B-shaped Q4_K_M decoder, eager launches", "runs": runs,
+           "classes": {k: classes[k] for k in PROFILE_CLASSES if k in classes}}
     with open(out_path, "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
@@ -133,26 +145,34 @@ def kernel_breakdown(eng, n_tokens=8):
     return out
 
 
-def persistent_measure(eng, prompt, steps, warmup, default_tps):
+PATH_LAUNCH = {"persistent": "one launch per token for every layer (one work group per CU), hipGraph per token",
+               "five_launch": "five launches per layer (QKV, attention, O, gate/up, down), hipGraph per token"}
+
+
+def other_path_measure(eng, prompt, steps, warmup, default_tps):
     """The same decode (prompt, warmup, then `steps` timed steps) through the
-    persistent launch (every layer of a token in one launch; off by default,
-    mcpm_engine_set_persistent), on the same engine and KV cache, graph
-    replay as the default launches; None where the shape does not fit it."""
-    eng.set_persistent(True)
+    decode path the default does not take, on the same engine and KV cache,
+    graph replay as the default: five launches per layer where the default
+    is the persistent launch (mcpm_engine_set_persistent mode 0; with their
+    per-class kernel timings), else the persistent launch wherever the shape
+    fits (mode 1; None where it does not).  The default mode is restored."""
+    persistent_default = eng.uses_persistent()
+    eng.set_persistent(0 if persistent_default else 1)
     try:
-        if not eng.uses_persistent():
-            return None
+        if not persistent_default and not eng.uses_persistent():
+            return None, None
         eng.generate_greedy(prompt, 1 + warmup)
         eng.sync()
         t0 = time.perf_counter()
         eng.decode_steps(steps)
         eng.sync()
         dt = time.perf_counter() - t0
-        return {"tokens_per_s": round(steps / dt, 2), "ms_per_step": round(1e3 * dt / steps, 4),
-                "over_default_launches": round(steps / dt / default_tps, 4),
-                "launch": "one launch per token for every layer (one work group per CU), hipGraph per token"}
+        name = "five_launch" if persistent_default else "persistent"
+        out = {"path": name, "tokens_per_s": round(steps / dt, 2), "ms_per_step": round(1e3 * dt / steps, 4),
+               "over_default": round(steps / dt / default_tps, 4), "launch": PATH_LAUNCH[name]}
+        return out, kernel_breakdown(eng) if persistent_default else None
     finally:
-        eng.set_persistent(False)
+        eng.set_persistent(mcpm.PERSIST_AUTO)
 
 
 def prefill_measure(eng, cfg, n_prompt=1024, reps=3):
@@ -271,6 +291,7 @@ def ops_measure(ctx, eng, cfg, bd, cold_mb=640):
     kvd = cfg.n_kv_heads * cfg.head_dim
     qkv_w = eng.kernel_bytes(mcpm.KC_QKV)
     c3 = {}
+    eng.set_persistent(0)  # the five launches' QKV and attention kernels
     eng.init_kv_cache(4096 + 64)
     for ctx_len in (512, 2048, 4096):
         prompt = np.random.default_rng(SEED + ctx_len).integers(0, cfg.vocab, ctx_len).astype(np.int32)
@@ -291,6 +312,7 @@ def ops_measure(ctx, eng, cfg, bd, cold_mb=640):
                             "bytes": b, "GBps": round(b / (t * 1e-6) / 1e9, 1),
                             "frac": round(b / (t * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
     out["c3_qkv_attention"] = c3
+    eng.set_persistent(mcpm.PERSIST_AUTO)
     return out
 
 
@@ -443,8 +465,9 @@ def main():
     ap.add_argument("--mix", type=int, default=0, help="0: Q6_K v/down in every layer; 1: llama.cpp layers")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of a graph replay")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 1024-token prefill measurement")
-    ap.add_argument("--no-persistent", action="store_true",
-                    help="skip the same decode through the persistent launch (opt-in, off by default)")
+    ap.add_argument("--no-other-path", "--no-persistent", dest="no_other_path", action="store_true",
+                    help="skip the same decode through the decode path the default does not take (five launches "
+                         "per layer where the default is the persistent launch)")
     ap.add_argument("--no-sampled", action="store_true",
                     help="skip the sampled decode after a 1024-token prompt (device sampler)")
     ap.add_argument("--no-ops", action="store_true",
@@ -454,9 +477,12 @@ def main():
                          "size for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--summarize-profiles", nargs=3, metavar=("STATS_CSV", "FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/decode_2p4b_traffic.json from rocprofv3 outputs and exit (no GPU)")
+    ap.add_argument("--profile-run", default="default decode path",
+                    help="with --summarize-profiles: the name the classes of these runs are filed under")
     args = ap.parse_args()
     if args.summarize_profiles:
-        out = summarize_profiles(*args.summarize_profiles, (args.copy_calibration_mb or 256) << 20, TRAFFIC_FILE)
+        out = summarize_profiles(*args.summarize_profiles, (args.copy_calibration_mb or 256) << 20, TRAFFIC_FILE,
+                                 args.profile_run)
         print(json.dumps(out["classes"]))
         return
     if args.gpus != 1:
@@ -489,7 +515,8 @@ def main():
     dt = t1 - t0
     tps = args.steps / dt
     wbytes = eng.weight_bytes_per_token()
-    log(f"decode: {args.steps} tokens in {dt * 1e3:.1f} ms -> {tps:.1f} tok/s, "
+    path = "persistent" if eng.uses_persistent() else "five_launch"
+    log(f"decode ({path.replace('_', ' ')}): {args.steps} tokens in {dt * 1e3:.1f} ms -> {tps:.1f} tok/s, "
         f"{wbytes * tps / 1e9:.1f} GB/s effective")
 
     # per-kernel durations with HIP events (eager launches of the same kernels)
@@ -502,12 +529,26 @@ def main():
             f"= {v['us_per_token']:8.1f} us/token  "
             f"{v['bytes_per_launch'] / (v['avg_us'] * 1e-6) / 1e9 if v['bytes_per_launch'] and v['avg_us'] else 0:7.1f} GB/s")
 
-    persistent = None
-    if not args.no_persistent and not args.eager:
-        persistent = persistent_measure(eng, prompt, args.steps, args.warmup, tps)
-        if persistent:
-            log(f"persistent launch, same decode: {persistent['tokens_per_s']:.1f} tok/s "
-                f"({persistent['over_default_launches']:.3f} of the default launches)")
+    other, bd_five = None, None
+    if not args.no_other_path and not args.eager:
+        other, bd_five = other_path_measure(eng, prompt, args.steps, args.warmup, tps)
+        if other:
+            log(f"{other['path'].replace('_', ' ')} path, same decode: {other['tokens_per_s']:.1f} tok/s "
+                f"({other['over_default']:.3f} of the default path)")
+    if path == "five_launch":
+        bd_five = bd
+    elif bd_five is None and not args.no_ops:
+        # the single-op figures and the read floor take the five launches'
+        # per-class timings, at the same contexts
+        eng.set_persistent(0)
+        eng.generate_greedy(prompt, 1 + args.warmup)
+        eng.decode_steps(args.steps)
+        bd_five = kernel_breakdown(eng)
+        eng.set_persistent(mcpm.PERSIST_AUTO)
+    if bd_five is not bd and bd_five:
+        log("  five launches per layer, per class:")
+        for k, v in bd_five.items():
+            log(f"  {k:8s} {v['avg_us']:8.2f} us x {v['launches_per_token']:.0f}/token = {v['us_per_token']:8.1f} us/token")
 
     if args.copy_calibration_mb > 0:
         nbytes = args.copy_calibration_mb << 20
@@ -535,13 +576,13 @@ def main():
 
     ops = None
     if not args.no_ops:
-        ops = ops_measure(ctx, eng, cfg, bd)
+        ops = ops_measure(ctx, eng, cfg, bd_five)
         c1 = ops["c1_gemv_q4k_5760x2304"]
         log(f"ops: C1 GEMV {c1['warm']['us']:.2f} us warm ({c1['warm']['GBps']:.0f} GB/s), "
             f"{c1['cold']['us']:.2f} us cold ({c1['cold']['GBps']:.0f} GB/s); "
             f"C2 FFN block {ops['c2_ffn_block']['us']:.2f} us; C3 QKV+attention "
             + ", ".join(f"{k}: {v['us']:.2f} us" for k, v in ops["c3_qkv_attention"].items()))
-        rf = read_floor_measure(ctx, bd)
+        rf = read_floor_measure(ctx, bd_five)
         ops["read_floor"] = rf
         log("read floor (one read-only launch of each GEMV class's bytes): "
             + ", ".join(f"{k} {v['floor_us']:.2f} us vs {v['kernel_us']:.2f}" for k, v in rf["classes"].items())
@@ -583,7 +624,8 @@ def main():
         "config": {"workload": "greedy decode, batch 1, 2.4B-shaped Q4_K_M decoder", "layers": cfg.n_layers,
                    "hidden": cfg.dim, "heads": f"{cfg.n_heads}q/{cfg.n_kv_heads}kv x {cfg.head_dim}",
                    "ffn": cfg.ffn, "vocab": cfg.vocab, "quant_mix": "literal" if args.mix == 0 else "llama",
-                   "launch": "eager" if args.eager else "hipGraph per token", "prompt_tokens": PROMPT, "context_at_end": PROMPT + args.warmup + args.steps,
+                   "launch": "eager" if args.eager else "hipGraph per token", "decode_path": path,
+                   "prompt_tokens": PROMPT, "context_at_end": PROMPT + args.warmup + args.steps,
                    "weight_bytes_per_token": wbytes, "effective_GBps": round(wbytes * tps / 1e9, 1),
                    "token_roofline_frac": round(wbytes * tps / 1e9 / HBM_PEAK_GBPS, 4),
                    "eager_kernels_us_per_token": {k: round(v["us_per_token"], 2) for k, v in bd.items()},
@@ -596,7 +638,8 @@ def main():
                      "timing": "eager launches of the class, HIP events around each kernel on the engine stream",
                      "rocprof": prof},
         "cpu_baseline": cpu,
-        "persistent_decode": persistent,
+        "decode_paths": {"default": path, path: {"tokens_per_s": round(tps, 2), "launch": PATH_LAUNCH[path]},
+                         **({other["path"]: other} if other else {})},
         "prefill": prefill,
         "sampled_decode": sampled,
         "ops": ops,

@@ -258,17 +258,28 @@ int mcpm_sample_logits(const float *logits, int n, float temperature, float top_
 /* 1: replay each token as one captured hipGraph (default); 0: eager launches. */
 int mcpm_engine_set_graph(mcpm_engine *e, int enable);
 
-/* 1 (MCPM_PERSIST=1 in the environment at load sets it; default 0): where
- * the model's shape and the KV capacity fit (8 kv heads of 64, 4 query heads
- * per kv head, a CU count that is a multiple of 8, at most 2 attention chunks
- * of 64 positions per CU), every layer of a token runs in one persistent
- * launch, the per-token loop of MiniCPM5Engine::forward (src/model.cpp:171-226)
- * as one kernel; 0: five launches per layer.  Results are the same.  While
- * it is on (and a KV cache is set up) the engine holds the launch's weight
- * slab, the layer weights once more in the launch's layout; 0 frees it. */
-int mcpm_engine_set_persistent(mcpm_engine *e, int enable);
+/* Where every layer of a token runs in one persistent launch, the per-token
+ * loop of MiniCPM5Engine::forward (src/model.cpp:171-226) as one kernel,
+ * instead of five launches per layer.  Results are the same.
+ *   1: wherever the model's shape and the KV capacity fit (8 kv heads of 64,
+ *      4 query heads per kv head, a CU count that is a multiple of 8, at
+ *      most 2 attention chunks of 64 positions per CU);
+ *   2 (the default): only where the launch also has an instance compiled for
+ *      the shape (every plan field a constant): the 2.4B-shaped decoder
+ *      (hidden 2304, 32/8 heads of 64, FFN 5760, Q4_K q/k/o/gate/up, Q6_K
+ *      v/down, any layer count) on 256 CUs with a KV capacity of at most
+ *      4096 positions;
+ *   0: never.
+ * MCPM_PERSIST=0/1/2 in the environment at load sets the mode.  While the
+ * launch is taken the engine holds its weight slab, the layer weights once
+ * more in the launch's layout; mode 0 frees it, and so does mode 2 for a
+ * shape it does not take.  MCPM_ERR_ARG for another mode. */
+int mcpm_engine_set_persistent(mcpm_engine *e, int mode);
 /* 1 when the next token runs its layers in one launch. */
 int mcpm_engine_uses_persistent(const mcpm_engine *e);
+/* 1 when that launch is the instance compiled for the model's shape.  No
+ * counterpart in the reference. */
+int mcpm_engine_persistent_fixed_shape(const mcpm_engine *e);
 /* 1 when that launch also hands the records read on one XCD only (a kv
  * head's q/k/v rows, its attention chunks' partials) through that XCD's L2:
  * set up when every work group b runs on the XCD of work group b % 8

@@ -134,7 +134,9 @@ struct mcpm_engine {
   // the plan for the current KV cache, each work group's weight slabs, the
   // hand-off records, launch count and error word, and the launch's
   // arguments in device memory
-  bool pd_want = false;  // MCPM_PERSIST=1 or mcpm_engine_set_persistent(1) turn it on
+  // 0 off, 1 wherever the shape fits, 2 (default) where the launch has a
+  // compiled instance for the shape (MCPM_PERSIST, mcpm_engine_set_persistent)
+  int pd_mode = 2;
   bool pd_ready = false;
   PdShape pd{};
   PdLayer* d_pd_layers = nullptr;
@@ -361,7 +363,7 @@ int load_from_image(mcpm_ctx* ctx, const uint8_t* data, size_t size, mcpm_engine
     const char* a = std::getenv("MCPM_FUSED_ATTN");
     e->fused_attn = a && std::atoi(a) != 0;
     const char* pv = std::getenv("MCPM_PERSIST");
-    e->pd_want = pv && std::atoi(pv) != 0;
+    if (pv) e->pd_mode = std::atoi(pv) == 0 ? 0 : std::atoi(pv) == 2 ? 2 : 1;
   }
   *out = e;
   return MCPM_OK;
@@ -491,7 +493,7 @@ int enqueue_token(mcpm_engine* e, bool short_ctx, bool one_chunk) {
   const int* st = reinterpret_cast<const int*>(e->st);
   const bool in_o = one_chunk && e->attn_in_o && !e->fused_attn;
   const bool q8k = short_ctx && e->attn_q8k && !e->fused_attn && !in_o;
-  const bool persist = e->pd_ready && e->pd_want;
+  const bool persist = e->pd_ready && e->pd_mode != 0;
   if (persist)
     MCPM_HIP(timed(e, MCPM_KC_LAYERS, [&] { return launch_decode_persist(e->pd_args, s); }));
   else
@@ -784,7 +786,7 @@ void pd_release(mcpm_engine* e) {
 int pd_setup(mcpm_engine* e) {
   e->pd_ready = false;
   const mcpm_model_config& c = e->cfg;
-  if (!e->pd_want) {
+  if (e->pd_mode == 0) {
     pd_release(e);
     return MCPM_OK;
   }
@@ -792,8 +794,12 @@ int pd_setup(mcpm_engine* e) {
   const Layer& L0 = e->L[0];
   PdShape s{};
   const char* why = nullptr;
-  if (!pd_plan(c, e->ctx->n_cu, e->max_seq, L0.wq.type, L0.wk.type, L0.wv.type, L0.wo.type, L0.wd.type, s, &why))
+  if (!pd_plan(c, e->ctx->n_cu, e->max_seq, L0.wq.type, L0.wk.type, L0.wv.type, L0.wo.type, L0.wd.type, s, &why) ||
+      (e->pd_mode == 2 && !pd_fixed_shape(s))) {
+    // the default mode holds no slab for a shape it does not take
+    if (e->pd_mode == 2) pd_release(e);
     return MCPM_OK;
+  }
   if (prepare_decode_persist(s) != hipSuccess) return MCPM_OK;
   // every layer must have the first layer's types (the slab layout's)
   for (const Layer& l : e->L)
@@ -981,16 +987,20 @@ int mcpm_engine_set_graph(mcpm_engine* e, int enable) {
   return MCPM_OK;
 }
 
-int mcpm_engine_set_persistent(mcpm_engine* e, int enable) {
-  if (!e) return fail(MCPM_ERR_ARG, "mcpm_engine_set_persistent: null engine");
+int mcpm_engine_set_persistent(mcpm_engine* e, int mode) {
+  if (!e || mode < 0 || mode > 2) return fail(MCPM_ERR_ARG, "mcpm_engine_set_persistent: bad argument");
   MCPM_HIP(hipStreamSynchronize(e->ctx->stream));
   drop_graph(e);
-  if ((enable != 0) == e->pd_want && (e->pd_ready || !enable || !e->kc)) return MCPM_OK;
-  e->pd_want = enable != 0;
+  if (mode == e->pd_mode && (e->pd_ready || !mode || !e->kc)) return MCPM_OK;
+  e->pd_mode = mode;
   return pd_setup(e);  // builds the slab (with a KV cache) or releases it
 }
 
-int mcpm_engine_uses_persistent(const mcpm_engine* e) { return e && e->pd_ready && e->pd_want ? 1 : 0; }
+int mcpm_engine_uses_persistent(const mcpm_engine* e) { return e && e->pd_ready && e->pd_mode ? 1 : 0; }
+
+int mcpm_engine_persistent_fixed_shape(const mcpm_engine* e) {
+  return mcpm_engine_uses_persistent(e) && pd_fixed_shape(e->pd) ? 1 : 0;
+}
 
 int mcpm_engine_persistent_xcd_local(const mcpm_engine* e) {
   return mcpm_engine_uses_persistent(e) && e->pd_args.xcd_local ? 1 : 0;

@@ -17,6 +17,8 @@ LIB_PATH = os.path.join(PKG_DIR, "libmcpm_hip.so")
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
 KC_QKV, KC_ATTN, KC_OPROJ, KC_GATE_UP, KC_DOWN, KC_LM_HEAD, KC_LAYERS = range(7)
+# mcpm_engine_set_persistent's default mode
+PERSIST_AUTO = 2
 KC_NAMES = ["qkv", "attn", "oproj", "gate_up", "down", "lm_head", "layers"]
 # include/mcpm_hip.h error codes
 ERR_HIP, ERR_ARG, ERR_UNSUPPORTED, ERR_CONTEXT, ERR_IO, ERR_FORMAT, ERR_NOMEM = -1, -2, -3, -4, -5, -6, -7
@@ -125,6 +127,7 @@ _SIGS = {
     "mcpm_engine_set_graph": (_I, [_P, _I]),
     "mcpm_engine_set_persistent": (_I, [_P, _I]),
     "mcpm_engine_uses_persistent": (_I, [_P]),
+    "mcpm_engine_persistent_fixed_shape": (_I, [_P]),
     "mcpm_engine_persistent_xcd_local": (_I, [_P]),
     "mcpm_engine_set_spin_limit": (_I, [_P, C.c_uint]),
     "mcpm_set_op_timing": (_I, [_P, _I]),
@@ -392,11 +395,17 @@ class Engine:
     def set_graph(self, enable: bool):
         check(self.lib.mcpm_engine_set_graph(self.h, int(enable)))
 
-    def set_persistent(self, enable: bool):
-        check(self.lib.mcpm_engine_set_persistent(self.h, int(enable)))
+    def set_persistent(self, mode):
+        """False/0: five launches per layer; True/1: the persistent launch
+        wherever the shape fits; PERSIST_AUTO (2, the default): only where it
+        has an instance compiled for the shape."""
+        check(self.lib.mcpm_engine_set_persistent(self.h, int(mode)))
 
     def uses_persistent(self) -> bool:
         return bool(self.lib.mcpm_engine_uses_persistent(self.h))
+
+    def persistent_fixed_shape(self) -> bool:
+        return bool(self.lib.mcpm_engine_persistent_fixed_shape(self.h))
 
     def persistent_xcd_local(self) -> bool:
         return bool(self.lib.mcpm_engine_persistent_xcd_local(self.h))

@@ -153,18 +153,26 @@ def _sha(a):
     return hashlib.sha256(np.ascontiguousarray(a).view(np.uint8).tobytes()).hexdigest()
 
 
-@pytest.fixture(scope="module")
-def full_engine(ctx):
+@pytest.fixture(scope="module", params=["persistent", "five-launch"])
+def full_engine(ctx, request):
     """The 2.4B-shaped model of the benchmark (40 layers, 2304 hidden, 32/8
     heads of 64, FFN 5760, vocab 130560, tied Q6_K head, Q6_K v/down), KV
-    capacity 1536."""
+    capacity 1536: through the default decode path (every layer of a token
+    in one persistent launch, the instance compiled for this shape) and
+    through five launches per layer."""
     g = golden("full_model_oracle.npz")
-    announce("full model synth")
+    announce(f"full model synth ({request.param})")
     img = mcpm.synth_gguf(mcpm.config_2p4b(), seed=int(g["seed"]), mix=0)
     assert _sha(img) == str(g["image_sha"]), "model generator changed"
     e = mcpm.Engine(ctx, image=img)
     del img
+    if request.param == "five-launch":
+        e.set_persistent(False)
     e.init_kv_cache(1536)
+    if request.param == "persistent":
+        assert e.uses_persistent() and e.persistent_fixed_shape(), "the default decode path of the 2.4B shape"
+    else:
+        assert not e.uses_persistent()
     yield e
     e.free()
 
@@ -398,6 +406,7 @@ def test_fused_ffn_block_matches_oracle(ctx, small_image, monkeypatch):
     e = mcpm.Engine(ctx, image=img)
     del img
     try:
+        e.set_persistent(False)  # the fused FFN runs on the five-launch path
         e.init_kv_cache(128)
         np.testing.assert_array_equal(e.generate_greedy(gf["prompt"], 32), gf["tokens"][:32])
     finally:
@@ -485,6 +494,7 @@ def test_fused_qkv_attention_matches_oracle(ctx, small_image, monkeypatch, case)
         e = mcpm.Engine(ctx, image=img)
         del img
         try:
+            e.set_persistent(False)  # the fused launch runs on the five-launch path
             e.init_kv_cache(128)
             np.testing.assert_array_equal(e.generate_greedy(gf["prompt"], 32), gf["tokens"][:32])
         finally:

@@ -31,10 +31,18 @@ def engines(ctx, kv8_image):
     b.free()
 
 
-def test_off_by_default_and_taken_when_asked(ctx, kv8_image, engines):
+def test_default_mode_and_taken_when_asked(ctx, kv8_image, engines):
+    """The default mode takes the persistent launch only for a shape it has
+    a compiled instance of: not this one, which mode 1 takes."""
     e = mcpm.Engine(ctx, image=kv8_image)
     e.init_kv_cache(64)
     assert not e.uses_persistent()
+    e.set_persistent(True)
+    assert e.uses_persistent() and not e.persistent_fixed_shape()
+    e.set_persistent(mcpm.PERSIST_AUTO)
+    assert not e.uses_persistent()
+    with pytest.raises(mcpm.McpmError):
+        e.set_persistent(3)
     e.free()
     a, b = engines
     a.init_kv_cache(256)
@@ -174,20 +182,27 @@ def test_hand_off_give_up_then_recovers(engines, kv8_image):
 
 
 # The 2.4B shape's own plan (hidden 2304, FFN 5760: 23 blocks of h, the
-# single-wait down prologue, staging in the down region) on 3 layers
+# single-wait down prologue, staging in the down region) on 3 layers: the
+# shape the launch has an instance compiled for (every plan field but the
+# layer and chunk counts a constant), taken by default
 SHAPE24 = dict(n_layers=3, dim=2304, n_heads=32, n_kv_heads=8, head_dim=64, ffn=5760, vocab=4096)
 
 
-def test_2p4b_shape_vs_oracle_and_five_launch_path(ctx):
-    img = mcpm.synth_gguf(mcpm.make_config(**SHAPE24), seed=23, mix=0)
+@pytest.fixture(scope="module")
+def shape24_image():
+    return mcpm.synth_gguf(mcpm.make_config(**SHAPE24), seed=23, mix=0)
+
+
+def test_2p4b_shape_vs_oracle_and_five_launch_path(ctx, shape24_image):
+    img = shape24_image
     a = mcpm.Engine(ctx, image=img)
     b = mcpm.Engine(ctx, image=img)
     try:
-        a.set_persistent(True)
+        b.set_persistent(False)
         a.init_kv_cache(512)
         b.init_kv_cache(512)
         assert a.uses_persistent() and not b.uses_persistent()
-        assert a.persistent_xcd_local()
+        assert a.persistent_fixed_shape() and a.persistent_xcd_local()
         om = O.OracleModel(img)
         om.init_kv(512)
         rng = np.random.default_rng(8)
@@ -208,8 +223,35 @@ def test_2p4b_shape_vs_oracle_and_five_launch_path(ctx):
         a.set_persistent(False)
         assert not a.uses_persistent()
         a.set_persistent(True)
-        assert a.uses_persistent()
+        assert a.uses_persistent() and a.persistent_fixed_shape()
         np.testing.assert_array_equal(a.generate_greedy(prompt[:50], 32), b.generate_greedy(prompt[:50], 32))
+        # past 4096 positions (three chunks for some work groups) the default
+        # mode runs the five launches and holds no slab
+        a.init_kv_cache(4160)
+        assert not a.uses_persistent()
+        a.init_kv_cache(512)
+        assert a.uses_persistent()
+    finally:
+        a.free()
+        b.free()
+
+
+def test_2p4b_shape_agent_scope_hand_offs(ctx, shape24_image, monkeypatch):
+    """MCPM_PD_XCD_LOCAL=0 on the compiled shape: every record at agent
+    scope, the same greedy and sampled tokens as the five launches."""
+    monkeypatch.setenv("MCPM_PD_XCD_LOCAL", "0")
+    a = mcpm.Engine(ctx, image=shape24_image)
+    b = mcpm.Engine(ctx, image=shape24_image)
+    try:
+        b.set_persistent(False)
+        a.init_kv_cache(512)
+        b.init_kv_cache(512)
+        assert a.uses_persistent() and a.persistent_fixed_shape() and not a.persistent_xcd_local()
+        prompt = np.arange(7, 40, dtype=np.int32)
+        announce("2.4B-shaped persistent, agent-scope hand-offs, vs five launches")
+        np.testing.assert_array_equal(a.generate_greedy(prompt, 64), b.generate_greedy(prompt, 64))
+        np.testing.assert_array_equal(a.generate_sampled(prompt, 100, 0.9, 0.95, 3),
+                                      b.generate_sampled(prompt, 100, 0.9, 0.95, 3))
     finally:
         a.free()
         b.free()
