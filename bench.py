@@ -6,16 +6,20 @@ Workload (the full 2.4B-shaped model): 40 layers, hidden 2304,
 head, Q6_K attn_v / ffn_down, Q4_K elsewhere, F32 norms; random-init weights
 N(0, 0.02) from a fixed seed; a 32-token random-ID prompt, then greedy decode.
 A step is one decoded token (one captured hipGraph replay of the whole
-forward plus argmax on the device).  --warmup steps run untimed, then exactly
---steps steps are timed between device synchronisations.
+forward plus argmax on the device) through the engine's default decode path:
+every layer of the token in one persistent launch where that launch has an
+instance compiled for the shape (this one, on 256 CUs), else five launches
+per layer.  --warmup steps run untimed, then exactly --steps steps are timed
+between device synchronisations.
 
 Printed: one JSON line with tokens/s, the achieved HBM bandwidth of the
 dominant kernel against the 8 TB/s peak (HIP events around its launches, on
 the engine stream), and the reference's CPU path timed on this host's cores;
-beside them the long-context prefill and sampled decode, and the single-op
-configurations (one GEMV cold and warm, the FFN block, QKV + attention)
-with, for each GEMV class, one read-only launch of its bytes as the floor a
-single launch of that size can reach.
+beside them the same decode through the other decode path, the long-context
+prefill and sampled decode, and the single-op configurations (one GEMV cold
+and warm, the FFN block, QKV + attention) with, for each GEMV class of the
+five-launch path, one read-only launch of its bytes as the floor a single
+launch of that size can reach.
 """
 import argparse
 import platform
@@ -523,7 +527,6 @@ def main():
     bd = kernel_breakdown(eng)
     dom = max(bd, key=lambda k: bd[k]["us_per_token"])
     d = bd[dom]
-    achieved = d["bytes_per_launch"] / (d["avg_us"] * 1e-6) / 1e9
     for k, v in bd.items():
         log(f"  {k:8s} {v['avg_us']:8.2f} us x {v['launches_per_token']:.0f}/token "
             f"= {v['us_per_token']:8.1f} us/token  "
@@ -589,18 +592,37 @@ def main():
             + f"; GEMVs {rf['gemv_us_per_token']:.0f} us/token, floor {rf['floor_us_per_token']:.0f} us/token "
             f"({100 * rf['floor_over_gemv_per_token']:.0f} %)")
 
-    traffic, prof = None, None
+    traffic_classes = {}
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            tr = json.load(f).get("classes", {}).get(dom)
-        if tr and "fetch_bytes" in tr:
-            traffic = int(tr["fetch_bytes"] + tr["write_bytes"])
-        if tr and tr.get("kernel_avg_us"):
-            # the same class's launches timed by rocprofv3 (eager run, the
-            # committed kernel statistics) beside this run's HIP events
+            traffic_classes = json.load(f).get("classes", {})
+
+    def roofline_of(cls, d):
+        """The class's achieved HBM rate (algorithmic bytes per launch over
+        this run's HIP-event launch time), with the committed rocprofv3
+        figures for it: read + written bytes per launch, and its average
+        launch time from the kernel statistics of the same decode path."""
+        tr = traffic_classes.get(cls, {})
+        a = d["bytes_per_launch"] / (d["avg_us"] * 1e-6) / 1e9
+        prof = None
+        if tr.get("kernel_avg_us"):
             pa = d["bytes_per_launch"] / (tr["kernel_avg_us"] * 1e-6) / 1e9
-            prof = {"source": "profiles/decode_2p4b_kernel_stats.md", "avg_launch_us": tr["kernel_avg_us"],
-                    "achieved": round(pa, 1), "frac": round(pa / HBM_PEAK_GBPS, 4)}
+            src = "decode_2p4b_persistent_kernel_stats.md" if "persistent" in tr.get("run", "") \
+                else "decode_2p4b_kernel_stats.md"
+            prof = {"source": "profiles/" + src, "avg_launch_us": tr["kernel_avg_us"], "achieved": round(pa, 1),
+                    "frac": round(pa / HBM_PEAK_GBPS, 4)}
+        return {"bound": "hbm", "kernel": cls, "achieved": round(a, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(a / HBM_PEAK_GBPS, 4),
+                "traffic": int(tr["fetch_bytes"] + tr["write_bytes"]) if "fetch_bytes" in tr else None,
+                "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 3),
+                "timing": "eager launches of the class, HIP events around each kernel on the engine stream",
+                "rocprof": prof}
+
+    roofline = roofline_of(dom, d)
+    if bd_five is not bd and bd_five:
+        # the five launches' dominant GEMV class, for comparison
+        d5 = max(bd_five, key=lambda k: bd_five[k]["us_per_token"])
+        roofline["five_launch_dominant"] = roofline_of(d5, bd_five[d5])
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -632,11 +654,7 @@ def main():
                    "eager_kernels_sum_us_per_token": round(sum(v["us_per_token"] for v in bd.values()), 1),
                    "eager_sum_over_graph_step": round(sum(v["us_per_token"] for v in bd.values())
                                                       / (1e6 * dt / args.steps), 4)},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 3),
-                     "timing": "eager launches of the class, HIP events around each kernel on the engine stream",
-                     "rocprof": prof},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "decode_paths": {"default": path, path: {"tokens_per_s": round(tps, 2), "launch": PATH_LAUNCH[path]},
                          **({other["path"]: other} if other else {})},
