@@ -35,8 +35,10 @@
 // before the one that reads it: O at Q; the next layer's QKV, this layer's
 // gate/up and down at O (at A on the work groups that combine attention
 // chunks, which wait there for the chunks' partials).  The wait ends with
-// every copy landed.  The chunk owners' K and V rows go into the down region
-// at Q, the attention's staging.
+// every copy landed.  The chunk owners' K and V rows go into the gate/up
+// region at the previous layer's D (where that region holds them; the
+// combining work group's into the down region at Q), the attention's
+// staging.
 //
 // Every wait is bounded: past spin_limit, or once another work group has
 // given up, the work group sets the error word and returns.
@@ -539,6 +541,32 @@ __device__ __forceinline__ void pd_copy_region(const PdArgs& a, uint8_t* LDS, in
   pd_copy(pd_slab<FS>(a, l, r), LDS + s.reg_off[r], s.reg_sz[r]);
 }
 
+// Whether chunk owner k (k < the chunk count) stages its layer's chunk
+// early, into the gate/up region during the previous layer's D (layer 0's
+// at E): where that region holds the attention's staging, on every owner
+// but the combining work group (k = W-1), which takes its gate/up copy at
+// A and stages into the down region at Q.
+__device__ __forceinline__ bool pd_stage_early(const PdShape& s, int k) {
+  return s.reg_sz[2] >= PD_ATTN_LDS && k != s.W - 1;
+}
+
+// The attention staging of chunk k's owner: the gate/up region when it
+// stages early, else the down region.
+__device__ __forceinline__ int pd_stage_off(const PdShape& s, int k) {
+  return pd_stage_early(s, k) ? s.reg_off[2] : s.reg_off[3];
+}
+
+// Chunk k of layer l's K and V rows of this work group's kv head (context
+// pos + 1) into its attention staging.
+template <bool FS>
+__device__ __forceinline__ void pd_stage_layer(const PdArgs& a, int l, int k, int pos, uint8_t* LDS) {
+  const PdShape& s = pd_s<FS>(a);
+  const size_t lay = static_cast<size_t>(l) * a.max_seq * s.kvd;
+  pd_stage_chunk(a.kc + lay, a.vc + lay, k, pos + 1, s.kvd,
+                 static_cast<size_t>(static_cast<int>(blockIdx.x) % PD_XCDS) * s.hd, a.norms,
+                 LDS + pd_stage_off(s, k));
+}
+
 // Q (kind 0), O (2), G (3) or D (4) of layer l.
 template <bool XL, bool FS>
 __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_t* LDS, uint32_t* S, uint32_t tag,
@@ -608,13 +636,15 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // chunk, whose staging holds the down region until then).
   if (kind == 0) {
     pd_copy_region<FS>(a, LDS, l, 1);
-    // this layer's attention chunk (the down region is free until G)
-    if (me.k < (pos + ATTN_CHUNK) / ATTN_CHUNK) {
-      const size_t lay = static_cast<size_t>(l) * a.max_seq * s.kvd;
-      pd_stage_chunk(a.kc + lay, a.vc + lay, me.k, pos + 1, s.kvd, static_cast<size_t>(me.kvh) * s.hd, a.norms,
-                     LDS + s.reg_off[3]);
-    }
+    // this layer's attention chunk (the down region is free until G), where
+    // it was not staged at the previous layer's D
+    if (me.k < (pos + ATTN_CHUNK) / ATTN_CHUNK && !pd_stage_early(s, me.k)) pd_stage_layer<FS>(a, l, me.k, pos, LDS);
   }
+  // the next layer's attention chunk, into the gate/up region (free from the
+  // end of G until this work group's next gate/up copy at O, after A), so
+  // that the copy lands during this phase's wait instead of the next Q's
+  if (kind == 4 && l + 1 < a.s.L && me.k < (pos + ATTN_CHUNK) / ATTN_CHUNK && pd_stage_early(s, me.k))
+    pd_stage_layer<FS>(a, l + 1, me.k, pos, LDS);
   if (kind == 2 && me.k != s.W - 1) {
     if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
     pd_copy_region<FS>(a, LDS, l, 2);
@@ -810,7 +840,7 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
   }
   constexpr int HD = 64, GH = 256, OPT = ATTN_MAX_GROUP * HD / 256;
   const int group = s.group, kvd = s.kvd;
-  const AttnLds<HD> A(reinterpret_cast<float*>(LDS + s.reg_off[3]));
+  const AttnLds<HD> A(reinterpret_cast<float*>(LDS + pd_stage_off(s, k)));
   float* kr = reinterpret_cast<float*>(S + s.s_u);
   float* vr = kr + HD;
   float* sX = vr + HD;       // [GH] the combined output
@@ -879,6 +909,9 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
         rec_stf_xcd<XL>(pr + GH + group + t, mz.y, tag);
       }
     }
+    // (m_c, z_c) are read from the staging, which the next phase's weight
+    // copies overwrite
+    pd_bar();
     return true;
   }
   // The combining work group takes the chunks in chunk order with the
@@ -1027,6 +1060,10 @@ __global__ void __launch_bounds__(256) k_decode_persist(const PdArgs a) {
     }
   }
   pd_copy_region<FS>(a, LDS, 0, 0);
+  {
+    const int k = static_cast<int>(blockIdx.x) / PD_XCDS;
+    if (k < (pos + ATTN_CHUNK) / ATTN_CHUNK && pd_stage_early(pd_s<FS>(a), k)) pd_stage_layer<FS>(a, 0, k, pos, LDS);
+  }
   // one loop over the phases, so that each phase's code exists once
 #pragma unroll 1
   for (int ph = 0; ph < 5 * L; ++ph) {
