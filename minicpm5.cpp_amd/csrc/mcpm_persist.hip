@@ -645,7 +645,9 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // that the copy lands during this phase's wait instead of the next Q's
   if (kind == 4 && l + 1 < a.s.L && me.k < (pos + ATTN_CHUNK) / ATTN_CHUNK && pd_stage_early(s, me.k))
     pd_stage_layer<FS>(a, l + 1, me.k, pos, LDS);
-  if (kind == 2 && me.k != s.W - 1) {
+  // (with one chunk the combining work group has nothing to wait for at A,
+  // where the chunk's owner finishes the head, and takes its copies here)
+  if (kind == 2 && (me.k != s.W - 1 || pos < ATTN_CHUNK)) {
     if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
     pd_copy_region<FS>(a, LDS, l, 2);
     pd_copy_region<FS>(a, LDS, l, 3);
@@ -831,7 +833,9 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
             k = static_cast<int>(blockIdx.x) / PD_XCDS, W = s.W;
   uint32_t* misc = S + s.s_misc;
   const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
-  const bool combiner = k == W - 1;
+  // one chunk: its owner finishes the head (the combine of one chunk is the
+  // chunk's own o_c / z_c), so no partials go to the combining work group
+  const bool combiner = k == W - 1 && nch > 1;
   if (k >= nch && !combiner) return true;  // no chunk of this context
   if (combiner) {
     if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
@@ -893,6 +897,48 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
       sO[cc * GH + t] = o[0];
     }
     pd_bar();  // (m_c, z_c) of every head, every chunk's o_c
+  }
+  // the head group's Q8_K block (ties even) of sX on lanes 0..15, to its
+  // attention-output records
+  auto publish = [&]() {
+    if (t < 16) {
+      const int j = t;
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 x4 = *reinterpret_cast<const f32x4*>(sX + 16 * j + 4 * i);
+        v[4 * i] = x4.x;
+        v[4 * i + 1] = x4.y;
+        v[4 * i + 2] = x4.z;
+        v[4 * i + 3] = x4.w;
+      }
+      u32x4 packed;
+      float d;
+      int gsum;
+      quant_block_row16(v, false, packed, d, gsum);
+      const int vs = gsum + dpp_i<DPP_XOR1>(gsum);
+      const uint32_t w = (static_cast<uint32_t>(vs) & 0xffffu) | (static_cast<uint32_t>(dpp_i<DPP_XOR2>(vs)) << 16);
+      uint64_t* rb = a.ratt + static_cast<size_t>(h) * PD_REC_BLK;
+      rec_st(rb + 1 + 4 * j, packed.x, tag);
+      rec_st(rb + 2 + 4 * j, packed.y, tag);
+      rec_st(rb + 3 + 4 * j, packed.z, tag);
+      rec_st(rb + 4 + 4 * j, packed.w, tag);
+      rec_st(rb + 65 + j, static_cast<uint32_t>(gsum), tag);
+      if (j == 0) rec_stf(rb, d, tag);
+      if ((j & 3) == 0) rec_st(rb + 81 + (j >> 2), w, tag);
+    }
+  };
+  if (nch == 1) {
+    // the combining work group's arithmetic on one chunk: m = m_0,
+    // f = exp(m_0 - m), Z = fma(z_0, f, 0), O = fma(o_0, f, 0), out = O / Z
+    const float2 mz = A.sMZ[t / HD];
+    const float f = exp_f32(mz.x - mz.x);
+    sX[t] = __builtin_fmaf(sO[t], f, 0.0f) / __builtin_fmaf(mz.y, f, 0.0f);
+    pd_bar();
+    publish();
+    // the staging (read above) is overwritten by the next phase's copies
+    pd_bar();
+    return true;
   }
   const int ppc = s.part_stride;  // o_c (GH), m_c (group), z_c (group), in whole lines
   uint64_t* part = a.rpart + static_cast<size_t>(h) * a.s.max_chunks * ppc;
@@ -990,37 +1036,11 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
     }
   }
   sX[t] = O / Z;
-  if (pd_any(!ok, misc + 4, vit)) {
+  if (pd_any(!ok, misc + 4, vit)) {  // (its barrier also orders sX)
     if (t == 0) st_u32c(a.err, 1u);
     return false;
   }
-  // the head group's Q8_K block (ties even) on lanes 0..15
-  if (t < 16) {
-    const int j = t;
-    float v[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x4 x4 = *reinterpret_cast<const f32x4*>(sX + 16 * j + 4 * i);
-      v[4 * i] = x4.x;
-      v[4 * i + 1] = x4.y;
-      v[4 * i + 2] = x4.z;
-      v[4 * i + 3] = x4.w;
-    }
-    u32x4 packed;
-    float d;
-    int gsum;
-    quant_block_row16(v, false, packed, d, gsum);
-    const int vs = gsum + dpp_i<DPP_XOR1>(gsum);
-    const uint32_t w = (static_cast<uint32_t>(vs) & 0xffffu) | (static_cast<uint32_t>(dpp_i<DPP_XOR2>(vs)) << 16);
-    uint64_t* rb = a.ratt + static_cast<size_t>(h) * PD_REC_BLK;
-    rec_st(rb + 1 + 4 * j, packed.x, tag);
-    rec_st(rb + 2 + 4 * j, packed.y, tag);
-    rec_st(rb + 3 + 4 * j, packed.z, tag);
-    rec_st(rb + 4 + 4 * j, packed.w, tag);
-    rec_st(rb + 65 + j, static_cast<uint32_t>(gsum), tag);
-    if (j == 0) rec_stf(rb, d, tag);
-    if ((j & 3) == 0) rec_st(rb + 81 + (j >> 2), w, tag);
-  }
+  publish();
   return true;
 }
 
