@@ -652,9 +652,10 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
     pd_copy_region<FS>(a, LDS, l, 2);
     pd_copy_region<FS>(a, LDS, l, 3);
   }
-  // the combining work group with a chunk of its own (its staging is the
-  // down region until its chunks are done)
-  if (kind == 3 && me.k == s.W - 1 && me.k <= pos / ATTN_CHUNK) pd_copy_region<FS>(a, LDS, l, 3);
+  // the combining work group (its partials' wait at A is as long as the
+  // copies it takes there, and where it owns a chunk its staging is the
+  // down region until then)
+  if (kind == 3 && me.k == s.W - 1 && pos >= ATTN_CHUNK) pd_copy_region<FS>(a, LDS, l, 3);
 
   // hand-off and prologue: the Q8_K activations into the scratch
   if (kind == 0 || kind == 3) {
@@ -837,10 +838,9 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
   // chunk's own o_c / z_c), so no partials go to the combining work group
   const bool combiner = k == W - 1 && nch > 1;
   if (k >= nch && !combiner) return true;  // no chunk of this context
-  if (combiner) {
+  if (combiner) {  // (its down weights at G)
     if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
     pd_copy_region<FS>(a, LDS, l, 2);
-    if (k >= nch) pd_copy_region<FS>(a, LDS, l, 3);  // no chunk staged in the down region
   }
   constexpr int HD = 64, GH = 256, OPT = ATTN_MAX_GROUP * HD / 256;
   const int group = s.group, kvd = s.kvd;
