@@ -655,7 +655,10 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // the combining work group (its partials' wait at A is as long as the
   // copies it takes there, and where it owns a chunk its staging is the
   // down region until then)
-  if (kind == 3 && me.k == s.W - 1 && pos >= ATTN_CHUNK) pd_copy_region<FS>(a, LDS, l, 3);
+  if (kind == 3 && me.k == s.W - 1 && pos >= ATTN_CHUNK) {
+    if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
+    pd_copy_region<FS>(a, LDS, l, 3);
+  }
 
   // hand-off and prologue: the Q8_K activations into the scratch
   if (kind == 0 || kind == 3) {
@@ -838,10 +841,7 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
   // chunk's own o_c / z_c), so no partials go to the combining work group
   const bool combiner = k == W - 1 && nch > 1;
   if (k >= nch && !combiner) return true;  // no chunk of this context
-  if (combiner) {  // (its down weights at G)
-    if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
-    pd_copy_region<FS>(a, LDS, l, 2);
-  }
+  if (combiner) pd_copy_region<FS>(a, LDS, l, 2);  // (its next QKV and down weights at G)
   constexpr int HD = 64, GH = 256, OPT = ATTN_MAX_GROUP * HD / 256;
   const int group = s.group, kvd = s.kvd;
   const AttnLds<HD> A(reinterpret_cast<float*>(LDS + pd_stage_off(s, k)));
