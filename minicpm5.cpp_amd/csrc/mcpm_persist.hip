@@ -965,27 +965,30 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
   // Z = fma(z_c, f_c, Z); O = fma(o_c, f_c, O); out = O / Z.  Its own chunks
   // (W-1 and 2W-1, where they exist) come from LDS, the others from their
   // records: in one wait, every chunk's (m_c, z_c) (one (chunk, head) per
-  // thread, into LDS) and this thread's o_c of chunks 0..7; later chunks' o_c
-  // in batches of 8 as the chain reaches them.
+  // thread, into LDS) and this thread's o_c of the first 8 chunks; later
+  // chunks' o_c in batches of 8.  m and the f_c are formed once per head,
+  // on its wave (lane c: chunk c; the max is exact in any order), so each
+  // step of the chains is two fmas.
+  constexpr int B = 8;
   const int own0 = W - 1, own1 = 2 * W - 1;
   bool ok = true;
   const int hh = t / HD;
-  uint32_t rv[10];
+  uint32_t rv[2 + B];
   {
     const int cq = t / group, hq = t - cq * group;
     const bool mine = cq == own0 || cq == own1;
     const bool mz_rec = t < nch * group && !mine;
-    const uint64_t* p[10];
+    const uint64_t* p[2 + B];
     p[0] = part + static_cast<size_t>(min(cq, nch - 1)) * ppc + GH + hq;
     p[1] = p[0] + group;
     uint32_t mask = mz_rec ? 3u : 0u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < B; ++i) {
       const int c = i;
       p[2 + i] = part + static_cast<size_t>(min(c, nch - 1)) * ppc + t;
       if (c < nch && c != own0 && c != own1) mask |= 1u << (2 + i);
     }
-    ok = pd_wait_m<10>(p, mask, tag, a.spin_limit, rv);
+    ok = pd_wait_m<2 + B>(p, mask, tag, a.spin_limit, rv);
     if (t < nch * group) {
       float mc, zc;
       if (mine) {
@@ -1004,33 +1007,40 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
     if (t == 0) st_u32c(a.err, 1u);
     return false;
   }
-  float m = sM[hh];
-  for (int c = 1; c < nch; ++c) m = fmaxf(m, sM[c * group + hh]);
+  {
+    // head hh's f_c in place of its m_c (read and written by its own wave;
+    // nch <= 64)
+    const int c = t & 63;
+    const float mc = c < nch ? sM[c * group + hh] : -__builtin_inff();
+    const float m = wave_max_fast(mc);
+    if (c < nch) sM[c * group + hh] = exp_f32(mc - m);
+    wave_sync();
+  }
   float Z = 0.0f, O = 0.0f;
   auto step = [&](int c, float o) {
-    const float f = exp_f32(sM[c * group + hh] - m);
+    const float f = sM[c * group + hh];
     Z = __builtin_fmaf(sZ[c * group + hh], f, Z);
     O = __builtin_fmaf(o, f, O);
   };
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < B; ++i) {
     const int c = i;
     if (c < nch) step(c, c == own0 ? sO[t] : c == own1 ? sO[GH + t] : __uint_as_float(rv[2 + i]));
   }
 #pragma unroll 1
-  for (int c0 = 8; c0 < nch && ok; c0 += 8) {
-    const uint64_t* pb[8];
+  for (int c0 = B; c0 < nch && ok; c0 += B) {
+    const uint64_t* pb[B];
     uint32_t mask = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < B; ++i) {
       const int c = c0 + i;
       pb[i] = part + static_cast<size_t>(min(c, nch - 1)) * ppc + t;
       if (c < nch && c != own0 && c != own1) mask |= 1u << i;
     }
-    uint32_t ov[8];
-    ok = pd_wait_m<8>(pb, mask, tag, a.spin_limit, ov);
+    uint32_t ov[B];
+    ok = pd_wait_m<B>(pb, mask, tag, a.spin_limit, ov);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < B; ++i) {
       const int c = c0 + i;
       if (ok && c < nch) step(c, c == own0 ? sO[t] : c == own1 ? sO[GH + t] : __uint_as_float(ov[i]));
     }
