@@ -647,15 +647,18 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
     pd_stage_layer<FS>(a, l + 1, me.k, pos, LDS);
   // (with one chunk the combining work group has nothing to wait for at A,
   // where the chunk's owner finishes the head, and takes its copies here)
+  // The owner of the only chunk reaches O last, behind every other work
+  // group's copies: there it takes only its gate/up weights, the rest at G.
+  const bool solo = pos < ATTN_CHUNK && me.k == 0;
   if (kind == 2 && (me.k != s.W - 1 || pos < ATTN_CHUNK)) {
-    if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
+    if (l + 1 < a.s.L && !solo) pd_copy_region<FS>(a, LDS, l + 1, 0);
     pd_copy_region<FS>(a, LDS, l, 2);
-    pd_copy_region<FS>(a, LDS, l, 3);
+    if (!solo) pd_copy_region<FS>(a, LDS, l, 3);
   }
   // the combining work group (its partials' wait at A is as long as the
   // copies it takes there, and where it owns a chunk its staging is the
   // down region until then)
-  if (kind == 3 && me.k == s.W - 1 && pos >= ATTN_CHUNK) {
+  if (kind == 3 && ((me.k == s.W - 1 && pos >= ATTN_CHUNK) || solo)) {
     if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
     pd_copy_region<FS>(a, LDS, l, 3);
   }
