@@ -445,12 +445,19 @@ __device__ __forceinline__ void pd_tasks(const PdShape& s, const PdPhase& ph, co
     const int row = qq % R, bp = qq / R, blk = H == 2 ? bp >> 1 : bp;
     uint32_t* e = chain + (blk * ph.rtot + rbase + row) * 12;
     const float xd = __uint_as_float(S[s.s_xd + blk]);
-#pragma unroll 1
-    for (int p = H == 2 ? (bp & 1) : 0; p < (H == 2 ? (bp & 1) + 1 : 2); ++p) {
+    auto half = [&](int p) {
       if (ty == MCPM_TYPE_Q4_K)
         q4k_half(ph.w + off, RA, blk, row, p, S + s.s_xs + blk * 68, S + s.s_xbp + blk * 4, xd, e);
       else
         q6k_half(ph.w + off, RA, ph.nb, blk, row, p, S + s.s_xs + blk * 68, S + s.s_xbs + blk * 16, xd, e);
+    };
+    // both halves of a row-block in one straight run, so that the second's
+    // LDS reads can be issued while the first computes
+    if (H == 2) {
+      half(bp & 1);
+    } else {
+      half(0);
+      half(1);
     }
   }
 }
