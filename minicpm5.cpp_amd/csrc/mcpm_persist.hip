@@ -11,7 +11,8 @@
 //   A  attention of kv head h: chunk c of 64 positions on work group
 //      (h, c mod W); work group (h, W-1), which has no chunk below W chunks,
 //      combines the chunks' partials in chunk order and quantizes the head
-//      group's output ties-even (Q8_K blocks)
+//      group's output ties-even (Q8_K blocks); with one chunk its owner
+//      finishes the head itself
 //   O  O projection of this work group's rows of x, residual add
 //   G  RMSNorm + Q8_K (ties away); gate and up rows of its FFN pairs; SwiGLU
 //   D  Q8_K (ties away) of h; down projection of its rows of x; residual add
@@ -33,9 +34,11 @@
 // region is copied into LDS (direct-to-LDS loads, 1 KiB per wave
 // instruction) after its previous use, during the hand-off wait of a phase
 // before the one that reads it: O at Q; the next layer's QKV, this layer's
-// gate/up and down at O (at A on the work groups that combine attention
-// chunks, which wait there for the chunks' partials).  The wait ends with
-// every copy landed.  The chunk owners' K and V rows go into the gate/up
+// gate/up and down at O, where every other phase's wait is an all-to-all
+// wait but O's runs beside the attention (on the work groups that combine
+// attention chunks gate/up at A, while they wait for the chunks' partials,
+// the rest at G; on the owner of a single chunk, which reaches O last,
+// gate/up at O and the rest at G).  The wait ends with every copy landed.  The chunk owners' K and V rows go into the gate/up
 // region at the previous layer's D (where that region holds them; the
 // combining work group's into the down region at Q), the attention's
 // staging.
