@@ -665,9 +665,9 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
     pd_copy_region<FS>(a, LDS, l, 2);
     if (!solo) pd_copy_region<FS>(a, LDS, l, 3);
   }
-  // the combining work group (its partials' wait at A is as long as the
-  // copies it takes there, and where it owns a chunk its staging is the
-  // down region until then)
+  // the combining work group's next QKV and down copies (at A they would
+  // lengthen its wait for the partials; where it owns a chunk its staging is
+  // the down region until then), and those of the single chunk's owner
   if (kind == 3 && ((me.k == s.W - 1 && pos >= ATTN_CHUNK) || solo)) {
     if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
     pd_copy_region<FS>(a, LDS, l, 3);
@@ -839,9 +839,10 @@ __device__ __forceinline__ void pd_fill_last(AttnRegs<4>& R, const float* kr, co
 // head_dim 64, a head group of 256 outputs (gh).  Chunk c of 64 positions on
 // work group (h, c mod W); work group (h, W-1) combines the head's chunks.
 // Below W chunks the combining work group has no chunk of its own and would
-// wait idle for the partials, so it takes its weight copies for the next
-// phases here (the next layer's QKV, this layer's gate/up), and every other
-// work group its own at O.
+// wait idle for the partials, so it takes its gate/up copy here (its next
+// QKV and down copies at G: at A they would end its wait later than the
+// partials, competing with every other work group's copies at O).  With
+// one chunk the chunk's owner finishes the head and no work group combines.
 template <bool XL, bool FS>
 __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LDS, uint32_t* S, uint32_t tag, int T,
                                              uint32_t& vit) {
