@@ -104,12 +104,28 @@ struct PdRows {
   int qr0, kr0; // first q row, first k (and v) row
 };
 
+// FFN pairs of each of the 8 work groups b < 8 (index 0 in their XCDs, the
+// owners of the first attention chunk): the fewest that leave every other
+// work group at most np_max.  The owner of a context's only chunk finishes
+// its head's attention and reaches O last; fewer gate/up rows leave it fewer
+// weights to copy and less work before G's hand-off.
+__host__ __device__ constexpr int pd_owner_pairs(const PdShape& s) {
+  const int spare = s.ffn - s.np_max * (s.G - PD_XCDS);
+  return spare <= 0 ? 0 : (spare + PD_XCDS - 1) / PD_XCDS;
+}
+
 __host__ __device__ inline PdRows pd_rows(const PdShape& s, int b) {
   PdRows r;
   r.hr0 = static_cast<int>((static_cast<int64_t>(b) * s.dim) / s.G);
   r.nh = static_cast<int>((static_cast<int64_t>(b + 1) * s.dim) / s.G) - r.hr0;
-  r.fp0 = static_cast<int>((static_cast<int64_t>(b) * s.ffn) / s.G);
-  r.np = static_cast<int>((static_cast<int64_t>(b + 1) * s.ffn) / s.G) - r.fp0;
+  const int p0 = pd_owner_pairs(s), rest = s.ffn - PD_XCDS * p0, g = s.G - PD_XCDS;
+  if (b < PD_XCDS) {
+    r.fp0 = b * p0;
+    r.np = p0;
+  } else {
+    r.fp0 = PD_XCDS * p0 + static_cast<int>((static_cast<int64_t>(b - PD_XCDS) * rest) / g);
+    r.np = PD_XCDS * p0 + static_cast<int>((static_cast<int64_t>(b + 1 - PD_XCDS) * rest) / g) - r.fp0;
+  }
   r.kvh = b % PD_XCDS;
   r.k = b / PD_XCDS;
   r.qr0 = r.kvh * s.gh + r.k * s.nq;

@@ -11,6 +11,7 @@
 //    records exactly once, every record array starts on a cache line, and
 //    the blocks stored at workgroup scope fill whole lines;
 //  - shapes the kernel does not take are refused;
+//  - the first-chunk owners' lighter FFN share (pd_owner_pairs);
 //  - the plan the fixed-shape instance compiles in (pd_fixed_plan, evaluated
 //    at compile time) equals the plan made at run time for that shape, and
 //    pd_fixed_shape picks that instance for it at any layer count and KV
@@ -242,7 +243,13 @@ static void check_fixed_shape() {
   mcpm_model_config e = cfg(40, 2304, 32, 8, 64, 5760);
   e.eps = 1e-5f;
   CHECK(!pd_fixed_shape(plan_of(e, 256, 512, Q6, Q4, Q6)), "eps 1e-5 taken as the fixed shape");
-  std::printf("fixed-shape instance: plan %d B of LDS, taken for the 2.4B shape only\n", f.lds_bytes);
+  // the first-chunk owners' FFN pairs: the 56 the other 248 work groups
+  // leave at 23 each, 7 per owner
+  CHECK(pd_owner_pairs(f) == 7 && pd_rows(f, 0).np == 7 && pd_rows(f, 7).fp0 == 49 && pd_rows(f, 8).fp0 == 56 &&
+            pd_rows(f, 8).np == 23 && pd_rows(f, 255).fp0 + pd_rows(f, 255).np == 5760,
+        "owner FFN pairs of the fixed plan");
+  std::printf("fixed-shape instance: plan %d B of LDS, taken for the 2.4B shape only; owners take %d FFN pairs\n",
+              f.lds_bytes, pd_owner_pairs(f));
 }
 
 int main() {
