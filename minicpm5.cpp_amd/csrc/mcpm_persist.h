@@ -133,6 +133,24 @@ __host__ __device__ inline PdRows pd_rows(const PdShape& s, int b) {
   return r;
 }
 
+// The gate and up sub-regions of work group b and the bytes of its gate/up
+// region they fill: the plan's (np_max rows each, reg_sz[2]) or, on the
+// first-chunk owners, rows for their own pairs only, so that their copy of
+// the region is shorter.
+struct PdGu {
+  PdSub g, u;
+  int bytes;
+};
+
+__host__ __device__ inline PdGu pd_gu(const PdShape& s, int b) {
+  const int p0 = pd_owner_pairs(s);
+  if (b < PD_XCDS && p0 < s.np_max) {
+    const int gb = pd_sub_bytes(MCPM_TYPE_Q4_K, p0, s.nbx);
+    return PdGu{PdSub{0, p0, MCPM_TYPE_Q4_K}, PdSub{gb, p0, MCPM_TYPE_Q4_K}, (2 * gb + 1023) / 1024 * 1024};
+  }
+  return PdGu{s.sg, s.su, s.reg_sz[2]};
+}
+
 // Where slab byte `off` (a multiple of 16) of work group b's layer slab comes
 // from: tensor (0..6: q, k, v, o, gate, up, down; -1: padding, zeros) and
 // either one 16-byte chunk of plane `plane` at byte src[0] (n = 1) or, for
@@ -163,7 +181,8 @@ __host__ __device__ inline PdSrc pd_slab_src(const PdShape& s, int b, int off, c
     nsub = 1;
     nb = s.nbq;
   } else if (r == 2) {
-    sb[0] = s.sg; sb[1] = s.su;
+    const PdGu gu = pd_gu(s, b);
+    sb[0] = gu.g; sb[1] = gu.u;
     tens[0] = 4; tens[1] = 5;
     valid[0] = me.np; valid[1] = me.np;
     row0[0] = me.fp0; row0[1] = me.fp0;

@@ -548,7 +548,7 @@ __device__ __forceinline__ const uint8_t* pd_slab(const PdArgs& a, int l, int r)
 template <bool FS>
 __device__ __forceinline__ void pd_copy_region(const PdArgs& a, uint8_t* LDS, int l, int r) {
   const PdShape& s = pd_s<FS>(a);
-  pd_copy(pd_slab<FS>(a, l, r), LDS + s.reg_off[r], s.reg_sz[r]);
+  pd_copy(pd_slab<FS>(a, l, r), LDS + s.reg_off[r], r == 2 ? pd_gu(s, static_cast<int>(blockIdx.x)).bytes : s.reg_sz[r]);
 }
 
 // Whether chunk owner k (k < the chunk count) stages its layer's chunk
@@ -595,7 +595,8 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   } else if (kind == 2) {
     ph = pd_phase(LDS + s.reg_off[1], s.so, s.so, s.so, me.nh, 0, 0, 1, s.nbq, me.nh);
   } else if (kind == 3) {
-    ph = pd_phase(LDS + s.reg_off[2], s.sg, s.su, s.su, me.np, me.np, 0, 2, s.nbx, 2 * me.np);
+    const PdGu gu = pd_gu(s, static_cast<int>(blockIdx.x));
+    ph = pd_phase(LDS + s.reg_off[2], gu.g, gu.u, gu.u, me.np, me.np, 0, 2, s.nbx, 2 * me.np);
   } else {
     ph = pd_phase(LDS + s.reg_off[3], s.sd, s.sd, s.sd, me.nh, 0, 0, 1, s.nbh, me.nh);
   }

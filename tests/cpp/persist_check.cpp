@@ -153,13 +153,16 @@ static void check_shape(const char* name, const mcpm_model_config& c, int n_cu, 
   // every byte a task reads maps back to the expected (row, block, chunk)
   for (int b = 0; b < s.G; ++b) {
     const PdRows me = pd_rows(s, b);
+    const PdGu gu = pd_gu(s, b);
+    CHECK(gu.bytes <= s.reg_sz[2] && gu.u.off + pd_sub_bytes(gu.u.type, gu.u.R, s.nbx) <= gu.bytes,
+          "%s: WG %d gate/up copy", name, b);
     struct Sub {
       int region, tensor, valid, row0, nb;
       PdSub sb;
     };
     const Sub subs[7] = {{0, 0, s.nq, me.qr0, s.nbx, s.sq},  {0, 1, s.nk, me.kr0, s.nbx, s.sk},
                          {0, 2, s.nk, me.kr0, s.nbx, s.sv},  {1, 3, me.nh, me.hr0, s.nbq, s.so},
-                         {2, 4, me.np, me.fp0, s.nbx, s.sg}, {2, 5, me.np, me.fp0, s.nbx, s.su},
+                         {2, 4, me.np, me.fp0, s.nbx, gu.g}, {2, 5, me.np, me.fp0, s.nbx, gu.u},
                          {3, 6, me.nh, me.hr0, s.nbh, s.sd}};
     for (const Sub& q : subs) {
       const int R = q.sb.R, nc = q.sb.type == MCPM_TYPE_Q4_K ? 9 : 13;
