@@ -562,8 +562,18 @@ __device__ __forceinline__ bool pd_stage_early(const PdShape& s, int k) {
 
 // The attention staging of chunk k's owner: the gate/up region when it
 // stages early, else the down region.
-__device__ __forceinline__ int pd_stage_off(const PdShape& s, int k) {
-  return pd_stage_early(s, k) ? s.reg_off[2] : s.reg_off[3];
+// Whether the owner of a context's only chunk (k = 0, a first-chunk owner
+// with its short gate/up rows) stages at G instead of D, past its gate/up
+// rows in that region: its G, with few rows, ends before the others', while
+// a copy at D made its D end after theirs.
+__device__ __forceinline__ bool pd_solo_stage_g(const PdShape& s, int k, int nch) {
+  return nch == 1 && k == 0 && pd_stage_early(s, k) && pd_gu(s, 0).bytes + PD_ATTN_LDS <= s.reg_sz[2];
+}
+
+__device__ __forceinline__ int pd_stage_off(const PdShape& s, int k, int nch) {
+  return pd_solo_stage_g(s, k, nch) ? s.reg_off[2] + pd_gu(s, 0).bytes
+         : pd_stage_early(s, k)     ? s.reg_off[2]
+                                    : s.reg_off[3];
 }
 
 // Chunk k of layer l's K and V rows of this work group's kv head (context
@@ -574,7 +584,7 @@ __device__ __forceinline__ void pd_stage_layer(const PdArgs& a, int l, int k, in
   const size_t lay = static_cast<size_t>(l) * a.max_seq * s.kvd;
   pd_stage_chunk(a.kc + lay, a.vc + lay, k, pos + 1, s.kvd,
                  static_cast<size_t>(static_cast<int>(blockIdx.x) % PD_XCDS) * s.hd, a.norms,
-                 LDS + pd_stage_off(s, k));
+                 LDS + pd_stage_off(s, k, (pos + ATTN_CHUNK) / ATTN_CHUNK));
 }
 
 // Q (kind 0), O (2), G (3) or D (4) of layer l.
@@ -654,7 +664,8 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // the next layer's attention chunk, into the gate/up region (free from the
   // end of G until this work group's next gate/up copy at O, after A), so
   // that the copy lands during this phase's wait instead of the next Q's
-  if (kind == 4 && l + 1 < a.s.L && me.k < (pos + ATTN_CHUNK) / ATTN_CHUNK && pd_stage_early(s, me.k))
+  if (kind == 4 && l + 1 < a.s.L && me.k < (pos + ATTN_CHUNK) / ATTN_CHUNK && pd_stage_early(s, me.k) &&
+      !pd_solo_stage_g(s, me.k, (pos + ATTN_CHUNK) / ATTN_CHUNK))
     pd_stage_layer<FS>(a, l + 1, me.k, pos, LDS);
   // (with one chunk the combining work group has nothing to wait for at A,
   // where the chunk's owner finishes the head, and takes its copies here)
@@ -673,6 +684,8 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
     if (l + 1 < a.s.L) pd_copy_region<FS>(a, LDS, l + 1, 0);
     pd_copy_region<FS>(a, LDS, l, 3);
   }
+  if (kind == 3 && l + 1 < a.s.L && pd_solo_stage_g(s, me.k, (pos + ATTN_CHUNK) / ATTN_CHUNK))
+    pd_stage_layer<FS>(a, l + 1, me.k, pos, LDS);
 
   // hand-off and prologue: the Q8_K activations into the scratch
   if (kind == 0 || kind == 3) {
@@ -859,7 +872,7 @@ __device__ __forceinline__ bool pd_attention(const PdArgs& a, int l, uint8_t* LD
   if (combiner) pd_copy_region<FS>(a, LDS, l, 2);  // (its next QKV and down weights at G)
   constexpr int HD = 64, GH = 256, OPT = ATTN_MAX_GROUP * HD / 256;
   const int group = s.group, kvd = s.kvd;
-  const AttnLds<HD> A(reinterpret_cast<float*>(LDS + pd_stage_off(s, k)));
+  const AttnLds<HD> A(reinterpret_cast<float*>(LDS + pd_stage_off(s, k, nch)));
   float* kr = reinterpret_cast<float*>(S + s.s_u);
   float* vr = kr + HD;
   float* sX = vr + HD;       // [GH] the combined output
