@@ -649,12 +649,16 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // weight copies for later phases, issued while this phase waits for its
   // hand-off (the waves are idle then, and a copy stalls the wave issuing it
   // for most of its transfer): each region after its last use, before the
-  // wait of a phase ahead of its next.  Q: this layer's O (and the chunk
-  // owners' attention rows, into the down region); O: the next layer's QKV,
-  // this layer's gate/up and down (the attention's staging is done), except
-  // on the kv heads' combining work groups (k = W-1), which take them at A,
-  // while they wait for the chunks' partials (down at G where they own a
-  // chunk, whose staging holds the down region until then).
+  // wait of a phase ahead of its next.  Q: this layer's O (and, where the
+  // down region is the attention's staging, the chunk's rows); O: the next
+  // layer's QKV, this layer's gate/up and down (the attention's staging is
+  // done), where every other phase's wait is an all-to-all wait but O's runs
+  // beside the attention.  The kv heads' combining work groups (k = W-1)
+  // take gate/up at A, while they wait for the chunks' partials, and the
+  // rest at G; the owner of a context's only chunk, which reaches O last,
+  // takes gate/up (its own rows only) at O and the rest, with its next
+  // chunk's staging, at G, where its few FFN rows leave it time.  D: the
+  // other chunk owners' next attention rows, into the gate/up region.
   if (kind == 0) {
     pd_copy_region<FS>(a, LDS, l, 1);
     // this layer's attention chunk (the down region is free until G), where
@@ -669,8 +673,6 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
     pd_stage_layer<FS>(a, l + 1, me.k, pos, LDS);
   // (with one chunk the combining work group has nothing to wait for at A,
   // where the chunk's owner finishes the head, and takes its copies here)
-  // The owner of the only chunk reaches O last, behind every other work
-  // group's copies: there it takes only its gate/up weights, the rest at G.
   const bool solo = pos < ATTN_CHUNK && me.k == 0;
   if (kind == 2 && (me.k != s.W - 1 || pos < ATTN_CHUNK)) {
     if (l + 1 < a.s.L && !solo) pd_copy_region<FS>(a, LDS, l + 1, 0);
