@@ -674,11 +674,14 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
   // (with one chunk the combining work group has nothing to wait for at A,
   // where the chunk's owner finishes the head, and takes its copies here)
   const bool solo = pos < ATTN_CHUNK && me.k == 0;
+  // (with one chunk, the plain work groups' next QKV at D: O's wait ends
+  // with its copies, the attention being short)
   if (kind == 2 && (me.k != s.W - 1 || pos < ATTN_CHUNK)) {
-    if (l + 1 < a.s.L && !solo) pd_copy_region<FS>(a, LDS, l + 1, 0);
+    if (l + 1 < a.s.L && !solo && pos >= ATTN_CHUNK) pd_copy_region<FS>(a, LDS, l + 1, 0);
     pd_copy_region<FS>(a, LDS, l, 2);
     if (!solo) pd_copy_region<FS>(a, LDS, l, 3);
   }
+  if (kind == 4 && l + 1 < a.s.L && pos < ATTN_CHUNK && !solo) pd_copy_region<FS>(a, LDS, l + 1, 0);
   // the combining work group's next QKV and down copies (at A they would
   // lengthen its wait for the partials; where it owns a chunk its staging is
   // the down region until then), and those of the single chunk's owner
