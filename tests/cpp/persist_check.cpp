@@ -267,6 +267,12 @@ int main() {
               MCPM_TYPE_Q6_K);
   check_shape("small 8-kv Q6_K o", cfg(2, 768, 32, 8, 64, 2000), 256, 512, MCPM_TYPE_Q4_K, MCPM_TYPE_Q6_K,
               MCPM_TYPE_Q4_K);
+  // FFN sizes whose spare pairs give the first-chunk owners fewer rows than
+  // the plan's (7 of 11, and none at all), in the gate/up layout of their own
+  check_shape("small 8-kv ffn 2780", cfg(2, 1024, 32, 8, 64, 2780), 256, 512, MCPM_TYPE_Q6_K, MCPM_TYPE_Q4_K,
+              MCPM_TYPE_Q6_K);
+  check_shape("small 8-kv ffn 2600", cfg(2, 1024, 32, 8, 64, 2600), 256, 512, MCPM_TYPE_Q6_K, MCPM_TYPE_Q4_K,
+              MCPM_TYPE_Q6_K);
   check_refused("2 kv heads", cfg(2, 512, 8, 2, 64, 1400), 256, 32);
   check_refused("head_dim 128", cfg(2, 2048, 16, 8, 128, 6144), 256, 64);
   check_refused("context past 2 chunks per work group", big, 256, 4160);

@@ -108,6 +108,41 @@ def test_agent_scope_hand_offs_match(ctx, kv8_image, engines, monkeypatch):
     np.testing.assert_array_equal(got[1], want[1])
 
 
+@pytest.mark.parametrize("ffn", [2780, 2600])
+def test_first_chunk_owners_light_ffn_share(ctx, ffn):
+    """FFN sizes whose spare pairs leave the eight first-chunk owners fewer
+    gate/up rows than the plan's 11 (7 at 2780; none at 2600) in a gate/up
+    layout of their own: the generic instance against the oracle and the
+    five launches."""
+    cfg = dict(KV8, n_layers=2, ffn=ffn, vocab=2048)
+    img = mcpm.synth_gguf(mcpm.make_config(**cfg), seed=ffn, mix=0)
+    a = mcpm.Engine(ctx, image=img)
+    b = mcpm.Engine(ctx, image=img)
+    try:
+        a.set_persistent(True)
+        b.set_persistent(False)
+        a.init_kv_cache(256)
+        b.init_kv_cache(256)
+        assert a.uses_persistent() and not a.persistent_fixed_shape() and not b.uses_persistent()
+        om = O.OracleModel(img)
+        om.init_kv(256)
+        rng = np.random.default_rng(ffn)
+        want = np.empty(cfg["vocab"], np.float32)
+        for pos, t in enumerate(rng.integers(0, cfg["vocab"], 24)):
+            announce(f"light FFN share ffn={ffn} pos={pos}")
+            got, _ = a.forward(int(t), pos)
+            om.forward(int(t), pos, want)
+            assert_bits(got, want)
+        prompt = rng.integers(0, cfg["vocab"], 40).astype(np.int32)
+        announce(f"light FFN share ffn={ffn}: greedy and sampled vs five launches")
+        np.testing.assert_array_equal(a.generate_greedy(prompt, 48), b.generate_greedy(prompt, 48))
+        np.testing.assert_array_equal(a.generate_sampled(prompt, 48, 0.9, 0.95, 7),
+                                      b.generate_sampled(prompt, 48, 0.9, 0.95, 7))
+    finally:
+        a.free()
+        b.free()
+
+
 def test_long_context_two_chunks_per_work_group(engines):
     """Positions past 32 chunks of 64 per kv head (the work groups of one
     XCD): the first work groups take two chunks each, and the combiner reads
