@@ -721,8 +721,9 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
     // h in rounds of up to 16 blocks: records t + 256k of the round (lanes
     // on consecutive records) into the staging area, then block r16 of the
     // round quantized by its row of 16 lanes (zero past ffn).  Up to 24
-    // blocks every record is waited for at once (two rounds from registers),
-    // so the second round costs no second round trip.
+    // blocks every record is waited for at once, so the second round costs
+    // no second round trip, and where the O weights' region holds the blocks
+    // past the 16th the two rounds are one.
     const int nbh = s.nbh, ffn = s.ffn;
     float* U = reinterpret_cast<float*>(S + s.s_u);
     auto quant_round = [&](int b0, int nbr) {
@@ -754,14 +755,57 @@ __device__ __forceinline__ bool pd_gemv(const PdArgs& a, int l, int kind, uint8_
                        },
                        hv, misc, vit))
         return false;
+      if (nbh > 16 && (nbh - 16) * QK_K * 4 <= s.reg_sz[1]) {
+        // one round: blocks 16.. staged in the O weights' region (read at O,
+        // next written by the next layer's Q copy), the rows of waves 0 and 1
+        // quantizing two blocks each in one straight run
+        float* U2 = reinterpret_cast<float*>(LDS + s.reg_off[1]);
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        const int b0 = 16 * rr, nbr = min(16, nbh - b0);
-        if (nbr > 0) {  // uniform
+        for (int k = 0; k < 16; ++k) U[t + 256 * k] = __uint_as_float(hv[k]);
 #pragma unroll
-          for (int k = 0; k < 16; ++k)
-            if (k < nbr) U[t + 256 * k] = __uint_as_float(hv[b0 + k < 24 ? b0 + k : 0]);
-          quant_round(b0, nbr);
+        for (int k = 0; k < 8; ++k)
+          if (k < nbh - 16) U2[t + 256 * k] = __uint_as_float(hv[16 + k]);
+        pd_bar();
+        auto ld16 = [&](const float* src, float (&v)[16]) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 x4 = *reinterpret_cast<const f32x4*>(src + 16 * j + 4 * i);
+            v[4 * i] = x4.x;
+            v[4 * i + 1] = x4.y;
+            v[4 * i + 2] = x4.z;
+            v[4 * i + 3] = x4.w;
+          }
+        };
+        float v0[16];
+        ld16(U + r16 * 256, v0);
+        u32x4 p0;
+        float d0;
+        int g0;
+        if (r16 < 8) {  // waves 0 and 1; rows past the last block quantize a copy of it and store nothing
+          float v1[16];
+          ld16(U2 + min(r16, nbh - 17) * 256, v1);
+          u32x4 p1;
+          float d1;
+          int g1;
+          quant_block_row16(v0, true, p0, d0, g0);
+          quant_block_row16(v1, true, p1, d1, g1);
+          pd_store_xblock(S, s, r16, j, p0, d0, g0);
+          if (r16 < nbh - 16) pd_store_xblock(S, s, 16 + r16, j, p1, d1, g1);
+        } else {
+          quant_block_row16(v0, true, p0, d0, g0);
+          pd_store_xblock(S, s, r16, j, p0, d0, g0);
+        }
+        pd_bar();
+      } else {
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const int b0 = 16 * rr, nbr = min(16, nbh - b0);
+          if (nbr > 0) {  // uniform
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+              if (k < nbr) U[t + 256 * k] = __uint_as_float(hv[b0 + k < 24 ? b0 + k : 0]);
+            quant_round(b0, nbr);
+          }
         }
       }
     } else {
