@@ -273,6 +273,13 @@ int main() {
               MCPM_TYPE_Q6_K);
   check_shape("small 8-kv ffn 2600", cfg(2, 1024, 32, 8, 64, 2600), 256, 512, MCPM_TYPE_Q6_K, MCPM_TYPE_Q4_K,
               MCPM_TYPE_Q6_K);
+  // FFN sizes past 16 Q8_K blocks: 20 blocks, whose 4 past the 16th fit the
+  // 5 KiB of O weights a work group holds (one quantize round), and 23
+  // blocks, whose 7 do not (two rounds)
+  check_shape("small 8-kv ffn 5120", cfg(2, 1024, 32, 8, 64, 5120), 256, 512, MCPM_TYPE_Q6_K, MCPM_TYPE_Q4_K,
+              MCPM_TYPE_Q6_K);
+  check_shape("small 8-kv ffn 5888", cfg(2, 1024, 32, 8, 64, 5888), 256, 512, MCPM_TYPE_Q6_K, MCPM_TYPE_Q4_K,
+              MCPM_TYPE_Q6_K);
   check_refused("2 kv heads", cfg(2, 512, 8, 2, 64, 1400), 256, 32);
   check_refused("head_dim 128", cfg(2, 2048, 16, 8, 128, 6144), 256, 64);
   check_refused("context past 2 chunks per work group", big, 256, 4160);

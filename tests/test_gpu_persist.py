@@ -114,6 +114,20 @@ def test_first_chunk_owners_light_ffn_share(ctx, ffn):
     gate/up rows than the plan's 11 (7 at 2780; none at 2600) in a gate/up
     layout of their own: the generic instance against the oracle and the
     five launches."""
+    generic_vs_oracle(ctx, ffn, "light FFN share")
+
+
+@pytest.mark.parametrize("ffn", [5120, 5888])
+def test_ffn_activation_quantize_rounds(ctx, ffn):
+    """The down phase's Q8_K blocks of the FFN activations past the 16th:
+    staged in the O weights' region and quantized in the same round where
+    that region holds them (20 blocks at 5120 against 5 KiB of O weights per
+    work group), in a second round where it does not (23 blocks at 5888):
+    the generic instance against the oracle and the five launches."""
+    generic_vs_oracle(ctx, ffn, "h quantize rounds")
+
+
+def generic_vs_oracle(ctx, ffn, label):
     cfg = dict(KV8, n_layers=2, ffn=ffn, vocab=2048)
     img = mcpm.synth_gguf(mcpm.make_config(**cfg), seed=ffn, mix=0)
     a = mcpm.Engine(ctx, image=img)
@@ -129,12 +143,12 @@ def test_first_chunk_owners_light_ffn_share(ctx, ffn):
         rng = np.random.default_rng(ffn)
         want = np.empty(cfg["vocab"], np.float32)
         for pos, t in enumerate(rng.integers(0, cfg["vocab"], 24)):
-            announce(f"light FFN share ffn={ffn} pos={pos}")
+            announce(f"{label} ffn={ffn} pos={pos}")
             got, _ = a.forward(int(t), pos)
             om.forward(int(t), pos, want)
             assert_bits(got, want)
         prompt = rng.integers(0, cfg["vocab"], 40).astype(np.int32)
-        announce(f"light FFN share ffn={ffn}: greedy and sampled vs five launches")
+        announce(f"{label} ffn={ffn}: greedy and sampled vs five launches")
         np.testing.assert_array_equal(a.generate_greedy(prompt, 48), b.generate_greedy(prompt, 48))
         np.testing.assert_array_equal(a.generate_sampled(prompt, 48, 0.9, 0.95, 7),
                                       b.generate_sampled(prompt, 48, 0.9, 0.95, 7))
